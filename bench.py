@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark of the BFP decode datapath on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: the standalone BFP matvec sweep at
+batch 1 -- shapes 576x576, 192x576, 1536x576, 576x1536, 49152x576, 1000
+reps each.  One "step" is the whole sweep: one launch per shape computing
+1000 independent y = W x, each rep reading a distinct weight copy from a
+ring of >= 512 MiB so that the bytes come from HBM, not from the 256 MiB
+MALL.  Weights are N(0, 0.02) float32 quantised to BFP on the device,
+inputs N(0, 1) quantised to BFP; everything is resident in HBM before the
+timed region.  `value` is algorithmic bytes / second over the K timed steps
+(out*in*2 + out*in/16 weight bytes + x and y BFP bytes per rep).
+
+The JSON line also carries the roofline of the dominant matvec kernel
+(HIP events on the launch stream), the parity check of sampled reps
+against the CPU oracle, and the CPU baseline (the oracle timed on a bounded
+sample on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "tinyllm-fpga_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+SHAPES = [(576, 576), (192, 576), (1536, 576), (576, 1536), (49152, 576)]
+RING_BYTES = 512 << 20
+
+
+def alg_bytes(n_out, n_in):
+    return n_out * n_in * 2 + n_out * n_in // 16 + n_in * 2 + n_in // 16 + n_out * 2 + n_out // 16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--reps", type=int, default=1000)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+class ShapeCase:
+    """Device-resident ring of BFP weight copies + inputs for one shape."""
+
+    def __init__(self, n_out, n_in, reps, seed):
+        import torch
+        from bfp import _dev
+        from bfp._lib import call
+        self.n_out, self.n_in, self.reps = n_out, n_in, reps
+        self.bm = n_out * n_in * 2
+        self.be = n_out * n_in // 16
+        self.ring = min(reps, max(2, -(-RING_BYTES // (self.bm + self.be))))
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.Pm = torch.empty(self.ring * self.bm, dtype=torch.uint8, device="cuda")
+        self.Pe = torch.empty(self.ring * self.be, dtype=torch.uint8, device="cuda")
+        # generate and pack in slabs to bound the fp32 staging memory
+        per = max(1, (256 << 20) // (n_out * n_in * 4))
+        self.W0 = None
+        for r0 in range(0, self.ring, per):
+            k = min(per, self.ring - r0)
+            W = torch.randn((k * n_out, n_in), generator=g, device="cuda", dtype=torch.float32)
+            W.mul_(0.02)
+            if r0 == 0:
+                self.W0 = W[:n_out].cpu().numpy()
+            call("bfp_quantize_pack_f32_d", W.data_ptr(), k * n_out, n_in,
+                 self.Pm.data_ptr() + r0 * self.bm, self.Pe.data_ptr() + r0 * self.be,
+                 _dev.stream())
+            del W
+        X = torch.randn((reps, n_in), generator=g, device="cuda", dtype=torch.float32)
+        self.X_last = X[reps - 1].cpu().numpy()
+        self.X0 = X[0].cpu().numpy()
+        self.xm = torch.empty(reps * n_in, dtype=torch.int16, device="cuda")
+        self.xe = torch.empty(reps * n_in // 16, dtype=torch.int8, device="cuda")
+        call("bfp_tile_quantize_f32_d", X.data_ptr(), reps * n_in, self.xm.data_ptr(),
+             self.xe.data_ptr(), _dev.stream())
+        del X
+        self.ym = torch.empty(reps * n_out, dtype=torch.int16, device="cuda")
+        self.ye = torch.empty(reps * n_out // 16, dtype=torch.int8, device="cuda")
+        self.waves = 0
+        torch.cuda.synchronize()
+
+    def launch(self):
+        from bfp import _dev
+        from bfp._lib import call
+        call("bfp_matvec_ring_d", self.Pm.data_ptr(), self.Pe.data_ptr(), self.n_out, self.n_in,
+             self.reps, self.ring, self.bm, self.be, self.xm.data_ptr(), self.xe.data_ptr(),
+             self.n_in, self.ym.data_ptr(), self.ye.data_ptr(), self.n_out, self.waves,
+             _dev.stream())
+
+    def bytes_per_launch(self):
+        return alg_bytes(self.n_out, self.n_in) * self.reps
+
+    def check(self):
+        """Reps 0 and reps-1 against the CPU oracle, bit for bit."""
+        import numpy as np
+        from oracle import bfp_sim as sim
+        ym = self.ym.cpu().numpy().reshape(self.reps, -1)
+        ye = self.ye.cpu().numpy().reshape(self.reps, -1)
+        Wm, We = sim.tile_quantize(self.W0.astype(np.float64))
+        nt = self.n_in // 16
+        Wm, We = Wm.reshape(self.n_out, nt, 16), We.reshape(self.n_out, nt)
+        ok = True
+        for r, x in ((0, self.X0), (self.reps - 1, self.X_last)):
+            if r % self.ring != 0:
+                continue                      # only ring slot 0 is mirrored on the host
+            xm, xe = sim.tile_quantize(x.astype(np.float64))
+            wm, we = sim.tile_quantize(sim.matvec_hw_golden(xm, xe, Wm, We))
+            ok &= bool((ym[r] == wm.reshape(-1)).all() and (ye[r] == we).all())
+        return ok
+
+
+def kernel_config(n_in):
+    """(waves, tiles per lane) the library picks for this input width."""
+    nT = n_in // 16
+    nw = next(a for a in (1, 2, 3, 4, 6, 8, 9) if a >= (nT + 11) // 12) if nT <= 108 else 9
+    tpt = -(-nT // (4 * nw))
+    return nw, tpt
+
+
+def cpu_baseline(seconds):
+    """The oracle's numpy matvec_hw_golden (restating full.py:217-233),
+    single-threaded, on a bounded sample of the same sweep."""
+    import numpy as np
+    from oracle import bfp_sim as sim
+    from bfp import synth
+    os.environ.setdefault("OPENBLAS_NUM_THREADS", "1")
+    total_b, total_t, done = 0, 0.0, []
+    per_shape = seconds / len(SHAPES)
+    for n_out, n_in in SHAPES:
+        W, x = synth.make_matvec_case(n_out, n_in, seed=5)
+        Wm, We = sim.tile_quantize(W[0].astype(np.float64))
+        nt = n_in // 16
+        Wm, We = Wm.reshape(n_out, nt, 16), We.reshape(n_out, nt)
+        xm, xe = sim.tile_quantize(x[0])
+        n, t0 = 0, time.perf_counter()
+        while True:
+            sim.matvec_hw_golden(xm, xe, Wm, We)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= per_shape or n >= 1000:
+                break
+        total_b += alg_bytes(n_out, n_in) * n
+        total_t += dt
+        done.append(f"{n_out}x{n_in}:{n}")
+    return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": "oracle/bfp_sim.matvec_hw_golden (numpy, 1 thread), reps per shape "
+                      + ", ".join(done) + f" in {total_t:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: only --gpus 1 is supported on this build (asked for {args.gpus}); "
+              "the BFP datapath is measured on one GPU", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP GPU visible", file=sys.stderr)
+        sys.exit(1)
+    from bfp import _lib
+    _lib.lib()
+    print(f"[bench] building device rings for {len(SHAPES)} shapes x {args.reps} reps",
+          file=sys.stderr, flush=True)
+    cases = [ShapeCase(o, i, args.reps, seed=17 + k) for k, (o, i) in enumerate(SHAPES)]
+    for _ in range(args.warmup):
+        for c in cases:
+            c.launch()
+    torch.cuda.synchronize()
+    parity = all(c.check() for c in cases)
+    print(f"[bench] parity of sampled reps vs oracle: {parity}", file=sys.stderr, flush=True)
+
+    stream = torch.cuda.current_stream()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in cases] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for k, c in enumerate(cases):
+            ev[s][k][0].record(stream)
+            c.launch()
+            ev[s][k][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_shape = []
+    for k, c in enumerate(cases):
+        ms = sum(ev[s][k][0].elapsed_time(ev[s][k][1]) for s in range(args.steps)) / args.steps
+        gbs = c.bytes_per_launch() / (ms * 1e-3) / 1e9
+        per_shape.append({"shape": f"{c.n_out}x{c.n_in}", "ms_per_launch": round(ms, 4),
+                          "GB_s": round(gbs, 1), "ring": c.ring,
+                          "kernel": "matvec_kernel<%d,%d>" % kernel_config(c.n_in)})
+    total_bytes = sum(c.bytes_per_launch() for c in cases) * args.steps
+    value = total_bytes / wall / 1e9
+    # dominant kernel instantiation: the one with the most time
+    groups = {}
+    for k, c in enumerate(cases):
+        g = groups.setdefault(per_shape[k]["kernel"], [0.0, 0, 0])
+        g[0] += per_shape[k]["ms_per_launch"]
+        g[1] += c.bytes_per_launch()
+        g[2] += 1
+    kname, (gms, gbytes, nl) = max(groups.items(), key=lambda kv: kv[1][0])
+    achieved = (gbytes / nl) / ((gms / nl) * 1e-3) / 1e9
+    out = {
+        "metric": "decode tokens/s at 1 GPU + BFP matvec HBM GB/s (% of peak), bit-exact",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16",
+        "data": "synthetic",
+        "config": {"workload": "bfp_matvec_sweep (BASELINE configs[1])",
+                   "shapes": [f"{o}x{i}" for o, i in SHAPES], "reps_per_shape": args.reps,
+                   "batch": 1},
+        "bit_exact": parity,
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "per_shape": per_shape,
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

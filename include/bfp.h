@@ -1,0 +1,115 @@
+/*
+ * libbfp -- MI355X (gfx950) block-floating-point decode datapath, C ABI.
+ *
+ * The reference has no native API for this path: its interface is the
+ * numpy-in/numpy-out function set of its model-level simulator,
+ * rtl/vc707/host/gen_smollm_blockfp_full.py (below: full.py).  Each entry
+ * point names the function(s) it replaces.  The Python package
+ * (tinyllm-fpga_amd/bfp) binds these with ctypes and re-exposes the
+ * reference's names.
+ *
+ * BFP format: a tile is 16 int16 mantissas sharing one int8 exponent;
+ * value = m * 2^(e-15)  (rtl/vc707/src/smollm/bfp_format.svh:1-27).
+ * "Reference layout": mantissas (rows, in/16, 16) int16 row-major and
+ * exponents (rows, in/16) int8, i.e. what full.py:110-119 quantize_W returns.
+ *
+ * Conventions: every function returns 0 (BFP_OK) or a negative errno-style
+ * code; no exception crosses the ABI.  *_d functions take device pointers
+ * and a hipStream_t passed as void* (NULL = default stream) and are
+ * stream-ordered (asynchronous).  Context functions are synchronous, and a
+ * context must not be used from two threads at once.
+ * bfp_last_error() returns the message of the calling thread's last error.
+ */
+#ifndef BFP_H
+#define BFP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BFP_OK 0
+#define BFP_EINVAL (-22) /* bad argument / shape */
+#define BFP_ENOMEM (-12) /* device allocation failed */
+#define BFP_EIO (-5)     /* HIP runtime error */
+#define BFP_ERANGE (-34) /* position / token beyond the configured capacity */
+
+#define BFP_TILE 16
+
+/* Model dimensions (full.py:54-60 reads them from env vars). */
+typedef struct bfp_dims {
+  int D, H_Q, H_KV, HD, FFN, NL, MAX_CTX, VOCAB;
+} bfp_dims;
+
+/* Weight slots of a layer (full.py:312-318), plus the model-level tables. */
+enum bfp_which {
+  BFP_WQ = 0, BFP_WK = 1, BFP_WV = 2, BFP_WO = 3, BFP_WG = 4, BFP_WU = 5, BFP_WD = 6,
+  BFP_G1 = 7, BFP_G2 = 8,       /* per-layer RMSNorm gammas (D,)           */
+  BFP_EMBED = 9,                /* tied embedding (VOCAB, D), layer ignored */
+  BFP_NORM_W = 10               /* final norm weight (D,), layer ignored    */
+};
+
+const char *bfp_last_error(void);
+const char *bfp_version(void);
+
+/* ---------------------------------------------------------------- layout */
+/* Bytes of one matrix in the device layout (16-row chunks, tile-major). */
+size_t bfp_packed_bytes_m(int n_out, int n_in);
+size_t bfp_packed_bytes_e(int n_out, int n_in);
+
+/* Reference layout -> device layout.  Replaces the wide packing of
+ * full.py:131-161 / gen_smollm_blockfp_ddr.py:88-119 with this build's HBM
+ * layout. */
+int bfp_pack_d(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
+               void *P_m, void *P_e, void *stream);
+
+/* Device layout -> reference layout (inverse of bfp_pack_d). */
+int bfp_unpack_d(const void *P_m, const void *P_e, int n_out, int n_in,
+                 int16_t *W_m, int8_t *W_e, void *stream);
+
+/* ----------------------------------------------------------- quantisation */
+/* tile_quantize (full.py:90-97) of n float64 values (n % 16 == 0):
+ * m (n) int16, e (n/16) int8. */
+int bfp_tile_quantize_f64_d(const double *v, size_t n, int16_t *m, int8_t *e, void *stream);
+/* Same for float32 input (widened exactly, as full.py:319 does). */
+int bfp_tile_quantize_f32_d(const float *v, size_t n, int16_t *m, int8_t *e, void *stream);
+/* quantize_W (full.py:110-119) of a float32 (n_out, n_in) matrix straight
+ * into the device layout. */
+int bfp_quantize_pack_f32_d(const float *W, int n_out, int n_in, void *P_m, void *P_e,
+                            void *stream);
+/* tile_decode (full.py:100-102): (m, e) -> float64, exact. */
+int bfp_tile_decode_d(const int16_t *m, const int8_t *e, size_t n, double *v, void *stream);
+
+/* ---------------------------------------------------------------- matvec */
+/* matvec_hw_golden (full.py:217-233) for n_mats independent problems in one
+ * launch: y_r = W_r x_r, r < n_mats.  W_r is in the device layout at
+ * P_m + r*mat_stride_m bytes / P_e + r*mat_stride_e bytes; x_r mantissas at
+ * x_m + r*x_stride elements and exponents at x_e + r*(x_stride/16); y_r at
+ * y_m + r*y_stride, y_e + r*(y_stride/16).  Output is the BFP (m, e) of
+ * fp_quantize_vec over 16-row tiles, computed in exact integer arithmetic.
+ * n_out % 16 == 0, n_in % 16 == 0.  waves = 0 picks the default workgroup
+ * shape; otherwise 1, 2, 3, 4, 6, 8 or 9 waves per 16-row chunk. */
+int bfp_matvec_d(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats,
+                 long long mat_stride_m, long long mat_stride_e, const int16_t *x_m,
+                 const int8_t *x_e, long long x_stride, int16_t *y_m, int8_t *y_e,
+                 long long y_stride, int waves, void *stream);
+
+/* Same, but problem r reads matrix (r mod ring) -- a ring of distinct weight
+ * copies, so a long batch streams from HBM rather than from cache.  ring = 0
+ * means ring = n_mats.  (Benchmark form; no reference counterpart.) */
+int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats,
+                      int ring, long long mat_stride_m, long long mat_stride_e,
+                      const int16_t *x_m, const int8_t *x_e, long long x_stride, int16_t *y_m,
+                      int8_t *y_e, long long y_stride, int waves, void *stream);
+
+/* Host-buffer convenience form of matvec_hw_golden: W in the reference
+ * layout, x and y in host memory.  Allocates and frees device memory. */
+int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
+                 const int16_t *x_m, const int8_t *x_e, int16_t *y_m, int8_t *y_e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BFP_H */

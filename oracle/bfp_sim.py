@@ -1,0 +1,345 @@
+"""CPU oracle for the BFP decode datapath -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module, and only as the checker (or,
+for bench, as the timed CPU baseline).  The product path
+(``tinyllm-fpga_amd/bfp``) never imports it: it calls the HIP kernels
+through ``libbfp.so`` and fails loudly when that library is missing.
+
+This module restates the model-level block-floating-point simulator of the
+reference ("sim A"), ``rtl/vc707/host/gen_smollm_blockfp_full.py`` (below:
+``full.py``), with the same float64 operations in the same order, so that on
+one machine it yields the same bits as the reference.  Each function cites
+the lines it follows.  Where the reference leans on numpy/BLAS/libm
+internals the restatement uses the same calls:
+
+* ``np.mean``/``ndarray.sum`` -- numpy's pairwise summation (``pairwise_sum``
+  below restates it and the tests pin it against numpy);
+* ``np.dot`` of two 64-vectors -- OpenBLAS ``ddot`` (numpy 2.2.6 bundles
+  scipy-openblas 0.3.29, DYNAMIC_ARCH); ``ddot_skx_order`` restates the
+  SkylakeX/SapphireRapids kernel order and the tests pin it against np.dot on
+  the machine that runs them;
+* ``np.exp`` -- numpy's SIMD exp (not correctly rounded in ~5% of inputs);
+* ``math.cos``/``math.sin``/``**`` -- glibc libm.
+
+BFP format (``rtl/vc707/src/smollm/bfp_format.svh:1-27``): a tile is 16
+int16 mantissas sharing one int8 exponent; value = m * 2**(e-15).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+TILE = 16            # full.py:65
+ALIGN_MAX = 47       # full.py:214
+SAT_HI = (1 << 47) - 1   # full.py:229
+SAT_LO = -(1 << 47)      # full.py:230
+
+
+@dataclass(frozen=True)
+class Dims:
+    """Model dimensions; the reference reads them from env vars
+    (full.py:54-60).  Defaults are SmolLM2-135M's."""
+    D: int = 576
+    H_Q: int = 9
+    H_KV: int = 3
+    HD: int = 64
+    FFN: int = 1536
+    NL: int = 30
+    MAX_CTX: int = 64
+    VOCAB: int = 49152
+
+    @property
+    def KV(self) -> int:
+        return self.H_KV * self.HD
+
+
+# ---------------------------------------------------------------------------
+# Tile quantisation  (full.py:90-119)
+# ---------------------------------------------------------------------------
+def tile_quantize(v):
+    """float vector (len % 16 == 0) -> (m int16 (n/16,16), e int8 (n/16,)).
+
+    full.py:90-97: e = clip(floor(log2(max(|v|, 1e-300))) + 1, -127, 127);
+    m = clip(round_half_even(v / 2**e * 32768), -32768, 32767).
+    """
+    tiles = np.asarray(v, dtype=np.float64).reshape(-1, TILE)
+    amax = np.maximum(np.abs(tiles).max(axis=1), 1e-300)
+    e = (np.floor(np.log2(amax)).astype(np.int32) + 1).clip(-127, 127)
+    scale = np.power(2.0, e.astype(np.float64))[:, None]
+    m = np.clip(np.round(tiles / scale * 32768.0).astype(np.int64), -32768, 32767)
+    return m.astype(np.int16), e.astype(np.int8)
+
+
+def tile_decode(m, e):
+    """(m, e) -> flat float64 (full.py:100-102); exact."""
+    scale = np.power(2.0, np.asarray(e).astype(np.float64))[:, None]
+    return ((np.asarray(m).astype(np.float64) / 32768.0) * scale).flatten()
+
+
+def fp_quantize_vec(v):
+    """quantise then decode (full.py:105-107)."""
+    m, e = tile_quantize(v)
+    return tile_decode(m, e)
+
+
+def quantize_W(W):
+    """Row-wise tile quantisation of a weight matrix (full.py:110-119):
+    (out, in) -> m (out, in/16, 16) int16, e (out, in/16) int8."""
+    n_out, n_in = W.shape
+    assert n_in % TILE == 0
+    nt = n_in // TILE
+    m = np.zeros((n_out, nt, TILE), dtype=np.int16)
+    e = np.zeros((n_out, nt), dtype=np.int8)
+    for r in range(n_out):
+        m[r], e[r] = tile_quantize(W[r])
+    return m, e
+
+
+# ---------------------------------------------------------------------------
+# Exact-integer BFP matvec  (full.py:217-233)
+# ---------------------------------------------------------------------------
+def matvec_acc(x_m, x_e, W_m, W_e):
+    """Integer core of matvec_hw_golden: per-row (A, M) before the float
+    scale.  S[o,t] = sum_k x_m[t,k]*W_m[o,t,k]; E = x_e[t] + W_e[o,t];
+    M = max_t E; A = sum_t floor(S / 2**(M-E)) (0 when M-E > 47), clipped to
+    +-2**47 (full.py:219-231)."""
+    prods = x_m[None, :, :].astype(np.int64) * W_m.astype(np.int64)
+    S = prods.sum(axis=2)
+    E = x_e[None, :].astype(np.int64) + W_e.astype(np.int64)
+    M = E.max(axis=1, keepdims=True)
+    sh = M - E
+    A = np.where(sh <= ALIGN_MAX, np.right_shift(S, np.clip(sh, 0, 63)), 0).sum(axis=1)
+    return np.clip(A, SAT_LO, SAT_HI), M[:, 0]
+
+
+def matvec_hw_golden(x_m, x_e, W_m, W_e):
+    """BFP matvec, float64 out (already re-quantised over 16-row tiles);
+    full.py:217-233."""
+    A, M = matvec_acc(x_m, x_e, W_m, W_e)
+    y = A.astype(np.float64) * np.power(2.0, M.astype(np.float64) - 30)
+    return fp_quantize_vec(y)
+
+
+# ---------------------------------------------------------------------------
+# float64 leaf ops  (full.py:236-258)
+# ---------------------------------------------------------------------------
+def rmsnorm_fp(x, gamma, eps=1e-5):
+    """full.py:236-238 -- note the order (x*gamma)/sqrt(v)."""
+    v = np.mean(x * x) + eps
+    return fp_quantize_vec(x * gamma / np.sqrt(v))
+
+
+def silu_fp(x):
+    """full.py:241-242."""
+    return fp_quantize_vec(x / (1.0 + np.exp(-x)))
+
+
+def softmax_fp(x):
+    """full.py:245-247 (float64 probabilities, not quantised)."""
+    ex = np.exp(x - x.max())
+    return ex / ex.sum()
+
+
+def rope_angle(j, pos, hd, base=10000.0):
+    """theta_j(pos) exactly as full.py:253 evaluates it (Python float pow,
+    then 1/ and *pos)."""
+    return 1.0 / (base ** (2 * j / hd)) * pos
+
+
+def rope_fp(x, pos, hd=64, base=10000.0):
+    """Rotate-half RoPE on one head, then re-quantise (full.py:250-258)."""
+    h2 = hd // 2
+    out = np.array(x, dtype=np.float64)
+    for j in range(h2):
+        th = rope_angle(j, pos, hd, base)
+        c = math.cos(th)
+        s = math.sin(th)
+        a, b = x[j], x[j + h2]
+        out[j] = a * c - b * s
+        out[j + h2] = b * c + a * s
+    return fp_quantize_vec(out)
+
+
+# ---------------------------------------------------------------------------
+# One decoder layer  (full.py:261-293)
+# ---------------------------------------------------------------------------
+STAGES = ("N1", "Q", "K", "V", "ATTN", "O", "H1", "N2", "G", "U", "MLP", "D", "HOUT")
+"""Stage names of the per-layer dump (gen_smollm_blockfp_bfp.py:398-409)."""
+
+
+def new_kv(dims: Dims, max_ctx: int | None = None):
+    n = dims.MAX_CTX if max_ctx is None else max_ctx
+    return {"k": np.zeros((n, dims.H_KV, dims.HD)), "v": np.zeros((n, dims.H_KV, dims.HD))}
+
+
+def fwd_layer(h, lw, pos, kv, kv_pos, dims: Dims = Dims(), dump=None):
+    """One layer of sim A (full.py:261-293).
+
+    ``lw``: dict with 'Wq'..'Wd' as (m, e) tuples and 'g1','g2' float64
+    (BFP-exact) gammas.  ``kv``: {'k','v'} float64 arrays (MAX_CTX, H_KV, HD),
+    mutated in place at ``kv_pos``.  ``dump``: optional dict that receives the
+    float64 value of every stage in ``STAGES`` (post-rope Q/K, as
+    gen_smollm_blockfp_bfp.py:399-400 dumps them).
+    """
+    HD, H_Q, H_KV, D = dims.HD, dims.H_Q, dims.H_KV, dims.D
+    grp = H_Q // H_KV
+    n1 = rmsnorm_fp(h, lw["g1"])
+    n1_m, n1_e = tile_quantize(n1)
+    q = matvec_hw_golden(n1_m, n1_e, *lw["Wq"])
+    k = matvec_hw_golden(n1_m, n1_e, *lw["Wk"])
+    v = matvec_hw_golden(n1_m, n1_e, *lw["Wv"])
+    for hq in range(H_Q):
+        q[hq * HD:(hq + 1) * HD] = rope_fp(q[hq * HD:(hq + 1) * HD], pos, HD)
+    for hk in range(H_KV):
+        k[hk * HD:(hk + 1) * HD] = rope_fp(k[hk * HD:(hk + 1) * HD], pos, HD)
+    for hk in range(H_KV):
+        kv["k"][kv_pos, hk] = k[hk * HD:(hk + 1) * HD]
+        kv["v"][kv_pos, hk] = v[hk * HD:(hk + 1) * HD]
+    attn = np.zeros(D)
+    inv = math.sqrt(HD)
+    for hq in range(H_Q):
+        kvh = hq // grp
+        qh = q[hq * HD:(hq + 1) * HD]
+        scores = np.zeros(kv_pos + 1)
+        for t in range(kv_pos + 1):
+            scores[t] = float(np.dot(qh, kv["k"][t, kvh])) / inv
+        p = softmax_fp(scores)
+        for t in range(kv_pos + 1):
+            attn[hq * HD:(hq + 1) * HD] += p[t] * kv["v"][t, kvh]
+    attn = fp_quantize_vec(attn)
+    a_m, a_e = tile_quantize(attn)
+    o = matvec_hw_golden(a_m, a_e, *lw["Wo"])
+    h1 = fp_quantize_vec(h + o)
+    n2 = rmsnorm_fp(h1, lw["g2"])
+    n2_m, n2_e = tile_quantize(n2)
+    g = matvec_hw_golden(n2_m, n2_e, *lw["Wg"])
+    u = matvec_hw_golden(n2_m, n2_e, *lw["Wu"])
+    mlp = fp_quantize_vec(silu_fp(g) * u)
+    mlp_m, mlp_e = tile_quantize(mlp)
+    d = matvec_hw_golden(mlp_m, mlp_e, *lw["Wd"])
+    h_out = fp_quantize_vec(h1 + d)
+    if dump is not None:
+        for name, val in zip(STAGES, (n1, q, k, v, attn, o, h1, n2, g, u, mlp, d, h_out)):
+            dump[name] = val.copy()
+    return h_out
+
+
+# ---------------------------------------------------------------------------
+# Decode head and the autoregressive loop  (full.py:411-443)
+# ---------------------------------------------------------------------------
+def head_logits(h, norm_w_q, embed):
+    """Final norm (no re-quantise) + tied-embedding logits in float64
+    (full.py:438-439): note the order (h/sqrt(v))*w, unlike rmsnorm_fp."""
+    h_normed = (h / np.sqrt(np.mean(h * h) + 1e-5)) * norm_w_q
+    return h_normed @ embed.T
+
+
+def head_argmax(h, norm_w_q, embed):
+    """Greedy next token: first index of the max logit (full.py:440)."""
+    return int(np.argmax(head_logits(h, norm_w_q, embed)))
+
+
+@dataclass
+class Model:
+    """A BFP model as sim A holds it: per-layer (m, e) weights and BFP-exact
+    gammas, the quantised embedding rows used as inputs (full.py:411-412),
+    the raw float64 embedding used by the head (full.py:439) and the
+    quantised final norm weight (full.py:413)."""
+    dims: Dims
+    layers: list
+    embed: np.ndarray          # (VOCAB, D) float64 (exact copy of fp32 weights)
+    norm_w_q: np.ndarray       # (D,) float64
+    embed_q: np.ndarray | None = field(default=None)
+
+    def embed_row_q(self, tid):
+        if self.embed_q is not None:
+            return self.embed_q[tid]
+        return fp_quantize_vec(self.embed[tid].astype(np.float64))
+
+
+def decode(model: Model, prompt, n_gen, max_ctx=None, on_layer=None, on_step=None):
+    """The golden-token loop of full.py:426-443, including its quirk: the
+    argmax at step len(prompt)-1 is computed but not appended, so step
+    len(prompt) feeds the last prompt token a second time.
+
+    Returns the list ``prompt + generated``.  ``on_layer(step, li, h)`` sees
+    every layer output; ``on_step(step, tid, nid)`` every head result.
+    """
+    dims = model.dims
+    ids = list(int(t) for t in prompt)
+    n_ctx = max_ctx if max_ctx is not None else max(dims.MAX_CTX, len(ids) + n_gen)
+    kv = [new_kv(dims, n_ctx) for _ in range(dims.NL)]
+    generated = list(ids)
+    for step in range(len(ids) + n_gen):
+        tid = ids[step] if step < len(ids) else generated[-1]
+        h = model.embed_row_q(tid)
+        for li in range(dims.NL):
+            h = fwd_layer(h, model.layers[li], pos=step, kv=kv[li], kv_pos=step, dims=dims)
+            if on_layer is not None:
+                on_layer(step, li, h)
+        if step >= len(ids) - 1:
+            nid = head_argmax(h, model.norm_w_q, model.embed)
+            if on_step is not None:
+                on_step(step, tid, nid)
+            if step >= len(ids):
+                generated.append(nid)
+    return generated
+
+
+# ---------------------------------------------------------------------------
+# Restatements of third-party reduction orders (pinned by tests against the
+# library calls themselves)
+# ---------------------------------------------------------------------------
+def pairwise_sum(a, lo=0, n=None):
+    """numpy's float64 add-reduce for one contiguous block (n <= 8192): the
+    8-accumulator pairwise scheme of numpy's ``pairwise_sum`` (block size
+    128, split point rounded down to a multiple of 8)."""
+    if n is None:
+        n = len(a)
+    if n < 8:
+        r = 0.0
+        for i in range(n):
+            r += float(a[lo + i])
+        return r
+    if n <= 128:
+        acc = [float(a[lo + j]) for j in range(8)]
+        i = 8
+        top = n - (n % 8)
+        while i < top:
+            for j in range(8):
+                acc[j] += float(a[lo + i + j])
+            i += 8
+        res = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))
+        while i < n:
+            res += float(a[lo + i])
+            i += 1
+        return res
+    half = n // 2
+    half -= half % 8
+    return pairwise_sum(a, lo, half) + pairwise_sum(a, lo + half, n - half)
+
+
+def _fma(a, b, c):
+    from fractions import Fraction
+    return float(Fraction(a) * Fraction(b) + Fraction(c))
+
+
+def ddot_skx_order(x, y):
+    """OpenBLAS 0.3.29 x86_64 ddot, SkylakeX/SapphireRapids micro-kernel,
+    for n % 32 == 0: four 8-lane FMA accumulators over blocks of 32, each
+    folded 512->256 bits (lane l + lane l+4), summed ((a0+a1)+a2)+a3, then
+    128-bit halves added and a final horizontal add.  Exact-FMA reference
+    (slow; for tests)."""
+    n = len(x)
+    assert n % 32 == 0
+    acc = [[0.0] * 8 for _ in range(4)]
+    for i in range(0, n, 32):
+        for r in range(4):
+            for l in range(8):
+                acc[r][l] = _fma(float(x[i + 8 * r + l]), float(y[i + 8 * r + l]), acc[r][l])
+    f = [[acc[r][l] + acc[r][l + 4] for l in range(4)] for r in range(4)]
+    s = [((f[0][l] + f[1][l]) + f[2][l]) + f[3][l] for l in range(4)]
+    return (s[0] + s[2]) + (s[1] + s[3])

@@ -1,0 +1,76 @@
+"""ctypes binding of libbfp.so (the C ABI declared in include/bfp.h).
+
+The library is built in-tree by ``tinyllm-fpga_amd/build.py`` (or
+``__graft_entry__.build()``).  There is no fallback: if the library is
+missing, or was built for another architecture, ``lib()`` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libbfp.so"
+
+BFP_OK = 0
+ERRNAMES = {-22: "EINVAL", -12: "ENOMEM", -5: "EIO", -34: "ERANGE"}
+
+
+class BfpError(RuntimeError):
+    """A libbfp entry point returned a negative status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed: {ERRNAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+vp, i32, i64, sz = C.c_void_p, C.c_int, C.c_longlong, C.c_size_t
+
+# name -> (restype, argtypes); the list of exported symbols is checked by the
+# CPU test suite against include/bfp.h.
+SIGNATURES = {
+    "bfp_last_error": (C.c_char_p, []),
+    "bfp_version": (C.c_char_p, []),
+    "bfp_packed_bytes_m": (sz, [i32, i32]),
+    "bfp_packed_bytes_e": (sz, [i32, i32]),
+    "bfp_pack_d": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "bfp_unpack_d": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "bfp_tile_quantize_f64_d": (i32, [vp, sz, vp, vp, vp]),
+    "bfp_tile_quantize_f32_d": (i32, [vp, sz, vp, vp, vp]),
+    "bfp_quantize_pack_f32_d": (i32, [vp, i32, i32, vp, vp, vp]),
+    "bfp_tile_decode_d": (i32, [vp, vp, sz, vp, vp]),
+    "bfp_matvec_d": (i32, [vp, vp, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64, i32, vp]),
+    "bfp_matvec_ring_d": (i32, [vp, vp, i32, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64,
+                                i32, vp]),
+    "bfp_matvec_h": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+}
+
+_LIB = None
+
+
+def lib():
+    """Load (once) and return the configured ctypes library."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is missing: build it with "
+                              "`python tinyllm-fpga_amd/build.py` (no CPU fallback exists)")
+        L = C.CDLL(os.fspath(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(fn: str, rc: int):
+    if rc != BFP_OK:
+        msg = lib().bfp_last_error()
+        raise BfpError(fn, rc, msg.decode() if msg else "")
+    return rc
+
+
+def call(fn: str, *args):
+    """Call an int-returning entry point and raise BfpError on failure."""
+    return check(fn, getattr(lib(), fn)(*args))

@@ -1,0 +1,130 @@
+"""The reference simulator's function set, computed on the MI355X.
+
+Drop-in names and argument meanings of
+rtl/vc707/host/gen_smollm_blockfp_full.py (full.py): numpy in, numpy out.
+Every function here runs the HIP kernels of libbfp.so; PyTorch only
+provides device memory and the current stream.  Shape errors raise
+ValueError where the reference would fail its reshape/assert.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import _dev
+from ._lib import call
+
+TILE = 16
+
+
+def _flat_f64(v):
+    a = np.ascontiguousarray(np.asarray(v, dtype=np.float64).reshape(-1))
+    if a.size % TILE:
+        raise ValueError(f"length {a.size} is not a multiple of {TILE}")
+    return a
+
+
+def tile_quantize(v):
+    """full.py:90-97 -> (m int16 (n/16, 16), e int8 (n/16,))."""
+    a = _flat_f64(v)
+    n = a.size
+    dv = _dev.to_dev(a)
+    m = _dev.empty(n, "int16")
+    e = _dev.empty(n // TILE, "int8")
+    call("bfp_tile_quantize_f64_d", _dev.ptr(dv), n, _dev.ptr(m), _dev.ptr(e), _dev.stream())
+    return _dev.to_host(m).reshape(-1, TILE), _dev.to_host(e)
+
+
+def tile_decode(m_int, e_int):
+    """full.py:100-102 -> flat float64 (exact)."""
+    m = np.ascontiguousarray(np.asarray(m_int, dtype=np.int16).reshape(-1))
+    e = np.ascontiguousarray(np.asarray(e_int, dtype=np.int8).reshape(-1))
+    if m.size != e.size * TILE:
+        raise ValueError(f"{m.size} mantissas vs {e.size} exponents")
+    dm, de = _dev.to_dev(m), _dev.to_dev(e)
+    v = _dev.empty(m.size, "float64")
+    call("bfp_tile_decode_d", _dev.ptr(dm), _dev.ptr(de), m.size, _dev.ptr(v), _dev.stream())
+    return _dev.to_host(v)
+
+
+def fp_quantize_vec(v):
+    """full.py:105-107."""
+    return tile_decode(*tile_quantize(v))
+
+
+def quantize_W(W):
+    """full.py:110-119: row-wise tile quantisation -> (m (out, in/16, 16),
+    e (out, in/16))."""
+    W = np.asarray(W)
+    if W.ndim != 2 or W.shape[1] % TILE:
+        raise ValueError(f"bad weight shape {W.shape}")
+    n_out, n_in = W.shape
+    m, e = tile_quantize(W.astype(np.float64))
+    return m.reshape(n_out, n_in // TILE, TILE), e.reshape(n_out, n_in // TILE)
+
+
+class PackedMatrix:
+    """A BFP weight matrix resident in HBM in the kernels' layout."""
+
+    def __init__(self, W_m, W_e):
+        W_m = np.ascontiguousarray(np.asarray(W_m, dtype=np.int16))
+        W_e = np.ascontiguousarray(np.asarray(W_e, dtype=np.int8))
+        if W_m.ndim != 3 or W_m.shape[2] != TILE or W_e.shape != W_m.shape[:2]:
+            raise ValueError(f"bad BFP weight shapes {W_m.shape} / {W_e.shape}")
+        self.n_out, nt, _ = W_m.shape
+        self.n_in = nt * TILE
+        if self.n_out % 16:
+            raise ValueError(f"n_out={self.n_out} is not a multiple of 16")
+        dm, de = _dev.to_dev(W_m), _dev.to_dev(W_e)
+        self.P_m = _dev.empty(W_m.size, "int16")
+        self.P_e = _dev.empty(W_e.size, "int8")
+        call("bfp_pack_d", _dev.ptr(dm), _dev.ptr(de), self.n_out, self.n_in,
+             _dev.ptr(self.P_m), _dev.ptr(self.P_e), _dev.stream())
+
+    @classmethod
+    def from_float(cls, W):
+        """quantize_W on the device from a float32 matrix."""
+        self = cls.__new__(cls)
+        W = np.ascontiguousarray(np.asarray(W, dtype=np.float32))
+        self.n_out, self.n_in = W.shape
+        if self.n_out % 16 or self.n_in % TILE:
+            raise ValueError(f"bad weight shape {W.shape}")
+        dW = _dev.to_dev(W)
+        self.P_m = _dev.empty(W.size, "int16")
+        self.P_e = _dev.empty(W.size // TILE, "int8")
+        call("bfp_quantize_pack_f32_d", _dev.ptr(dW), self.n_out, self.n_in,
+             _dev.ptr(self.P_m), _dev.ptr(self.P_e), _dev.stream())
+        return self
+
+    def unpack(self):
+        m = _dev.empty(self.n_out * self.n_in, "int16")
+        e = _dev.empty(self.n_out * self.n_in // TILE, "int8")
+        call("bfp_unpack_d", _dev.ptr(self.P_m), _dev.ptr(self.P_e), self.n_out, self.n_in,
+             _dev.ptr(m), _dev.ptr(e), _dev.stream())
+        nt = self.n_in // TILE
+        return _dev.to_host(m).reshape(self.n_out, nt, TILE), _dev.to_host(e).reshape(self.n_out, nt)
+
+    def matvec_bfp(self, x_m, x_e, waves=0):
+        """y = W x in BFP: returns (y_m (out,) int16, y_e (out/16,) int8)."""
+        x_m = np.ascontiguousarray(np.asarray(x_m, dtype=np.int16).reshape(-1))
+        x_e = np.ascontiguousarray(np.asarray(x_e, dtype=np.int8).reshape(-1))
+        if x_m.size != self.n_in or x_e.size != self.n_in // TILE:
+            raise ValueError(f"x has {x_m.size} mantissas / {x_e.size} exponents, "
+                             f"matrix expects {self.n_in}")
+        dxm, dxe = _dev.to_dev(x_m), _dev.to_dev(x_e)
+        ym = _dev.empty(self.n_out, "int16")
+        ye = _dev.empty(self.n_out // TILE, "int8")
+        call("bfp_matvec_d", _dev.ptr(self.P_m), _dev.ptr(self.P_e), self.n_out, self.n_in, 1,
+             0, 0, _dev.ptr(dxm), _dev.ptr(dxe), 0, _dev.ptr(ym), _dev.ptr(ye), 0, int(waves),
+             _dev.stream())
+        return _dev.to_host(ym), _dev.to_host(ye)
+
+
+def matvec_bfp(x_m, x_e, W_m, W_e):
+    """matvec_hw_golden with BFP output: (y_m (out,), y_e (out/16,))."""
+    return PackedMatrix(W_m, W_e).matvec_bfp(x_m, x_e)
+
+
+def matvec_hw_golden(x_m, x_e, W_m, W_e):
+    """full.py:217-233: float64 output (the decoded BFP result)."""
+    ym, ye = matvec_bfp(x_m, x_e, W_m, W_e)
+    return tile_decode(ym, ye)

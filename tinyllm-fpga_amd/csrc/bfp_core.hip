@@ -1,0 +1,531 @@
+// Core BFP kernels for gfx950: device weight layout, tile quantisation and
+// the exact-integer BFP matvec, plus their C-ABI launchers (include/bfp.h).
+//
+// Device weight layout (this build's own; the reference's DDR3 image is the
+// 16-lane "wide" layout of gen_smollm_blockfp_ddr.py:88-119).  A matrix of
+// n_out rows is cut into 16-row chunks (full.py's LANES=16 chunks).  Within a
+// chunk the 16 x nT tiles are stored tile-major, each tile as two 256-byte
+// half-planes:
+//     mantissas: byte ((c*nT + t)*2 + h)*256 + r*16 holds
+//                W_m[c*16 + r][t][8h .. 8h+7]   (8 x int16)
+//     exponents: byte (c*nT + t)*16 + r holds W_e[c*16 + r][t]
+// so a wave whose lanes are (row r = lane%16, tile t0 + lane/16) reads four
+// fully used 256-byte runs per 16-byte-per-lane load.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <climits>
+
+#include "bfp.h"
+#include "bfp_device.h"
+#include "bfp_internal.h"
+
+namespace bfp {
+
+// ------------------------------------------------------------------ errors
+static thread_local char g_err[1024] = "";
+
+int set_err(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+const char *last_error() { return g_err; }
+
+// ------------------------------------------------------------------ layout
+__global__ void pack_m_kernel(const int16_t *__restrict__ Wm, long long total, int nT,
+                              uint4 *__restrict__ Pm) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int r = (int)(i & 15), h = (int)((i >> 4) & 1);
+  long long ct = i >> 5;
+  long long c = ct / nT;
+  int t = (int)(ct % nT);
+  Pm[i] = *reinterpret_cast<const uint4 *>(Wm + ((c * 16 + r) * nT + t) * 16 + h * 8);
+}
+
+__global__ void pack_e_kernel(const int8_t *__restrict__ We, long long total, int nT,
+                              int8_t *__restrict__ Pe) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int r = (int)(i & 15);
+  long long ct = i >> 4;
+  long long c = ct / nT;
+  int t = (int)(ct % nT);
+  Pe[i] = We[(c * 16 + r) * nT + t];
+}
+
+__global__ void unpack_m_kernel(const uint4 *__restrict__ Pm, long long total, int nT,
+                                int16_t *__restrict__ Wm) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int r = (int)(i & 15), h = (int)((i >> 4) & 1);
+  long long ct = i >> 5;
+  long long c = ct / nT;
+  int t = (int)(ct % nT);
+  *reinterpret_cast<uint4 *>(Wm + ((c * 16 + r) * nT + t) * 16 + h * 8) = Pm[i];
+}
+
+__global__ void unpack_e_kernel(const int8_t *__restrict__ Pe, long long total, int nT,
+                                int8_t *__restrict__ We) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int r = (int)(i & 15);
+  long long ct = i >> 4;
+  long long c = ct / nT;
+  int t = (int)(ct % nT);
+  We[(c * 16 + r) * nT + t] = Pe[i];
+}
+
+// ------------------------------------------------------------ quantisation
+// One thread per 16-element tile.
+template <typename T>
+__global__ void tile_quantize_kernel(const T *__restrict__ v, long long n_tiles,
+                                     int16_t *__restrict__ m, int8_t *__restrict__ e) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= n_tiles) return;
+  double x[TILE];
+  double amax = 0.0;
+#pragma unroll
+  for (int k = 0; k < TILE; ++k) {
+    x[k] = (double)v[i * TILE + k];
+    amax = fmax(amax, fabs(x[k]));
+  }
+  int ex = tile_exp_of(amax);
+  int mm[TILE];
+#pragma unroll
+  for (int k = 0; k < TILE; ++k) mm[k] = tile_mant_of(x[k], ex);
+  uint4 lo, hi;
+  lo.x = (mm[0] & 0xffff) | (mm[1] << 16);
+  lo.y = (mm[2] & 0xffff) | (mm[3] << 16);
+  lo.z = (mm[4] & 0xffff) | (mm[5] << 16);
+  lo.w = (mm[6] & 0xffff) | (mm[7] << 16);
+  hi.x = (mm[8] & 0xffff) | (mm[9] << 16);
+  hi.y = (mm[10] & 0xffff) | (mm[11] << 16);
+  hi.z = (mm[12] & 0xffff) | (mm[13] << 16);
+  hi.w = (mm[14] & 0xffff) | (mm[15] << 16);
+  uint4 *dst = reinterpret_cast<uint4 *>(m + i * TILE);
+  dst[0] = lo;
+  dst[1] = hi;
+  e[i] = (int8_t)ex;
+}
+
+// quantize_W straight into the device layout: one thread per (row, tile).
+__global__ void quantize_pack_f32_kernel(const float *__restrict__ W, long long total, int nT,
+                                         uint4 *__restrict__ Pm, int8_t *__restrict__ Pe) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;  // row*nT + t
+  if (i >= total) return;
+  long long row = i / nT;
+  int t = (int)(i % nT);
+  const float4 *src = reinterpret_cast<const float4 *>(W + i * TILE);
+  double x[TILE];
+  double amax = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float4 f = src[q];
+    x[4 * q + 0] = f.x;
+    x[4 * q + 1] = f.y;
+    x[4 * q + 2] = f.z;
+    x[4 * q + 3] = f.w;
+  }
+#pragma unroll
+  for (int k = 0; k < TILE; ++k) amax = fmax(amax, fabs(x[k]));
+  int ex = tile_exp_of(amax);
+  int mm[TILE];
+#pragma unroll
+  for (int k = 0; k < TILE; ++k) mm[k] = tile_mant_of(x[k], ex);
+  long long c = row >> 4;
+  int r = (int)(row & 15);
+  long long base = ((c * nT + t) * 2) * 16 + r;
+  uint4 lo, hi;
+  lo.x = (mm[0] & 0xffff) | (mm[1] << 16);
+  lo.y = (mm[2] & 0xffff) | (mm[3] << 16);
+  lo.z = (mm[4] & 0xffff) | (mm[5] << 16);
+  lo.w = (mm[6] & 0xffff) | (mm[7] << 16);
+  hi.x = (mm[8] & 0xffff) | (mm[9] << 16);
+  hi.y = (mm[10] & 0xffff) | (mm[11] << 16);
+  hi.z = (mm[12] & 0xffff) | (mm[13] << 16);
+  hi.w = (mm[14] & 0xffff) | (mm[15] << 16);
+  Pm[base] = lo;
+  Pm[base + 16] = hi;
+  Pe[(c * nT + t) * 16 + r] = (int8_t)ex;
+}
+
+__global__ void tile_decode_kernel(const int16_t *__restrict__ m, const int8_t *__restrict__ e,
+                                   long long n, double *__restrict__ v) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  v[i] = ldexp((double)m[i], (int)e[i >> 4] - 15);
+}
+
+// ------------------------------------------------------------------ matvec
+// Exact integer matvec of one 16-row chunk per workgroup (NW waves).
+//
+// Lane (w, lane): row r = lane%16, tile lane tq = lane/16; it owns tiles
+// t = tq + 4*(w + NW*j), j < TPT.  Per tile the 16-term product sum is
+// exact: x is split as x = 256*xh + xl (xh in [-128,127], xl in [0,255]) so
+// both v_dot2 partial sums stay below 2^27 in int32, and
+// S = 256*sum(w*xh) + sum(w*xl) is formed in int64 (|S| <= 2^34).  Then
+// M = max_t(E) over the row, A = sum_t floor(S_t / 2^(M-E_t)) (dropped when
+// the shift exceeds 47), clip +-2^47, and the 16-row output tile is
+// quantised with the float-free epilogue: e = max_rows(msb|A| + M - 30) + 1,
+// m = rne(A * 2^(M - 15 - e)).  Equals full.py:217-233 bit for bit.
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void matvec_kernel(
+    const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
+    long long smat_e, int nT, int n_chunks, int ring, const int16_t *__restrict__ xm,
+    const int8_t *__restrict__ xe, long long x_stride, int16_t *__restrict__ ym,
+    int8_t *__restrict__ ye, long long y_stride) {
+  extern __shared__ int smem[];
+  int *xs = smem;              // nT * 16: per tile 8 packed xh pairs, 8 packed xl pairs
+  int *xes = smem + nT * 16;   // nT exponents
+  __shared__ int redM[NW * 16];
+  __shared__ long long redA[NW * 16];
+
+  const int mat = blockIdx.x / n_chunks;
+  const int c = blockIdx.x - mat * n_chunks;
+  const int wmat = ring > 0 ? mat % ring : mat;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+
+  const uint4 *pm = Pm + wmat * smat_m + (long long)c * nT * 32;
+  const int8_t *pe = Pe + wmat * smat_e + (long long)c * nT * 16;
+
+  uint4 wa[TPT], wb[TPT];
+  int we[TPT];
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int t = tq + 4 * (w + NW * j);
+    if (t < nT) {
+      wa[j] = pm[t * 32 + r];
+      wb[j] = pm[t * 32 + 16 + r];
+      we[j] = pe[t * 16 + r];
+    } else {
+      wa[j] = make_uint4(0, 0, 0, 0);
+      wb[j] = make_uint4(0, 0, 0, 0);
+      we[j] = 0;
+    }
+  }
+
+  // Stage the (shared) input vector in LDS, split into high/low bytes.
+  const int *x32 = reinterpret_cast<const int *>(xm + mat * x_stride);
+  for (int p = tid; p < nT * 8; p += 64 * NW) {
+    int v = x32[p];
+    int lo = (int)(short)(v & 0xffff), hi = v >> 16;
+    int t = p >> 3, k = p & 7;
+    xs[t * 16 + k] = ((lo >> 8) & 0xffff) | ((hi >> 8) << 16);
+    xs[t * 16 + 8 + k] = (lo & 0xff) | ((hi & 0xff) << 16);
+  }
+  const int8_t *xep = xe + mat * (x_stride / 16);
+  for (int p = tid; p < nT; p += 64 * NW) xes[p] = xep[p];
+  __syncthreads();
+
+  typedef short s2 __attribute__((ext_vector_type(2)));
+#define DOT2(a, b, acc) \
+  __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, (a)), __builtin_bit_cast(s2, (b)), (acc), false)
+
+  long long S[TPT];
+  int E[TPT];
+  int M = -(1 << 29);
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int t = tq + 4 * (w + NW * j);
+    if (t < nT) {
+      const int4 *xp = reinterpret_cast<const int4 *>(xs + t * 16);
+      int4 h0 = xp[0], h1 = xp[1], l0 = xp[2], l1 = xp[3];
+      int ah = 0, al = 0;
+      ah = DOT2(wa[j].x, h0.x, ah);
+      al = DOT2(wa[j].x, l0.x, al);
+      ah = DOT2(wa[j].y, h0.y, ah);
+      al = DOT2(wa[j].y, l0.y, al);
+      ah = DOT2(wa[j].z, h0.z, ah);
+      al = DOT2(wa[j].z, l0.z, al);
+      ah = DOT2(wa[j].w, h0.w, ah);
+      al = DOT2(wa[j].w, l0.w, al);
+      ah = DOT2(wb[j].x, h1.x, ah);
+      al = DOT2(wb[j].x, l1.x, al);
+      ah = DOT2(wb[j].y, h1.y, ah);
+      al = DOT2(wb[j].y, l1.y, al);
+      ah = DOT2(wb[j].z, h1.z, ah);
+      al = DOT2(wb[j].z, l1.z, al);
+      ah = DOT2(wb[j].w, h1.w, ah);
+      al = DOT2(wb[j].w, l1.w, al);
+      S[j] = (long long)ah * 256 + al;
+      E[j] = xes[t] + we[j];
+      M = E[j] > M ? E[j] : M;
+    } else {
+      S[j] = 0;
+      E[j] = -(1 << 29);
+    }
+  }
+#undef DOT2
+
+  // Row max exponent over the row's lanes (tq = 0..3) and waves.
+  M = xor_max(M, 16);
+  M = xor_max(M, 32);
+  if (NW > 1) {
+    if (tq == 0) redM[w * 16 + r] = M;
+    __syncthreads();
+    M = redM[r];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) M = redM[i * 16 + r] > M ? redM[i * 16 + r] : M;
+  }
+
+  long long A = 0;
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int sh = M - E[j];
+    if (sh <= ALIGN_MAX) A += S[j] >> sh;
+  }
+  A = xor_sum(A, 16);
+  A = xor_sum(A, 32);
+  if (NW > 1) {
+    if (tq == 0) redA[w * 16 + r] = A;
+    __syncthreads();
+    if (w == 0) {
+      A = redA[r];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) A += redA[i * 16 + r];
+    }
+  }
+  if (w == 0) {
+    A = A < SAT_LO ? SAT_LO : (A > SAT_HI ? SAT_HI : A);
+    int L = row_log2(A, M);
+    L = xor_max(L, 1);
+    L = xor_max(L, 2);
+    L = xor_max(L, 4);
+    L = xor_max(L, 8);
+    int e = chunk_exp_from_lmax(L);
+    int m = rne_shr_clip(A, e + 15 - M);
+    if (tq == 0) ym[mat * y_stride + c * 16 + r] = (int16_t)m;
+    if (lane == 0) ye[mat * (y_stride / 16) + c] = (int8_t)e;
+  }
+}
+
+typedef void (*matvec_fn)(const uint4 *, const int8_t *, long long, long long, int, int, int,
+                          const int16_t *, const int8_t *, long long, int16_t *, int8_t *,
+                          long long);
+
+template <int NW>
+static matvec_fn pick_tpt(int tpt) {
+  if (tpt <= 1) return matvec_kernel<NW, 1>;
+  if (tpt <= 2) return matvec_kernel<NW, 2>;
+  if (tpt <= 3) return matvec_kernel<NW, 3>;
+  if (tpt <= 4) return matvec_kernel<NW, 4>;
+  if (tpt <= 6) return matvec_kernel<NW, 6>;
+  if (tpt <= 8) return matvec_kernel<NW, 8>;
+  if (tpt <= 12) return matvec_kernel<NW, 12>;
+  if (tpt <= 16) return matvec_kernel<NW, 16>;
+  if (tpt <= 24) return matvec_kernel<NW, 24>;
+  return nullptr;
+}
+
+static matvec_fn pick_matvec(int nw, int tpt) {
+  switch (nw) {
+    case 1: return pick_tpt<1>(tpt);
+    case 2: return pick_tpt<2>(tpt);
+    case 3: return pick_tpt<3>(tpt);
+    case 4: return pick_tpt<4>(tpt);
+    case 6: return pick_tpt<6>(tpt);
+    case 8: return pick_tpt<8>(tpt);
+    case 9: return pick_tpt<9>(tpt);
+    default: return nullptr;
+  }
+}
+
+int default_waves(int nT) {
+  // about three tiles per lane, at most 9 waves
+  int nw = (nT + 11) / 12;
+  static const int allowed[] = {1, 2, 3, 4, 6, 8, 9};
+  for (int a : allowed)
+    if (a >= nw) return a;
+  return 9;
+}
+
+int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats, int ring,
+                  long long smat_m, long long smat_e, const int16_t *x_m, const int8_t *x_e,
+                  long long x_stride, int16_t *y_m, int8_t *y_e, long long y_stride, int waves,
+                  hipStream_t stream) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || n_mats <= 0 || ring < 0)
+    return set_err(BFP_EINVAL, "matvec: bad shape n_out=%d n_in=%d n_mats=%d ring=%d", n_out,
+                   n_in, n_mats, ring);
+  if (!P_m || !P_e || !x_m || !x_e || !y_m || !y_e)
+    return set_err(BFP_EINVAL, "matvec: null pointer");
+  if (smat_m % 16 || x_stride % 16 || y_stride % 16)
+    return set_err(BFP_EINVAL, "matvec: strides must be multiples of 16");
+  const int nT = n_in / 16;
+  const int nw = waves > 0 ? waves : default_waves(nT);
+  const int tpt = (nT + 4 * nw - 1) / (4 * nw);
+  matvec_fn fn = pick_matvec(nw, tpt);
+  if (!fn)
+    return set_err(BFP_EINVAL, "matvec: no kernel for n_in=%d with %d waves (tiles/lane=%d)",
+                   n_in, nw, tpt);
+  const int n_chunks = n_out / 16;
+  long long blocks = (long long)n_chunks * n_mats;
+  if (blocks > INT_MAX) return set_err(BFP_EINVAL, "matvec: grid too large");
+  size_t shm = (size_t)nT * 17 * sizeof(int);
+  if (shm > 60 * 1024) return set_err(BFP_EINVAL, "matvec: n_in=%d too large", n_in);
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * nw), shm, stream,
+                     reinterpret_cast<const uint4 *>(P_m), reinterpret_cast<const int8_t *>(P_e),
+                     smat_m / 16, smat_e, nT, n_chunks, ring, x_m, x_e, x_stride, y_m, y_e,
+                     y_stride);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_err(BFP_EIO, "matvec launch: %s", hipGetErrorString(err));
+  return BFP_OK;
+}
+
+static inline unsigned nblk(long long n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+int launch_status(const char *what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_err(BFP_EIO, "%s launch: %s", what, hipGetErrorString(err));
+  return BFP_OK;
+}
+
+int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, void *P_e,
+         hipStream_t s) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W_m || !W_e || !P_m || !P_e)
+    return set_err(BFP_EINVAL, "pack: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
+  int nT = n_in / 16;
+  long long tm = (long long)(n_out / 16) * nT * 32, te = (long long)(n_out / 16) * nT * 16;
+  hipLaunchKernelGGL(pack_m_kernel, dim3(nblk(tm, 256)), dim3(256), 0, s, W_m, tm, nT,
+                     reinterpret_cast<uint4 *>(P_m));
+  hipLaunchKernelGGL(pack_e_kernel, dim3(nblk(te, 256)), dim3(256), 0, s, W_e, te, nT,
+                     reinterpret_cast<int8_t *>(P_e));
+  return launch_status("pack");
+}
+
+int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W || !P_m || !P_e)
+    return set_err(BFP_EINVAL, "quantize_pack: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
+  int nT = n_in / 16;
+  long long total = (long long)n_out * nT;
+  hipLaunchKernelGGL(quantize_pack_f32_kernel, dim3(nblk(total, 256)), dim3(256), 0, s, W, total,
+                     nT, reinterpret_cast<uint4 *>(P_m), reinterpret_cast<int8_t *>(P_e));
+  return launch_status("quantize_pack");
+}
+
+int tile_quantize_f64(const double *v, size_t n, int16_t *m, int8_t *e, hipStream_t s) {
+  if (n % 16 || !v || !m || !e) return set_err(BFP_EINVAL, "tile_quantize: n=%zu", n);
+  if (n == 0) return BFP_OK;
+  long long nt = (long long)(n / 16);
+  hipLaunchKernelGGL(tile_quantize_kernel<double>, dim3(nblk(nt, 256)), dim3(256), 0, s, v, nt, m,
+                     e);
+  return launch_status("tile_quantize");
+}
+
+}  // namespace bfp
+
+using namespace bfp;
+
+// ------------------------------------------------------------------- C ABI
+extern "C" {
+
+const char *bfp_last_error(void) { return bfp::last_error(); }
+const char *bfp_version(void) { return "libbfp 0.1 (gfx950)"; }
+
+size_t bfp_packed_bytes_m(int n_out, int n_in) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16) return 0;
+  return (size_t)n_out * n_in * 2;
+}
+size_t bfp_packed_bytes_e(int n_out, int n_in) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16) return 0;
+  return (size_t)n_out * (n_in / 16);
+}
+
+int bfp_pack_d(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, void *P_e,
+               void *stream) {
+  return bfp::pack(W_m, W_e, n_out, n_in, P_m, P_e, (hipStream_t)stream);
+}
+
+int bfp_unpack_d(const void *P_m, const void *P_e, int n_out, int n_in, int16_t *W_m,
+                 int8_t *W_e, void *stream) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W_m || !W_e || !P_m || !P_e)
+    return set_err(BFP_EINVAL, "unpack: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
+  hipStream_t s = (hipStream_t)stream;
+  int nT = n_in / 16;
+  long long tm = (long long)(n_out / 16) * nT * 32, te = (long long)(n_out / 16) * nT * 16;
+  hipLaunchKernelGGL(unpack_m_kernel, dim3(nblk(tm, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const uint4 *>(P_m), tm, nT, W_m);
+  hipLaunchKernelGGL(unpack_e_kernel, dim3(nblk(te, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const int8_t *>(P_e), te, nT, W_e);
+  return launch_status("unpack");
+}
+
+int bfp_tile_quantize_f64_d(const double *v, size_t n, int16_t *m, int8_t *e, void *stream) {
+  return bfp::tile_quantize_f64(v, n, m, e, (hipStream_t)stream);
+}
+
+int bfp_tile_quantize_f32_d(const float *v, size_t n, int16_t *m, int8_t *e, void *stream) {
+  if (n % 16 || !v || !m || !e) return set_err(BFP_EINVAL, "tile_quantize: n=%zu", n);
+  if (n == 0) return BFP_OK;
+  long long nt = (long long)(n / 16);
+  hipLaunchKernelGGL(tile_quantize_kernel<float>, dim3(nblk(nt, 256)), dim3(256), 0,
+                     (hipStream_t)stream, v, nt, m, e);
+  return launch_status("tile_quantize");
+}
+
+int bfp_quantize_pack_f32_d(const float *W, int n_out, int n_in, void *P_m, void *P_e,
+                            void *stream) {
+  return bfp::quantize_pack_f32(W, n_out, n_in, P_m, P_e, (hipStream_t)stream);
+}
+
+int bfp_tile_decode_d(const int16_t *m, const int8_t *e, size_t n, double *v, void *stream) {
+  if (n % 16 || !m || !e || !v) return set_err(BFP_EINVAL, "tile_decode: n=%zu", n);
+  if (n == 0) return BFP_OK;
+  hipLaunchKernelGGL(tile_decode_kernel, dim3(nblk((long long)n, 256)), dim3(256), 0,
+                     (hipStream_t)stream, m, e, (long long)n, v);
+  return launch_status("tile_decode");
+}
+
+int bfp_matvec_d(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats,
+                 long long mat_stride_m, long long mat_stride_e, const int16_t *x_m,
+                 const int8_t *x_e, long long x_stride, int16_t *y_m, int8_t *y_e,
+                 long long y_stride, int waves, void *stream) {
+  return bfp::launch_matvec(P_m, P_e, n_out, n_in, n_mats, 0, mat_stride_m, mat_stride_e, x_m,
+                            x_e, x_stride, y_m, y_e, y_stride, waves, (hipStream_t)stream);
+}
+
+int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats,
+                      int ring, long long mat_stride_m, long long mat_stride_e,
+                      const int16_t *x_m, const int8_t *x_e, long long x_stride, int16_t *y_m,
+                      int8_t *y_e, long long y_stride, int waves, void *stream) {
+  return bfp::launch_matvec(P_m, P_e, n_out, n_in, n_mats, ring, mat_stride_m, mat_stride_e, x_m,
+                            x_e, x_stride, y_m, y_e, y_stride, waves, (hipStream_t)stream);
+}
+
+int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
+                 const int16_t *x_m, const int8_t *x_e, int16_t *y_m, int8_t *y_e) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W_m || !W_e || !x_m || !x_e ||
+      !y_m || !y_e)
+    return set_err(BFP_EINVAL, "matvec_h: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
+  DevBuf buf;
+  size_t bm = (size_t)n_out * n_in * 2, be = (size_t)n_out * n_in / 16;
+  int16_t *dWm, *dxm, *dym;
+  int8_t *dWe, *dxe, *dye;
+  void *dPm, *dPe;
+  int rc;
+  if ((rc = buf.alloc((void **)&dWm, bm)) || (rc = buf.alloc((void **)&dWe, be)) ||
+      (rc = buf.alloc(&dPm, bm)) || (rc = buf.alloc(&dPe, be)) ||
+      (rc = buf.alloc((void **)&dxm, (size_t)n_in * 2)) ||
+      (rc = buf.alloc((void **)&dxe, (size_t)n_in / 16)) ||
+      (rc = buf.alloc((void **)&dym, (size_t)n_out * 2)) ||
+      (rc = buf.alloc((void **)&dye, (size_t)n_out / 16)))
+    return rc;
+  HIP_TRY(hipMemcpy(dWm, W_m, bm, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(dWe, W_e, be, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(dxm, x_m, (size_t)n_in * 2, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(dxe, x_e, (size_t)n_in / 16, hipMemcpyHostToDevice));
+  if ((rc = bfp::pack(dWm, dWe, n_out, n_in, dPm, dPe, 0))) return rc;
+  if ((rc = bfp::launch_matvec(dPm, dPe, n_out, n_in, 1, 0, 0, 0, dxm, dxe, 0, dym, dye, 0, 0, 0)))
+    return rc;
+  HIP_TRY(hipMemcpy(y_m, dym, (size_t)n_out * 2, hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(y_e, dye, (size_t)n_out / 16, hipMemcpyDeviceToHost));
+  return BFP_OK;
+}
+
+}  // extern "C"

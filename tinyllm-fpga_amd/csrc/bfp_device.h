@@ -1,0 +1,87 @@
+// Device-side helpers shared by the BFP kernels (gfx950, wave64).
+//
+// Numerics follow the reference's model-level simulator,
+// rtl/vc707/host/gen_smollm_blockfp_full.py (full.py):
+//   tile_quantize  full.py:90-97   e = clip(floor(log2 max|v|) + 1, -127, 127)
+//                                  m = clip(rne(v * 2^(15-e)), -32768, 32767)
+//   matvec         full.py:217-233 exact integer tile sums, max-first floor
+//                                  alignment, float64 scale, re-quantise.
+// All float64 code in this build is compiled with -ffp-contract=off: every
+// product and sum is rounded separately, as numpy does.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bfp {
+
+constexpr int TILE = 16;
+constexpr int ALIGN_MAX = 47;
+constexpr long long SAT_HI = (1LL << 47) - 1;
+constexpr long long SAT_LO = -(1LL << 47);
+
+// Shared exponent of a tile from its max |v|: floor(log2(amax)) + 1 clipped to
+// [-127, 127].  frexp gives amax = f * 2^x with f in [0.5, 1), so
+// floor(log2(amax)) + 1 == x exactly.  amax == 0 -> -127 (the reference floors
+// amax at 1e-300, whose exponent clips to -127).
+__device__ __forceinline__ int tile_exp_of(double amax) {
+  if (!(amax > 0.0)) return -127;
+  int x;
+  (void)frexp(amax, &x);
+  return x < -127 ? -127 : (x > 127 ? 127 : x);
+}
+
+// Mantissa: rne(v * 2^(15-e)) clipped; ldexp is exact here, rint is
+// round-half-even (np.round with 0 decimals).
+__device__ __forceinline__ int tile_mant_of(double v, int e) {
+  double s = rint(ldexp(v, 15 - e));
+  s = fmin(fmax(s, -32768.0), 32767.0);
+  return (int)s;
+}
+
+// rne(A / 2^s) clipped to int16, for |A| < 2^48; s may be <= 0 (left shift).
+__device__ __forceinline__ int rne_shr_clip(long long A, int s) {
+  long long v;
+  if (A == 0) {
+    v = 0;
+  } else if (s <= 0) {
+    int l = -s;
+    v = (l > 20) ? (A > 0 ? 32767 : -32768) : (A * (1LL << l));
+  } else if (s >= 62) {
+    v = 0;
+  } else {
+    long long q = A >> s;                  // floor
+    long long r = A - q * (1LL << s);      // 0 <= r < 2^s
+    long long h = 1LL << (s - 1);
+    v = q + ((r > h || (r == h && (q & 1))) ? 1 : 0);
+  }
+  return v < -32768 ? -32768 : (v > 32767 ? 32767 : (int)v);
+}
+
+__device__ __forceinline__ int msb64(unsigned long long a) { return 63 - __clzll(a); }
+
+// floor(log2|y|) of y = A * 2^(M-30), or INT_MIN-ish sentinel when A == 0.
+constexpr int L_NONE = -(1 << 30);
+__device__ __forceinline__ int row_log2(long long A, int M) {
+  if (A == 0) return L_NONE;
+  unsigned long long a = A < 0 ? (unsigned long long)(-A) : (unsigned long long)A;
+  return msb64(a) + M - 30;
+}
+
+__device__ __forceinline__ int chunk_exp_from_lmax(int Lmax) {
+  if (Lmax == L_NONE) return -127;
+  int e = Lmax + 1;
+  return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+
+// Wave-level reductions (wave64) with cross-lane shuffles.
+template <typename T>
+__device__ __forceinline__ T xor_max(T v, int mask) {
+  T o = __shfl_xor(v, mask, 64);
+  return o > v ? o : v;
+}
+template <typename T>
+__device__ __forceinline__ T xor_sum(T v, int mask) {
+  return v + __shfl_xor(v, mask, 64);
+}
+
+}  // namespace bfp

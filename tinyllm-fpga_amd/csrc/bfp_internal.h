@@ -1,0 +1,60 @@
+// Host-side internals shared by the libbfp translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "bfp.h"
+
+namespace bfp {
+
+int set_err(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+const char *last_error();
+int launch_status(const char *what);
+
+#define HIP_TRY(expr)                                                                   \
+  do {                                                                                  \
+    hipError_t _e = (expr);                                                             \
+    if (_e != hipSuccess)                                                               \
+      return ::bfp::set_err(BFP_EIO, "%s: %s (%s:%d)", #expr, hipGetErrorString(_e),    \
+                            __FILE__, __LINE__);                                        \
+  } while (0)
+
+#define BFP_TRY(expr)          \
+  do {                         \
+    int _rc = (expr);          \
+    if (_rc) return _rc;       \
+  } while (0)
+
+// Scoped device allocations for the host-buffer convenience entry points.
+struct DevBuf {
+  std::vector<void *> ptrs;
+  int alloc(void **p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+      *p = nullptr;
+      return set_err(BFP_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    ptrs.push_back(*p);
+    return BFP_OK;
+  }
+  ~DevBuf() {
+    for (void *p : ptrs) (void)hipFree(p);
+  }
+};
+
+int default_waves(int nT);
+int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats, int ring,
+                  long long smat_m, long long smat_e, const int16_t *x_m, const int8_t *x_e,
+                  long long x_stride, int16_t *y_m, int8_t *y_e, long long y_stride, int waves,
+                  hipStream_t stream);
+int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, void *P_e,
+         hipStream_t s);
+int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s);
+int tile_quantize_f64(const double *v, size_t n, int16_t *m, int8_t *e, hipStream_t s);
+
+}  // namespace bfp
