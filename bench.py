@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--reps", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--probe", action="store_true",
+                    help="also time a 1 GiB device copy and a 2 GiB streaming read "
+                         "(practical HBM ceiling; the copy calibrates rocprof counters)")
     return ap.parse_args()
 
 
@@ -161,6 +164,30 @@ def cpu_baseline(seconds):
                       + ", ".join(done) + f" in {total_t:.1f} s"}
 
 
+def stream_probe():
+    """Practical HBM ceilings: a 1 GiB device-to-device copy (read + write
+    bytes) and a streaming read (float32 sum over 2 GiB)."""
+    import torch
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    f = torch.ones(1 << 29, dtype=torch.float32, device="cuda")
+    res = {}
+    for name, fn, nbytes in (("copy_1GiB", lambda: b.copy_(a), 2 << 30),
+                             ("read_sum_2GiB", lambda: f.sum(), 2 << 30)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name + "_GB_s"] = round(nbytes * 5 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del a, b, f
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -236,6 +263,8 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
     }
+    if args.probe:
+        out["stream_ceiling"] = stream_probe()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
