@@ -207,8 +207,6 @@ def main():
         for c in cases:
             c.launch()
     torch.cuda.synchronize()
-    parity = all(c.check() for c in cases)
-    print(f"[bench] parity of sampled reps vs oracle: {parity}", file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream()
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -222,6 +220,8 @@ def main():
             ev[s][k][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    parity = all(c.check() for c in cases)
+    print(f"[bench] parity of sampled reps vs oracle: {parity}", file=sys.stderr, flush=True)
     per_shape = []
     for k, c in enumerate(cases):
         ms = sum(ev[s][k][0].elapsed_time(ev[s][k][1]) for s in range(args.steps)) / args.steps

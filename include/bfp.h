@@ -109,6 +109,64 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
 int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
                  const int16_t *x_m, const int8_t *x_e, int16_t *y_m, int8_t *y_e);
 
+/* ------------------------------------------------------------- model */
+/* A context owns one GPU's copy of the model (BFP weights in the device
+ * layout, float64 gammas, the float32 tied embedding, the RoPE table), the
+ * KV cache for max_batch sequences x dims->MAX_CTX positions, and a stream.
+ * Replaces the module-level model state of full.py:299-428.  Returns NULL
+ * on error (see bfp_last_error). */
+typedef struct bfp_ctx bfp_ctx;
+bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch);
+void bfp_destroy(bfp_ctx *ctx);
+int bfp_get_dims(const bfp_ctx *ctx, bfp_dims *out);
+
+/* Load one tensor (which = enum bfp_which).  Matrices (rows x cols as in
+ * full.py:312-318) from float32 -- quantize_W on the device (full.py:110-119)
+ * -- or from the reference layout (m, e).  BFP_G1/G2/NORM_W: float32
+ * (quantised as fp_quantize_vec, full.py:322-323,413) or (m, e).
+ * BFP_EMBED: float32 only (the head uses the raw table, full.py:439).
+ * layer is ignored for EMBED and NORM_W.  Host buffers are copied. */
+int bfp_load_weights(bfp_ctx *ctx, int which, int layer, const float *fp32, const int16_t *m,
+                     const int8_t *e);
+
+/* Zero the KV cache (the reference starts every run from zeros, full.py:426-428). */
+int bfp_reset_kv(bfp_ctx *ctx);
+
+/* Per-stage BFP outputs of one layer step, as gen_smollm_blockfp_bfp.py:398-409
+ * dumps them (Q and K after RoPE).  Host buffers of batch x len mantissas and
+ * batch x len/16 exponents; NULL entries are skipped.  Stage order:
+ * N1 Q K V ATTN O H1 N2 G U MLP D HOUT, lengths D D KV KV D D D D FFN FFN FFN D D. */
+#define BFP_N_STAGES 13
+typedef struct bfp_stage_dump {
+  int16_t *m[BFP_N_STAGES];
+  int8_t *e[BFP_N_STAGES];
+} bfp_stage_dump;
+
+/* fwd_layer (full.py:261-293) at position pos (kv_pos = pos) for batch
+ * sequences: h (batch x D BFP, host) -> out; writes the KV cache slot pos of
+ * this layer. */
+int bfp_layer_step(bfp_ctx *ctx, int layer, int pos, int batch, const int16_t *h_m,
+                   const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump);
+
+/* Decode head (full.py:438-440): final norm, float64 logits over the raw
+ * embedding, first-index argmax.  logits may be NULL. */
+int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, double *logits,
+             int32_t *argmax);
+
+/* The golden-token loop (full.py:426-443) on the device for batch
+ * independent sequences, including the reference's quirk that step
+ * n_prompt re-feeds the last prompt token.  prompt: batch x n_prompt;
+ * tokens_out: batch x n_gen.  hist_m/hist_e (optional): every layer's
+ * output at every step, (batch, n_prompt + n_gen, NL, D) / (..., D/16).
+ * The KV cache is overwritten from position 0. */
+#define BFP_DECODE_NO_GRAPH 1
+int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int batch,
+               int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags);
+
+/* Device time (HIP events) of the last bfp_decode: all steps, and the steps
+ * from n_prompt on. */
+int bfp_decode_time(const bfp_ctx *ctx, float *total_ms, float *gen_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -343,3 +343,22 @@ def ddot_skx_order(x, y):
     f = [[acc[r][l] + acc[r][l + 4] for l in range(4)] for r in range(4)]
     s = [((f[0][l] + f[1][l]) + f[2][l]) + f[3][l] for l in range(4)]
     return (s[0] + s[2]) + (s[1] + s[3])
+
+
+def build_model(fm) -> Model:
+    """Quantise a float32 model the way full.py:309-328,411-413 does:
+    quantize_W per matrix (row loop), fp_quantize_vec of the gammas and the
+    final norm weight; the raw embedding is kept (widened to float64) for the
+    head.  ``fm`` has ``dims``, ``layers`` (dicts of float32 arrays),
+    ``embed`` and ``norm_w``."""
+    layers = []
+    for lw in fm.layers:
+        q = {name: quantize_W(np.asarray(lw[name]).astype(np.float64))
+             for name in ("Wq", "Wk", "Wv", "Wo", "Wg", "Wu", "Wd")}
+        q["g1"] = fp_quantize_vec(np.asarray(lw["g1"]).astype(np.float64))
+        q["g2"] = fp_quantize_vec(np.asarray(lw["g2"]).astype(np.float64))
+        layers.append(q)
+    d = fm.dims
+    dims = Dims(d.D, d.H_Q, d.H_KV, d.HD, d.FFN, d.NL, d.MAX_CTX, d.VOCAB)
+    return Model(dims, layers, np.asarray(fm.embed).astype(np.float64),
+                 fp_quantize_vec(np.asarray(fm.norm_w).astype(np.float64)))

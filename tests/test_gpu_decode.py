@@ -1,0 +1,97 @@
+"""GPU parity of the decode head and the autoregressive driver against the
+oracle (full.py:411-443): token ids and every layer's output at every step,
+bit for bit, graph-replayed and directly launched, batch 1 and batched."""
+import numpy as np
+import pytest
+
+from oracle import bfp_sim as sim
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(D=128, H_Q=2, H_KV=1, HD=64, FFN=256, NL=2, MAX_CTX=32, VOCAB=512)
+
+
+def _setup(cfg, seed, max_batch=1):
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    d = Dims(**cfg)
+    fm = synth.make_model(d, seed=seed)
+    om = sim.build_model(fm)
+    gm = BfpModel(d, max_batch=max_batch)
+    gm.load_fp32(fm)
+    return d, om, gm
+
+
+def _oracle_decode(om, prompt, n_gen):
+    d = om.dims
+    steps = len(prompt) + n_gen
+    hm = np.zeros((steps, d.NL, d.D), np.int16)
+    he = np.zeros((steps, d.NL, d.D // 16), np.int8)
+
+    def on_layer(step, li, h):
+        m, e = sim.tile_quantize(h)
+        hm[step, li] = m.reshape(-1)
+        he[step, li] = e
+
+    toks = sim.decode(om, prompt, n_gen, on_layer=on_layer)
+    return toks[len(prompt):], hm, he
+
+
+def test_head_argmax_and_logits(gpu):
+    d, om, gm = _setup(TINY, seed=4, max_batch=4)
+    rng = np.random.default_rng(1)
+    hs = [sim.fp_quantize_vec(rng.standard_normal(d.D) * s) for s in (0.5, 1.0, 3.0, 10.0)]
+    q = [sim.tile_quantize(h) for h in hs]
+    am, lg = gm.head(np.stack([x[0].reshape(-1) for x in q]), np.stack([x[1] for x in q]),
+                     logits=True)
+    for b, h in enumerate(hs):
+        want = sim.head_logits(h, om.norm_w_q, om.embed)
+        # float64 logits agree to rounding (BLAS order differs); argmax exactly
+        assert np.allclose(lg[b], want, rtol=1e-13, atol=1e-13)
+        assert am[b] == int(np.argmax(want))
+    gm.close()
+
+
+@pytest.mark.parametrize("graph", [True, False], ids=["graph", "direct"])
+def test_decode_tiny(gpu, graph):
+    d, om, gm = _setup(TINY, seed=5)
+    from bfp import synth
+    prompt = synth.make_prompt(d, 5, seed=5)
+    want, whm, whe = _oracle_decode(om, prompt, 10)
+    toks, (hm, he) = gm.decode(prompt[None, :], 10, hist=True, graph=graph)
+    for s in range(whm.shape[0]):
+        for li in range(d.NL):
+            assert (he[0, s, li] == whe[s, li]).all() and (hm[0, s, li] == whm[s, li]).all(), \
+                f"step {s} layer {li} differs"
+    assert list(toks[0]) == list(want)
+    gm.close()
+
+
+def test_decode_batched(gpu):
+    d, om, gm = _setup(TINY, seed=6, max_batch=3)
+    from bfp import synth
+    prompts = np.stack([synth.make_prompt(d, 4, seed=10 + b) for b in range(3)])
+    toks, _ = gm.decode(prompts, 6)
+    for b in range(3):
+        want, _, _ = _oracle_decode(om, prompts[b], 6)
+        assert list(toks[b]) == list(want), f"sequence {b}"
+    gm.close()
+
+
+def test_decode_single_token_prompt(gpu):
+    """n_prompt = 1: the head runs from step 0 and step 1 re-feeds the prompt."""
+    d, om, gm = _setup(TINY, seed=7)
+    want, _, _ = _oracle_decode(om, [3], 4)
+    toks, _ = gm.decode(np.array([[3]]), 4)
+    assert list(toks[0]) == list(want)
+    gm.close()
+
+
+def test_decode_errors(gpu):
+    from bfp._lib import BfpError
+    d, om, gm = _setup(TINY, seed=8)
+    with pytest.raises(BfpError):
+        gm.decode(np.array([[d.VOCAB]]), 2)           # token out of range
+    with pytest.raises(BfpError):
+        gm.decode(np.array([[1, 2]]), d.MAX_CTX)       # beyond the KV capacity
+    gm.close()

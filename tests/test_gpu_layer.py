@@ -1,0 +1,86 @@
+"""GPU parity of one decoder layer against the oracle's
+fwd_layer (oracle/bfp_sim.py restating
+rtl/vc707/host/gen_smollm_blockfp_full.py:261-293): every one of the 13
+stage outputs, bit for bit, at positions 0..7 with the KV cache growing."""
+import numpy as np
+import pytest
+
+from oracle import bfp_sim as sim
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(D=64, H_Q=1, H_KV=1, HD=64, FFN=128, NL=1, MAX_CTX=16, VOCAB=256)
+MID = dict(D=192, H_Q=3, H_KV=1, HD=64, FFN=256, NL=1, MAX_CTX=16, VOCAB=256)
+FULL = dict(D=576, H_Q=9, H_KV=3, HD=64, FFN=1536, NL=1, MAX_CTX=16, VOCAB=256)
+
+
+def _setup(cfg, seed, max_batch=1):
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    d = Dims(**cfg)
+    fm = synth.make_model(d, seed=seed)
+    om = sim.build_model(fm)
+    gm = BfpModel(d, max_batch=max_batch)
+    gm.load_fp32(fm)
+    return d, om, gm
+
+
+def _check_stages(stages, dump, b, pos, tag):
+    for name in sim.STAGES:
+        wm, we = sim.tile_quantize(dump[name])
+        gm_, ge_ = stages[name]
+        assert (ge_[b] == we).all(), f"{tag} pos {pos}: stage {name} exponents differ"
+        assert (gm_[b] == wm.reshape(-1)).all(), f"{tag} pos {pos}: stage {name} mantissas differ"
+
+
+@pytest.mark.parametrize("cfg", [SMALL, MID, FULL], ids=["small", "mid", "full"])
+def test_layer_8_positions(gpu, cfg):
+    d, om, gm = _setup(cfg, seed=1)
+    print(f"[layer] dims {cfg}", flush=True)
+    from bfp import synth
+    xs = synth.make_layer_inputs(d, 8, seed=1)
+    kv = sim.new_kv(om.dims, d.MAX_CTX)
+    for p in range(8):
+        h = sim.fp_quantize_vec(xs[p])
+        dump = {}
+        want = sim.fwd_layer(h, om.layers[0], pos=p, kv=kv, kv_pos=p, dims=om.dims, dump=dump)
+        hm, he = sim.tile_quantize(h)
+        out_m, out_e, st = gm.layer_step_bfp(0, p, hm.reshape(1, -1), he.reshape(1, -1), dump=True)
+        _check_stages(st, dump, 0, p, str(cfg["D"]))
+        wm, we = sim.tile_quantize(want)
+        assert (out_m[0] == wm.reshape(-1)).all() and (out_e[0] == we).all()
+    gm.close()
+
+
+def test_layer_batched_sequences(gpu):
+    """Three independent sequences in one launch: each matches its own
+    oracle run (own KV cache)."""
+    d, om, gm = _setup(MID, seed=2, max_batch=3)
+    rng = np.random.default_rng(5)
+    kvs = [sim.new_kv(om.dims, d.MAX_CTX) for _ in range(3)]
+    for p in range(5):
+        hs = [sim.fp_quantize_vec(rng.standard_normal(d.D) * (1 + b)) for b in range(3)]
+        q = [sim.tile_quantize(h) for h in hs]
+        hm = np.stack([x[0].reshape(-1) for x in q])
+        he = np.stack([x[1] for x in q])
+        out_m, out_e, st = gm.layer_step_bfp(0, p, hm, he, dump=True)
+        for b in range(3):
+            dump = {}
+            sim.fwd_layer(hs[b], om.layers[0], pos=p, kv=kvs[b], kv_pos=p, dims=om.dims, dump=dump)
+            _check_stages(st, dump, b, p, f"seq{b}")
+    gm.close()
+
+
+def test_fwd_layer_float_api(gpu):
+    """The reference-named float64 entry point."""
+    d, om, gm = _setup(SMALL, seed=3)
+    kv = sim.new_kv(om.dims, d.MAX_CTX)
+    rng = np.random.default_rng(0)
+    for p in range(3):
+        h = sim.fp_quantize_vec(rng.standard_normal(d.D))
+        want = sim.fwd_layer(h, om.layers[0], pos=p, kv=kv, kv_pos=p, dims=om.dims)
+        got = gm.fwd_layer(h, 0, p)
+        assert (got == want).all()
+    with pytest.raises(ValueError):
+        gm.fwd_layer(h, 0, 3, kv_pos=2)
+    gm.close()

@@ -25,6 +25,18 @@ class BfpError(RuntimeError):
 
 
 vp, i32, i64, sz = C.c_void_p, C.c_int, C.c_longlong, C.c_size_t
+N_STAGES = 13
+
+
+class DimsC(C.Structure):
+    """struct bfp_dims."""
+    _fields_ = [(n, C.c_int) for n in ("D", "H_Q", "H_KV", "HD", "FFN", "NL", "MAX_CTX", "VOCAB")]
+
+
+class StageDumpC(C.Structure):
+    """struct bfp_stage_dump."""
+    _fields_ = [("m", C.c_void_p * N_STAGES), ("e", C.c_void_p * N_STAGES)]
+
 
 # name -> (restype, argtypes); the list of exported symbols is checked by the
 # CPU test suite against include/bfp.h.
@@ -43,6 +55,15 @@ SIGNATURES = {
     "bfp_matvec_ring_d": (i32, [vp, vp, i32, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64,
                                 i32, vp]),
     "bfp_matvec_h": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+    "bfp_create": (vp, [C.POINTER(DimsC), i32, i32]),
+    "bfp_destroy": (None, [vp]),
+    "bfp_get_dims": (i32, [vp, C.POINTER(DimsC)]),
+    "bfp_load_weights": (i32, [vp, i32, i32, vp, vp, vp]),
+    "bfp_reset_kv": (i32, [vp]),
+    "bfp_layer_step": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, C.POINTER(StageDumpC)]),
+    "bfp_head": (i32, [vp, i32, vp, vp, vp, vp]),
+    "bfp_decode": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, i32]),
+    "bfp_decode_time": (i32, [vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
 }
 
 _LIB = None

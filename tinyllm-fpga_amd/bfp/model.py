@@ -1,0 +1,162 @@
+"""HBM-resident BFP model: layer step, decode head and the autoregressive
+driver of rtl/vc707/host/gen_smollm_blockfp_full.py (full.py:261-293,
+411-443), computed by libbfp.so on one GPU.
+
+Host arrays go in and out as numpy; the model, KV cache and every
+intermediate stay in device memory owned by the C context.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import synth
+from ._lib import BfpError, DimsC, N_STAGES, StageDumpC, call, lib
+from .dims import Dims
+
+STAGES = ("N1", "Q", "K", "V", "ATTN", "O", "H1", "N2", "G", "U", "MLP", "D", "HOUT")
+WHICH = {"Wq": 0, "Wk": 1, "Wv": 2, "Wo": 3, "Wg": 4, "Wu": 5, "Wd": 6, "g1": 7, "g2": 8,
+         "embed": 9, "norm_w": 10}
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _c16(a):
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int16))
+
+
+def _c8(a):
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int8))
+
+
+class BfpModel:
+    """One context: weights for ``dims.NL`` layers, KV cache for
+    ``max_batch`` sequences of ``dims.MAX_CTX`` positions."""
+
+    def __init__(self, dims: Dims, device: int = 0, max_batch: int = 1):
+        self.dims = dims.check()
+        self.max_batch = max_batch
+        cd = DimsC(dims.D, dims.H_Q, dims.H_KV, dims.HD, dims.FFN, dims.NL, dims.MAX_CTX,
+                   dims.VOCAB)
+        h = lib().bfp_create(C.byref(cd), device, max_batch)
+        if not h:
+            raise BfpError("bfp_create", -22, lib().bfp_last_error().decode())
+        self._h = C.c_void_p(h)
+
+    # ------------------------------------------------------------ lifetime
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().bfp_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -------------------------------------------------------------- weights
+    def load_tensor(self, name, layer=0, fp32=None, m=None, e=None):
+        w = WHICH[name]
+        if fp32 is not None:
+            f = np.ascontiguousarray(np.asarray(fp32, dtype=np.float32))
+            call("bfp_load_weights", self._h, w, layer, _p(f), None, None)
+        else:
+            mm, ee = _c16(m), _c8(e)
+            call("bfp_load_weights", self._h, w, layer, None, _p(mm), _p(ee))
+
+    def load_fp32(self, fm: synth.Fp32Model):
+        """Load a float32 model (quantize_W / fp_quantize_vec on the device)."""
+        if fm.dims != self.dims:
+            raise ValueError(f"model dims {fm.dims} != context dims {self.dims}")
+        for li, lw in enumerate(fm.layers):
+            for name in ("Wq", "Wk", "Wv", "Wo", "Wg", "Wu", "Wd", "g1", "g2"):
+                self.load_tensor(name, li, fp32=lw[name])
+        self.load_tensor("embed", fp32=fm.embed)
+        self.load_tensor("norm_w", fp32=fm.norm_w)
+
+    def reset_kv(self):
+        call("bfp_reset_kv", self._h)
+
+    # ----------------------------------------------------------- layer step
+    def _stage_len(self, name):
+        d = self.dims
+        return {"K": d.KV, "V": d.KV, "G": d.FFN, "U": d.FFN, "MLP": d.FFN}.get(name, d.D)
+
+    def layer_step_bfp(self, layer, pos, h_m, h_e, dump=False):
+        """fwd_layer on BFP input (batch, D) / (batch, D/16); returns
+        (out_m, out_e, stages) where stages maps stage name -> (m, e)."""
+        h_m = _c16(h_m).reshape(-1, self.dims.D)
+        batch = h_m.shape[0]
+        h_e = _c8(h_e).reshape(batch, self.dims.D // 16)
+        out_m = np.empty_like(h_m)
+        out_e = np.empty_like(h_e)
+        stages = {}
+        sd = None
+        if dump:
+            sd = StageDumpC()
+            for i, name in enumerate(STAGES):
+                n = self._stage_len(name)
+                sm = np.empty((batch, n), np.int16)
+                se = np.empty((batch, n // 16), np.int8)
+                stages[name] = (sm, se)
+                sd.m[i] = _p(sm)
+                sd.e[i] = _p(se)
+        call("bfp_layer_step", self._h, layer, pos, batch, _p(h_m), _p(h_e), _p(out_m), _p(out_e),
+             C.byref(sd) if sd is not None else None)
+        return out_m, out_e, stages
+
+    def fwd_layer(self, h, layer, pos, kv_pos=None):
+        """The reference's fwd_layer(h, lw, pos, kv, kv_pos) (full.py:261-293)
+        with the layer's weights and KV cache resident in the context:
+        float64 BFP-exact h (D,) in, float64 out."""
+        from . import api
+        if kv_pos is not None and kv_pos != pos:
+            raise ValueError("the device layer step uses kv_pos == pos (as the decode loop does)")
+        m, e = api.tile_quantize(h)
+        om, oe, _ = self.layer_step_bfp(layer, pos, m.reshape(1, -1), e.reshape(1, -1))
+        return api.tile_decode(om[0], oe[0])
+
+    # ----------------------------------------------------------------- head
+    def head(self, h_m, h_e, logits=False):
+        """Final norm + float64 logits + argmax (full.py:438-440) for a batch
+        of BFP hidden states; returns (argmax ids, logits or None)."""
+        h_m = _c16(h_m).reshape(-1, self.dims.D)
+        batch = h_m.shape[0]
+        h_e = _c8(h_e).reshape(batch, self.dims.D // 16)
+        am = np.empty(batch, np.int32)
+        lg = np.empty((batch, self.dims.VOCAB), np.float64) if logits else None
+        call("bfp_head", self._h, batch, _p(h_m), _p(h_e), _p(lg) if logits else None, _p(am))
+        return am, lg
+
+    # --------------------------------------------------------------- decode
+    def decode(self, prompts, n_gen, hist=False, graph=True):
+        """Greedy decode (full.py:426-443) of a batch of prompts
+        (batch, n_prompt).  Returns (tokens (batch, n_gen), hist) where hist
+        is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16))."""
+        P = np.ascontiguousarray(np.atleast_2d(np.asarray(prompts, dtype=np.int32)))
+        batch, n_prompt = P.shape
+        toks = np.zeros((batch, max(n_gen, 1)), np.int32)
+        hm = he = None
+        d = self.dims
+        if hist:
+            steps = n_prompt + n_gen
+            hm = np.zeros((batch, steps, d.NL, d.D), np.int16)
+            he = np.zeros((batch, steps, d.NL, d.D // 16), np.int8)
+        call("bfp_decode", self._h, _p(P), n_prompt, n_gen, batch, _p(toks),
+             _p(hm) if hist else None, _p(he) if hist else None, 0 if graph else 1)
+        return toks[:, :n_gen], ((hm, he) if hist else None)
+
+    def decode_time_ms(self):
+        t, g = C.c_float(), C.c_float()
+        call("bfp_decode_time", self._h, C.byref(t), C.byref(g))
+        return t.value, g.value

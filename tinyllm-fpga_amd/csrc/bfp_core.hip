@@ -20,6 +20,7 @@
 #include "bfp.h"
 #include "bfp_device.h"
 #include "bfp_internal.h"
+#include "bfp_mv.h"
 
 namespace bfp {
 
@@ -37,26 +38,29 @@ int set_err(int code, const char *fmt, ...) {
 const char *last_error() { return g_err; }
 
 // ------------------------------------------------------------------ layout
+// Source chunk c goes to destination chunk c*cstride (cstride 2 interleaves
+// two matrices chunk by chunk).
 __global__ void pack_m_kernel(const int16_t *__restrict__ Wm, long long total, int nT,
-                              uint4 *__restrict__ Pm) {
+                              int cstride, uint4 *__restrict__ Pm) {
   long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
   if (i >= total) return;
   int r = (int)(i & 15), h = (int)((i >> 4) & 1);
   long long ct = i >> 5;
   long long c = ct / nT;
   int t = (int)(ct % nT);
-  Pm[i] = *reinterpret_cast<const uint4 *>(Wm + ((c * 16 + r) * nT + t) * 16 + h * 8);
+  Pm[((c * cstride) * nT + t) * 32 + h * 16 + r] =
+      *reinterpret_cast<const uint4 *>(Wm + ((c * 16 + r) * nT + t) * 16 + h * 8);
 }
 
 __global__ void pack_e_kernel(const int8_t *__restrict__ We, long long total, int nT,
-                              int8_t *__restrict__ Pe) {
+                              int cstride, int8_t *__restrict__ Pe) {
   long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
   if (i >= total) return;
   int r = (int)(i & 15);
   long long ct = i >> 4;
   long long c = ct / nT;
   int t = (int)(ct % nT);
-  Pe[i] = We[(c * 16 + r) * nT + t];
+  Pe[((c * cstride) * nT + t) * 16 + r] = We[(c * 16 + r) * nT + t];
 }
 
 __global__ void unpack_m_kernel(const uint4 *__restrict__ Pm, long long total, int nT,
@@ -116,7 +120,8 @@ __global__ void tile_quantize_kernel(const T *__restrict__ v, long long n_tiles,
 
 // quantize_W straight into the device layout: one thread per (row, tile).
 __global__ void quantize_pack_f32_kernel(const float *__restrict__ W, long long total, int nT,
-                                         uint4 *__restrict__ Pm, int8_t *__restrict__ Pe) {
+                                         int cstride, uint4 *__restrict__ Pm,
+                                         int8_t *__restrict__ Pe) {
   long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;  // row*nT + t
   if (i >= total) return;
   long long row = i / nT;
@@ -138,7 +143,7 @@ __global__ void quantize_pack_f32_kernel(const float *__restrict__ W, long long 
   int mm[TILE];
 #pragma unroll
   for (int k = 0; k < TILE; ++k) mm[k] = tile_mant_of(x[k], ex);
-  long long c = row >> 4;
+  long long c = (row >> 4) * cstride;
   int r = (int)(row & 15);
   long long base = ((c * nT + t) * 2) * 16 + r;
   uint4 lo, hi;
@@ -163,17 +168,9 @@ __global__ void tile_decode_kernel(const int16_t *__restrict__ m, const int8_t *
 }
 
 // ------------------------------------------------------------------ matvec
-// Exact integer matvec of one 16-row chunk per workgroup (NW waves).
-//
-// Lane (w, lane): row r = lane%16, tile lane tq = lane/16; it owns tiles
-// t = tq + 4*(w + NW*j), j < TPT.  Per tile the 16-term product sum is
-// exact: x is split as x = 256*xh + xl (xh in [-128,127], xl in [0,255]) so
-// both v_dot2 partial sums stay below 2^27 in int32, and
-// S = 256*sum(w*xh) + sum(w*xl) is formed in int64 (|S| <= 2^34).  Then
-// M = max_t(E) over the row, A = sum_t floor(S_t / 2^(M-E_t)) (dropped when
-// the shift exceeds 47), clip +-2^47, and the 16-row output tile is
-// quantised with the float-free epilogue: e = max_rows(msb|A| + M - 30) + 1,
-// m = rne(A * 2^(M - 15 - e)).  Equals full.py:217-233 bit for bit.
+// Standalone matvec: one 16-row chunk of one problem per workgroup (the
+// engine and its exactness argument are in bfp_mv.h).  Problem r reads
+// matrix (r mod ring) when ring > 0.
 template <int NW, int TPT>
 __global__ __launch_bounds__(64 * NW) void matvec_kernel(
     const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
@@ -181,127 +178,28 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
     const int8_t *__restrict__ xe, long long x_stride, int16_t *__restrict__ ym,
     int8_t *__restrict__ ye, long long y_stride) {
   extern __shared__ int smem[];
-  int *xs = smem;              // nT * 16: per tile 8 packed xh pairs, 8 packed xl pairs
-  int *xes = smem + nT * 16;   // nT exponents
+  int *xs = smem;              // nT * 16
+  int *xes = smem + nT * 16;   // nT
   __shared__ int redM[NW * 16];
   __shared__ long long redA[NW * 16];
 
   const int mat = blockIdx.x / n_chunks;
   const int c = blockIdx.x - mat * n_chunks;
   const int wmat = ring > 0 ? mat % ring : mat;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int r = lane & 15, tq = lane >> 4;
 
-  const uint4 *pm = Pm + wmat * smat_m + (long long)c * nT * 32;
-  const int8_t *pe = Pe + wmat * smat_e + (long long)c * nT * 16;
-
-  uint4 wa[TPT], wb[TPT];
-  int we[TPT];
-#pragma unroll
-  for (int j = 0; j < TPT; ++j) {
-    int t = tq + 4 * (w + NW * j);
-    if (t < nT) {
-      wa[j] = pm[t * 32 + r];
-      wb[j] = pm[t * 32 + 16 + r];
-      we[j] = pe[t * 16 + r];
-    } else {
-      wa[j] = make_uint4(0, 0, 0, 0);
-      wb[j] = make_uint4(0, 0, 0, 0);
-      we[j] = 0;
-    }
-  }
-
-  // Stage the (shared) input vector in LDS, split into high/low bytes.
-  const int *x32 = reinterpret_cast<const int *>(xm + mat * x_stride);
-  for (int p = tid; p < nT * 8; p += 64 * NW) {
-    int v = x32[p];
-    int lo = (int)(short)(v & 0xffff), hi = v >> 16;
-    int t = p >> 3, k = p & 7;
-    xs[t * 16 + k] = ((lo >> 8) & 0xffff) | ((hi >> 8) << 16);
-    xs[t * 16 + 8 + k] = (lo & 0xff) | ((hi & 0xff) << 16);
-  }
-  const int8_t *xep = xe + mat * (x_stride / 16);
-  for (int p = tid; p < nT; p += 64 * NW) xes[p] = xep[p];
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, Pm + wmat * smat_m + (long long)c * nT * 32,
+                      Pe + wmat * smat_e + (long long)c * nT * 16, nT);
+  stage_x_bfp(xs, xes, xm + mat * x_stride, xe + mat * (x_stride / 16), nT);
   __syncthreads();
-
-  typedef short s2 __attribute__((ext_vector_type(2)));
-#define DOT2(a, b, acc) \
-  __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, (a)), __builtin_bit_cast(s2, (b)), (acc), false)
-
-  long long S[TPT];
-  int E[TPT];
-  int M = -(1 << 29);
-#pragma unroll
-  for (int j = 0; j < TPT; ++j) {
-    int t = tq + 4 * (w + NW * j);
-    if (t < nT) {
-      const int4 *xp = reinterpret_cast<const int4 *>(xs + t * 16);
-      int4 h0 = xp[0], h1 = xp[1], l0 = xp[2], l1 = xp[3];
-      int ah = 0, al = 0;
-      ah = DOT2(wa[j].x, h0.x, ah);
-      al = DOT2(wa[j].x, l0.x, al);
-      ah = DOT2(wa[j].y, h0.y, ah);
-      al = DOT2(wa[j].y, l0.y, al);
-      ah = DOT2(wa[j].z, h0.z, ah);
-      al = DOT2(wa[j].z, l0.z, al);
-      ah = DOT2(wa[j].w, h0.w, ah);
-      al = DOT2(wa[j].w, l0.w, al);
-      ah = DOT2(wb[j].x, h1.x, ah);
-      al = DOT2(wb[j].x, l1.x, al);
-      ah = DOT2(wb[j].y, h1.y, ah);
-      al = DOT2(wb[j].y, l1.y, al);
-      ah = DOT2(wb[j].z, h1.z, ah);
-      al = DOT2(wb[j].z, l1.z, al);
-      ah = DOT2(wb[j].w, h1.w, ah);
-      al = DOT2(wb[j].w, l1.w, al);
-      S[j] = (long long)ah * 256 + al;
-      E[j] = xes[t] + we[j];
-      M = E[j] > M ? E[j] : M;
-    } else {
-      S[j] = 0;
-      E[j] = -(1 << 29);
-    }
-  }
-#undef DOT2
-
-  // Row max exponent over the row's lanes (tq = 0..3) and waves.
-  M = xor_max(M, 16);
-  M = xor_max(M, 32);
-  if (NW > 1) {
-    if (tq == 0) redM[w * 16 + r] = M;
-    __syncthreads();
-    M = redM[r];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) M = redM[i * 16 + r] > M ? redM[i * 16 + r] : M;
-  }
-
-  long long A = 0;
-#pragma unroll
-  for (int j = 0; j < TPT; ++j) {
-    int sh = M - E[j];
-    if (sh <= ALIGN_MAX) A += S[j] >> sh;
-  }
-  A = xor_sum(A, 16);
-  A = xor_sum(A, 32);
-  if (NW > 1) {
-    if (tq == 0) redA[w * 16 + r] = A;
-    __syncthreads();
-    if (w == 0) {
-      A = redA[r];
-#pragma unroll
-      for (int i = 1; i < NW; ++i) A += redA[i * 16 + r];
-    }
-  }
-  if (w == 0) {
-    A = A < SAT_LO ? SAT_LO : (A > SAT_HI ? SAT_HI : A);
-    int L = row_log2(A, M);
-    L = xor_max(L, 1);
-    L = xor_max(L, 2);
-    L = xor_max(L, 4);
-    L = xor_max(L, 8);
-    int e = chunk_exp_from_lmax(L);
-    int m = rne_shr_clip(A, e + 15 - M);
-    if (tq == 0) ym[mat * y_stride + c * 16 + r] = (int16_t)m;
+  long long A;
+  int M;
+  chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
+  if (threadIdx.x < 64) {
+    int m, e;
+    chunk_quant(A, M, m, e);
+    const int lane = threadIdx.x;
+    if (lane < 16) ym[mat * y_stride + c * 16 + lane] = (int16_t)m;
     if (lane == 0) ye[mat * (y_stride / 16) + c] = (int8_t)e;
   }
 }
@@ -387,25 +285,26 @@ int launch_status(const char *what) {
 }
 
 int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, void *P_e,
-         hipStream_t s) {
+         hipStream_t s, int cstride) {
   if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W_m || !W_e || !P_m || !P_e)
     return set_err(BFP_EINVAL, "pack: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
   int nT = n_in / 16;
   long long tm = (long long)(n_out / 16) * nT * 32, te = (long long)(n_out / 16) * nT * 16;
-  hipLaunchKernelGGL(pack_m_kernel, dim3(nblk(tm, 256)), dim3(256), 0, s, W_m, tm, nT,
+  hipLaunchKernelGGL(pack_m_kernel, dim3(nblk(tm, 256)), dim3(256), 0, s, W_m, tm, nT, cstride,
                      reinterpret_cast<uint4 *>(P_m));
-  hipLaunchKernelGGL(pack_e_kernel, dim3(nblk(te, 256)), dim3(256), 0, s, W_e, te, nT,
+  hipLaunchKernelGGL(pack_e_kernel, dim3(nblk(te, 256)), dim3(256), 0, s, W_e, te, nT, cstride,
                      reinterpret_cast<int8_t *>(P_e));
   return launch_status("pack");
 }
 
-int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s) {
+int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s,
+                      int cstride) {
   if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W || !P_m || !P_e)
     return set_err(BFP_EINVAL, "quantize_pack: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
   int nT = n_in / 16;
   long long total = (long long)n_out * nT;
   hipLaunchKernelGGL(quantize_pack_f32_kernel, dim3(nblk(total, 256)), dim3(256), 0, s, W, total,
-                     nT, reinterpret_cast<uint4 *>(P_m), reinterpret_cast<int8_t *>(P_e));
+                     nT, cstride, reinterpret_cast<uint4 *>(P_m), reinterpret_cast<int8_t *>(P_e));
   return launch_status("quantize_pack");
 }
 

@@ -1,0 +1,561 @@
+// Model context: HBM-resident BFP weights and KV cache, the layer step and the
+// autoregressive decode driver (rtl/vc707/host/gen_smollm_blockfp_full.py
+// :411-443), replayed step by step as HIP graphs.
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "bfp.h"
+#include "bfp_internal.h"
+#include "bfp_layer.h"
+
+using namespace bfp;
+
+struct bfp_ctx {
+  bfp_dims d{};
+  int device = 0, max_batch = 1, max_ctx = 0;
+  hipStream_t stream = nullptr;
+  // weights (device layout); per layer at base + layer * stride
+  uint8_t *qkv_m = nullptr, *o_m = nullptr, *gu_m = nullptr, *d_m = nullptr;
+  int8_t *qkv_e = nullptr, *o_e = nullptr, *gu_e = nullptr, *d_e = nullptr;
+  size_t s_qkv_m = 0, s_o_m = 0, s_gu_m = 0, s_d_m = 0;
+  size_t s_qkv_e = 0, s_o_e = 0, s_gu_e = 0, s_d_e = 0;
+  double *g1 = nullptr, *g2 = nullptr, *norm_w = nullptr, *rope = nullptr;
+  float *embed = nullptr;
+  // activations (max_batch sequences)
+  int16_t *h_m = nullptr, *h1_m = nullptr, *qkv_am = nullptr, *att_m = nullptr, *mlp_m = nullptr;
+  int8_t *h_e = nullptr, *h1_e = nullptr, *qkv_ae = nullptr, *att_e = nullptr, *mlp_e = nullptr;
+  // KV cache: NL x max_batch x max_ctx x KV
+  int16_t *k_m = nullptr, *v_m = nullptr;
+  int8_t *k_e = nullptr, *v_e = nullptr;
+  size_t s_kv_m = 0, s_kv_e = 0;   // per layer
+  // head / driver state
+  int head_wg = 0, head_rows = 0;
+  double *part_v = nullptr;
+  int *part_i = nullptr, *state = nullptr, *last = nullptr;
+  StageDump *dump_dev = nullptr;
+  std::vector<void *> allocs;
+  float last_decode_ms = 0.f, last_gen_ms = 0.f;
+
+  int alloc(void **p, size_t bytes) {
+    *p = nullptr;
+    hipError_t e = hipMalloc(p, bytes ? bytes : 16);
+    if (e != hipSuccess) {
+      *p = nullptr;
+      return set_err(BFP_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    allocs.push_back(*p);
+    return BFP_OK;
+  }
+  ~bfp_ctx() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void *p : allocs) (void)hipFree(p);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace {
+
+int check_dims(const bfp_dims &d) {
+  if (d.D <= 0 || d.H_Q <= 0 || d.H_KV <= 0 || d.HD <= 0 || d.FFN <= 0 || d.NL <= 0 ||
+      d.MAX_CTX <= 0 || d.VOCAB <= 0)
+    return set_err(BFP_EINVAL, "dims must be positive");
+  if (d.HD != 64) return set_err(BFP_EINVAL, "HD=%d: the attention kernel is built for HD=64", d.HD);
+  if (d.H_Q % d.H_KV) return set_err(BFP_EINVAL, "H_Q=%d not a multiple of H_KV=%d", d.H_Q, d.H_KV);
+  if (d.H_Q * d.HD != d.D) return set_err(BFP_EINVAL, "H_Q*HD=%d != D=%d", d.H_Q * d.HD, d.D);
+  if (d.D % 64 || d.D < 64 || d.D > 1728)
+    return set_err(BFP_EINVAL, "D=%d must be a multiple of 64 in [64, 1728]", d.D);
+  if (d.FFN % 16 || d.FFN < 64 || d.FFN > 1728)
+    return set_err(BFP_EINVAL, "FFN=%d must be a multiple of 16 in [64, 1728]", d.FFN);
+  if (d.VOCAB % 16) return set_err(BFP_EINVAL, "VOCAB=%d not a multiple of 16", d.VOCAB);
+  if (d.MAX_CTX > 4096) return set_err(BFP_EINVAL, "MAX_CTX=%d > 4096", d.MAX_CTX);
+  return BFP_OK;
+}
+
+// RoPE table with the reference's own float expressions (full.py:253-254):
+// theta = 1.0 / (base ** (2*j/HD)) * pos, evaluated by the host's libm as
+// CPython's float ** and math.cos/sin do (both call pow/cos/sin).
+void rope_table(std::vector<double> &t, int max_ctx, int HD) {
+  t.resize((size_t)max_ctx * HD);
+  const int h2 = HD / 2;
+  for (int pos = 0; pos < max_ctx; ++pos)
+    for (int j = 0; j < h2; ++j) {
+      double theta = 1.0 / pow(10000.0, (double)(2 * j) / (double)HD) * (double)pos;
+      t[((size_t)pos * h2 + j) * 2] = cos(theta);
+      t[((size_t)pos * h2 + j) * 2 + 1] = sin(theta);
+    }
+}
+
+LayerArgs layer_args(bfp_ctx *c, int layer, int batch) {
+  const bfp_dims &d = c->d;
+  LayerArgs a;
+  memset(&a, 0, sizeof a);
+  a.D = d.D;
+  a.H_Q = d.H_Q;
+  a.H_KV = d.H_KV;
+  a.HD = d.HD;
+  a.FFN = d.FFN;
+  a.KV = d.H_KV * d.HD;
+  a.max_ctx = c->max_ctx;
+  a.batch = batch;
+  a.inv_sqrt_hd_div = sqrt((double)d.HD);
+  a.w_qkv_m = reinterpret_cast<const uint4 *>(c->qkv_m + layer * c->s_qkv_m);
+  a.w_qkv_e = c->qkv_e + layer * c->s_qkv_e;
+  a.w_o_m = reinterpret_cast<const uint4 *>(c->o_m + layer * c->s_o_m);
+  a.w_o_e = c->o_e + layer * c->s_o_e;
+  a.w_gu_m = reinterpret_cast<const uint4 *>(c->gu_m + layer * c->s_gu_m);
+  a.w_gu_e = c->gu_e + layer * c->s_gu_e;
+  a.w_d_m = reinterpret_cast<const uint4 *>(c->d_m + layer * c->s_d_m);
+  a.w_d_e = c->d_e + layer * c->s_d_e;
+  a.g1 = c->g1 + (size_t)layer * d.D;
+  a.g2 = c->g2 + (size_t)layer * d.D;
+  a.rope = c->rope;
+  a.h_m = c->h_m;
+  a.h_e = c->h_e;
+  a.h1_m = c->h1_m;
+  a.h1_e = c->h1_e;
+  a.qkv_m = c->qkv_am;
+  a.qkv_e = c->qkv_ae;
+  a.att_m = c->att_m;
+  a.att_e = c->att_e;
+  a.mlp_m = c->mlp_m;
+  a.mlp_e = c->mlp_e;
+  a.k_m = c->k_m + layer * c->s_kv_m;
+  a.k_e = c->k_e + layer * c->s_kv_e;
+  a.v_m = c->v_m + layer * c->s_kv_m;
+  a.v_e = c->v_e + layer * c->s_kv_e;
+  a.layer = layer;
+  a.NL = d.NL;
+  return a;
+}
+
+void stage_lens(const bfp_dims &d, int len[ST_COUNT]) {
+  const int KV = d.H_KV * d.HD;
+  const int L[ST_COUNT] = {d.D, d.D, KV, KV, d.D, d.D, d.D, d.D, d.FFN, d.FFN, d.FFN, d.D, d.D};
+  for (int i = 0; i < ST_COUNT; ++i) len[i] = L[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
+  if (!dims) {
+    set_err(BFP_EINVAL, "null dims");
+    return nullptr;
+  }
+  if (check_dims(*dims)) return nullptr;
+  if (max_batch <= 0 || max_batch > 1024) {
+    set_err(BFP_EINVAL, "max_batch=%d out of range", max_batch);
+    return nullptr;
+  }
+  if (hipSetDevice(device) != hipSuccess) {
+    set_err(BFP_EIO, "hipSetDevice(%d) failed", device);
+    return nullptr;
+  }
+  bfp_ctx *c = new bfp_ctx();
+  c->d = *dims;
+  c->device = device;
+  c->max_batch = max_batch;
+  c->max_ctx = dims->MAX_CTX;
+  const bfp_dims &d = c->d;
+  const int KV = d.H_KV * d.HD;
+  const size_t nq = (size_t)d.D + 2 * KV;
+  c->s_qkv_m = nq * d.D * 2;
+  c->s_qkv_e = nq * d.D / 16;
+  c->s_o_m = (size_t)d.D * d.D * 2;
+  c->s_o_e = (size_t)d.D * d.D / 16;
+  c->s_gu_m = (size_t)2 * d.FFN * d.D * 2;
+  c->s_gu_e = (size_t)2 * d.FFN * d.D / 16;
+  c->s_d_m = (size_t)d.D * d.FFN * 2;
+  c->s_d_e = (size_t)d.D * d.FFN / 16;
+  c->s_kv_m = (size_t)max_batch * c->max_ctx * KV;
+  c->s_kv_e = c->s_kv_m / 16;
+  c->head_rows = (d.VOCAB % 64 == 0) ? 64 : 16;
+  c->head_wg = d.VOCAB / c->head_rows;
+  const size_t B = max_batch;
+  int rc = 0;
+  std::vector<double> rope;
+  rope_table(rope, c->max_ctx, d.HD);
+  if ((rc = hipStreamCreate(&c->stream)) != hipSuccess) {
+    set_err(BFP_EIO, "hipStreamCreate failed");
+    delete c;
+    return nullptr;
+  }
+  if ((rc = c->alloc((void **)&c->qkv_m, c->s_qkv_m * d.NL)) ||
+      (rc = c->alloc((void **)&c->qkv_e, c->s_qkv_e * d.NL)) ||
+      (rc = c->alloc((void **)&c->o_m, c->s_o_m * d.NL)) ||
+      (rc = c->alloc((void **)&c->o_e, c->s_o_e * d.NL)) ||
+      (rc = c->alloc((void **)&c->gu_m, c->s_gu_m * d.NL)) ||
+      (rc = c->alloc((void **)&c->gu_e, c->s_gu_e * d.NL)) ||
+      (rc = c->alloc((void **)&c->d_m, c->s_d_m * d.NL)) ||
+      (rc = c->alloc((void **)&c->d_e, c->s_d_e * d.NL)) ||
+      (rc = c->alloc((void **)&c->g1, sizeof(double) * d.D * d.NL)) ||
+      (rc = c->alloc((void **)&c->g2, sizeof(double) * d.D * d.NL)) ||
+      (rc = c->alloc((void **)&c->norm_w, sizeof(double) * d.D)) ||
+      (rc = c->alloc((void **)&c->rope, sizeof(double) * rope.size())) ||
+      (rc = c->alloc((void **)&c->embed, sizeof(float) * (size_t)d.VOCAB * d.D)) ||
+      (rc = c->alloc((void **)&c->h_m, 2 * B * d.D)) || (rc = c->alloc((void **)&c->h_e, B * d.D / 16)) ||
+      (rc = c->alloc((void **)&c->h1_m, 2 * B * d.D)) ||
+      (rc = c->alloc((void **)&c->h1_e, B * d.D / 16)) ||
+      (rc = c->alloc((void **)&c->qkv_am, 2 * B * nq)) ||
+      (rc = c->alloc((void **)&c->qkv_ae, B * nq / 16)) ||
+      (rc = c->alloc((void **)&c->att_m, 2 * B * d.D)) ||
+      (rc = c->alloc((void **)&c->att_e, B * d.D / 16)) ||
+      (rc = c->alloc((void **)&c->mlp_m, 2 * B * d.FFN)) ||
+      (rc = c->alloc((void **)&c->mlp_e, B * d.FFN / 16)) ||
+      (rc = c->alloc((void **)&c->k_m, 2 * c->s_kv_m * d.NL)) ||
+      (rc = c->alloc((void **)&c->k_e, c->s_kv_e * d.NL)) ||
+      (rc = c->alloc((void **)&c->v_m, 2 * c->s_kv_m * d.NL)) ||
+      (rc = c->alloc((void **)&c->v_e, c->s_kv_e * d.NL)) ||
+      (rc = c->alloc((void **)&c->part_v, sizeof(double) * B * c->head_wg)) ||
+      (rc = c->alloc((void **)&c->part_i, sizeof(int) * B * c->head_wg)) ||
+      (rc = c->alloc((void **)&c->state, sizeof(int) * (B + 1))) ||
+      (rc = c->alloc((void **)&c->last, sizeof(int) * B)) ||
+      (rc = c->alloc((void **)&c->dump_dev, sizeof(StageDump)))) {
+    delete c;
+    return nullptr;
+  }
+  // s_kv_m counts elements; the mantissa arrays are int16
+  if (hipMemcpy(c->rope, rope.data(), sizeof(double) * rope.size(), hipMemcpyHostToDevice) !=
+          hipSuccess ||
+      hipMemset(c->k_m, 0, 2 * c->s_kv_m * d.NL) != hipSuccess ||
+      hipMemset(c->v_m, 0, 2 * c->s_kv_m * d.NL) != hipSuccess ||
+      hipMemset(c->k_e, 0, c->s_kv_e * d.NL) != hipSuccess ||
+      hipMemset(c->v_e, 0, c->s_kv_e * d.NL) != hipSuccess) {
+    set_err(BFP_EIO, "context initialisation copy failed");
+    delete c;
+    return nullptr;
+  }
+  return c;
+}
+
+void bfp_destroy(bfp_ctx *c) { delete c; }
+
+int bfp_get_dims(const bfp_ctx *c, bfp_dims *out) {
+  if (!c || !out) return set_err(BFP_EINVAL, "null argument");
+  *out = c->d;
+  return BFP_OK;
+}
+
+// Load one weight tensor.  Matrices: from float32 (quantize_W on the device,
+// full.py:110-119) or from the reference layout (m, e).  Gammas / final norm
+// weight: float32 (quantised to BFP-exact float64 as fp_quantize_vec does,
+// full.py:322-323,413) or (m, e).  The embedding must be float32: the head
+// uses the raw table (full.py:439).
+int bfp_load_weights(bfp_ctx *c, int which, int layer, const float *fp32, const int16_t *m,
+                     const int8_t *e) {
+  if (!c) return set_err(BFP_EINVAL, "null context");
+  const bfp_dims &d = c->d;
+  const int KV = d.H_KV * d.HD;
+  if (which != BFP_EMBED && which != BFP_NORM_W && (layer < 0 || layer >= d.NL))
+    return set_err(BFP_EINVAL, "layer %d out of range [0, %d)", layer, d.NL);
+  if (!fp32 && (!m || !e)) return set_err(BFP_EINVAL, "need fp32 or (m, e)");
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  int n_out = 0, n_in = d.D, cstride = 1;
+  uint8_t *Pm = nullptr;
+  int8_t *Pe = nullptr;
+  switch (which) {
+    case BFP_WQ: case BFP_WK: case BFP_WV: {
+      int row0 = which == BFP_WQ ? 0 : (which == BFP_WK ? d.D : d.D + KV);
+      n_out = which == BFP_WQ ? d.D : KV;
+      Pm = c->qkv_m + layer * c->s_qkv_m + (size_t)row0 * d.D * 2;
+      Pe = c->qkv_e + layer * c->s_qkv_e + (size_t)row0 * d.D / 16;
+      break;
+    }
+    case BFP_WO:
+      n_out = d.D;
+      Pm = c->o_m + layer * c->s_o_m;
+      Pe = c->o_e + layer * c->s_o_e;
+      break;
+    case BFP_WG: case BFP_WU: {
+      n_out = d.FFN;
+      cstride = 2;
+      size_t off = which == BFP_WG ? 0 : 1;   // chunks interleaved G0 U0 G1 U1 ...
+      Pm = c->gu_m + layer * c->s_gu_m + off * (size_t)16 * d.D * 2;
+      Pe = c->gu_e + layer * c->s_gu_e + off * (size_t)16 * d.D / 16;
+      break;
+    }
+    case BFP_WD:
+      n_out = d.D;
+      n_in = d.FFN;
+      Pm = c->d_m + layer * c->s_d_m;
+      Pe = c->d_e + layer * c->s_d_e;
+      break;
+    case BFP_G1: case BFP_G2: case BFP_NORM_W: {
+      double *dst = which == BFP_NORM_W ? c->norm_w
+                                        : (which == BFP_G1 ? c->g1 : c->g2) + (size_t)layer * d.D;
+      DevBuf tmp;
+      int16_t *qm;
+      int8_t *qe;
+      BFP_TRY(tmp.alloc((void **)&qm, (size_t)d.D * 2));
+      BFP_TRY(tmp.alloc((void **)&qe, (size_t)d.D / 16));
+      if (fp32) {
+        float *f;
+        BFP_TRY(tmp.alloc((void **)&f, (size_t)d.D * 4));
+        HIP_TRY(hipMemcpyAsync(f, fp32, (size_t)d.D * 4, hipMemcpyHostToDevice, s));
+        BFP_TRY(bfp_tile_quantize_f32_d(f, d.D, qm, qe, s));
+      } else {
+        HIP_TRY(hipMemcpyAsync(qm, m, (size_t)d.D * 2, hipMemcpyHostToDevice, s));
+        HIP_TRY(hipMemcpyAsync(qe, e, (size_t)d.D / 16, hipMemcpyHostToDevice, s));
+      }
+      BFP_TRY(bfp_tile_decode_d(qm, qe, d.D, dst, s));
+      HIP_TRY(hipStreamSynchronize(s));
+      return BFP_OK;
+    }
+    case BFP_EMBED: {
+      if (!fp32) return set_err(BFP_EINVAL, "the embedding must be given as float32");
+      HIP_TRY(hipMemcpy(c->embed, fp32, sizeof(float) * (size_t)d.VOCAB * d.D,
+                        hipMemcpyHostToDevice));
+      return BFP_OK;
+    }
+    default:
+      return set_err(BFP_EINVAL, "unknown weight slot %d", which);
+  }
+  DevBuf tmp;
+  if (fp32) {
+    float *f;
+    size_t bytes = (size_t)n_out * n_in * 4;
+    BFP_TRY(tmp.alloc((void **)&f, bytes));
+    HIP_TRY(hipMemcpyAsync(f, fp32, bytes, hipMemcpyHostToDevice, s));
+    BFP_TRY(quantize_pack_f32(f, n_out, n_in, Pm, Pe, s, cstride));
+  } else {
+    int16_t *dm;
+    int8_t *de;
+    size_t bm = (size_t)n_out * n_in * 2, be = (size_t)n_out * n_in / 16;
+    BFP_TRY(tmp.alloc((void **)&dm, bm));
+    BFP_TRY(tmp.alloc((void **)&de, be));
+    HIP_TRY(hipMemcpyAsync(dm, m, bm, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(de, e, be, hipMemcpyHostToDevice, s));
+    BFP_TRY(pack(dm, de, n_out, n_in, Pm, Pe, s, cstride));
+  }
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+int bfp_reset_kv(bfp_ctx *c) {
+  if (!c) return set_err(BFP_EINVAL, "null context");
+  const bfp_dims &d = c->d;
+  HIP_TRY(hipMemsetAsync(c->k_m, 0, 2 * c->s_kv_m * d.NL, c->stream));
+  HIP_TRY(hipMemsetAsync(c->v_m, 0, 2 * c->s_kv_m * d.NL, c->stream));
+  HIP_TRY(hipMemsetAsync(c->k_e, 0, c->s_kv_e * d.NL, c->stream));
+  HIP_TRY(hipMemsetAsync(c->v_e, 0, c->s_kv_e * d.NL, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return BFP_OK;
+}
+
+// fwd_layer (full.py:261-293) for `batch` sequences at position pos
+// (kv_pos = pos).  h in/out are host arrays (batch x D mantissas, batch x
+// D/16 exponents); dump (optional) receives every stage.
+int bfp_layer_step(bfp_ctx *c, int layer, int pos, int batch, const int16_t *h_m,
+                   const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump) {
+  if (!c || !h_m || !h_e || !out_m || !out_e) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  if (layer < 0 || layer >= d.NL) return set_err(BFP_EINVAL, "layer %d out of range", layer);
+  if (batch <= 0 || batch > c->max_batch) return set_err(BFP_EINVAL, "batch %d out of range", batch);
+  if (pos < 0 || pos >= c->max_ctx)
+    return set_err(BFP_ERANGE, "pos %d outside the KV capacity %d", pos, c->max_ctx);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)batch * d.D * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)batch * d.D / 16, hipMemcpyHostToDevice, s));
+  LayerArgs a = layer_args(c, layer, batch);
+  a.pos_const = pos;
+  DevBuf tmp;
+  StageDump sd;
+  int len[ST_COUNT];
+  stage_lens(d, len);
+  if (dump) {
+    for (int i = 0; i < ST_COUNT; ++i) {
+      BFP_TRY(tmp.alloc((void **)&sd.m[i], (size_t)batch * len[i] * 2));
+      BFP_TRY(tmp.alloc((void **)&sd.e[i], (size_t)batch * len[i] / 16));
+      sd.mstride[i] = len[i];
+    }
+    HIP_TRY(hipMemcpyAsync(c->dump_dev, &sd, sizeof sd, hipMemcpyHostToDevice, s));
+    a.dump = c->dump_dev;
+  }
+  BFP_TRY(launch_layer(a, s));
+  HIP_TRY(hipMemcpyAsync(out_m, c->h_m, (size_t)batch * d.D * 2, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(out_e, c->h_e, (size_t)batch * d.D / 16, hipMemcpyDeviceToHost, s));
+  if (dump) {
+    for (int i = 0; i < ST_COUNT; ++i) {
+      if (dump->m[i])
+        HIP_TRY(hipMemcpyAsync(dump->m[i], sd.m[i], (size_t)batch * len[i] * 2,
+                               hipMemcpyDeviceToHost, s));
+      if (dump->e[i])
+        HIP_TRY(hipMemcpyAsync(dump->e[i], sd.e[i], (size_t)batch * len[i] / 16,
+                               hipMemcpyDeviceToHost, s));
+    }
+  }
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+// Final norm + float64 logits + first-index argmax for `batch` hidden states
+// (full.py:438-440).  logits (optional): batch x VOCAB.
+int bfp_head(bfp_ctx *c, int batch, const int16_t *h_m, const int8_t *h_e, double *logits,
+             int32_t *argmax) {
+  if (!c || !h_m || !h_e || !argmax) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  if (batch <= 0 || batch > c->max_batch) return set_err(BFP_EINVAL, "batch %d out of range", batch);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  DevBuf tmp;
+  double *dl = nullptr;
+  if (logits) BFP_TRY(tmp.alloc((void **)&dl, sizeof(double) * batch * d.VOCAB));
+  HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)batch * d.D * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)batch * d.D / 16, hipMemcpyHostToDevice, s));
+  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, c->head_wg, c->h_m, c->h_e, c->norm_w,
+              c->embed, c->part_v, c->part_i, dl};
+  BFP_TRY(launch_head(ha, s));
+  // reuse the controller's reduction with an empty prompt schedule
+  std::vector<int> st(batch + 1, 0);
+  st[0] = 1 << 30;   // step beyond any prompt: no token bookkeeping
+  HIP_TRY(hipMemcpyAsync(c->state, st.data(), sizeof(int) * (batch + 1), hipMemcpyHostToDevice, s));
+  int *dprompt, *dout;
+  BFP_TRY(tmp.alloc((void **)&dprompt, sizeof(int) * batch));
+  BFP_TRY(tmp.alloc((void **)&dout, sizeof(int) * batch));
+  CtlArgs ca{batch, 1, 0, c->head_wg, 1, c->state, dprompt, dout, c->part_v, c->part_i, c->last};
+  BFP_TRY(launch_ctl(ca, s));
+  HIP_TRY(hipMemcpyAsync(argmax, c->last, sizeof(int) * batch, hipMemcpyDeviceToHost, s));
+  if (logits)
+    HIP_TRY(hipMemcpyAsync(logits, dl, sizeof(double) * batch * d.VOCAB, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+// The golden-token loop of full.py:426-443 for `batch` independent
+// sequences (prompt: batch x n_prompt, tokens_out: batch x n_gen).  All
+// steps run on the device: each step is embed -> NL layers -> (head from
+// step n_prompt-1 on) -> controller, captured once as a HIP graph and
+// replayed (flags & BFP_DECODE_NO_GRAPH launches the kernels directly).
+// hist_m/hist_e (optional): every layer's h_out at every step, laid out
+// (batch, n_prompt + n_gen, NL, D) and (..., D/16).
+int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int batch,
+               int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags) {
+  if (!c || !prompt || (!tokens_out && n_gen > 0)) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  if (n_prompt < 1 || n_gen < 0) return set_err(BFP_EINVAL, "n_prompt=%d n_gen=%d", n_prompt, n_gen);
+  if (batch <= 0 || batch > c->max_batch) return set_err(BFP_EINVAL, "batch %d out of range", batch);
+  const int steps = n_prompt + n_gen;
+  if (steps > c->max_ctx)
+    return set_err(BFP_ERANGE, "n_prompt + n_gen = %d exceeds the KV capacity %d", steps,
+                   c->max_ctx);
+  for (int i = 0; i < batch * n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= d.VOCAB)
+      return set_err(BFP_EINVAL, "prompt token %d out of range [0, %d)", prompt[i], d.VOCAB);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  DevBuf tmp;
+  int *dprompt, *dout;
+  BFP_TRY(tmp.alloc((void **)&dprompt, sizeof(int) * batch * n_prompt));
+  BFP_TRY(tmp.alloc((void **)&dout, sizeof(int) * batch * (n_gen > 0 ? n_gen : 1)));
+  int16_t *dhm = nullptr;
+  int8_t *dhe = nullptr;
+  if (hist_m && hist_e) {
+    BFP_TRY(tmp.alloc((void **)&dhm, (size_t)batch * steps * d.NL * d.D * 2));
+    BFP_TRY(tmp.alloc((void **)&dhe, (size_t)batch * steps * d.NL * d.D / 16));
+  }
+  HIP_TRY(hipMemcpyAsync(dprompt, prompt, sizeof(int) * batch * n_prompt, hipMemcpyHostToDevice, s));
+  std::vector<int> st(batch + 1);
+  st[0] = 0;
+  for (int b = 0; b < batch; ++b) st[1 + b] = prompt[b * n_prompt];
+  HIP_TRY(hipMemcpyAsync(c->state, st.data(), sizeof(int) * (batch + 1), hipMemcpyHostToDevice, s));
+
+  EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
+  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, c->head_wg, c->h_m, c->h_e, c->norm_w,
+              c->embed, c->part_v, c->part_i, nullptr};
+  CtlArgs ca{batch, n_prompt, n_gen, c->head_wg, 0, c->state, dprompt, dout, c->part_v,
+             c->part_i, c->last};
+  auto enqueue_step = [&](bool head) -> int {
+    BFP_TRY(launch_embed(ea, s));
+    for (int l = 0; l < d.NL; ++l) {
+      LayerArgs a = layer_args(c, l, batch);
+      a.pos_ptr = c->state;
+      a.hist_m = dhm;
+      a.hist_e = dhe;
+      a.hist_steps = steps;
+      BFP_TRY(launch_layer(a, s));
+    }
+    CtlArgs cc = ca;
+    cc.head = head ? 1 : 0;
+    if (head) BFP_TRY(launch_head(ha, s));
+    BFP_TRY(launch_ctl(cc, s));
+    return BFP_OK;
+  };
+  const bool use_graph = !(flags & BFP_DECODE_NO_GRAPH);
+  hipGraphExec_t ex[2] = {nullptr, nullptr};
+  hipGraph_t gr[2] = {nullptr, nullptr};
+  int rc = BFP_OK;
+  if (use_graph) {
+    for (int k = 0; k < 2 && !rc; ++k) {
+      HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      rc = enqueue_step(k == 1);
+      hipError_t e1 = hipStreamEndCapture(s, &gr[k]);
+      if (!rc && e1 != hipSuccess) rc = set_err(BFP_EIO, "graph capture: %s", hipGetErrorString(e1));
+      if (!rc) {
+        hipError_t e2 = hipGraphInstantiate(&ex[k], gr[k], nullptr, nullptr, 0);
+        if (e2 != hipSuccess) rc = set_err(BFP_EIO, "graph instantiate: %s", hipGetErrorString(e2));
+      }
+    }
+  }
+  hipEvent_t ev0 = nullptr, ev1 = nullptr, evg = nullptr;
+  if (!rc) {
+    (void)hipEventCreate(&ev0);
+    (void)hipEventCreate(&ev1);
+    (void)hipEventCreate(&evg);
+    (void)hipEventRecord(ev0, s);
+    for (int step = 0; step < steps && !rc; ++step) {
+      const bool head = step >= n_prompt - 1;
+      if (step == n_prompt) (void)hipEventRecord(evg, s);
+      if (use_graph) {
+        hipError_t e = hipGraphLaunch(ex[head ? 1 : 0], s);
+        if (e != hipSuccess) rc = set_err(BFP_EIO, "graph launch: %s", hipGetErrorString(e));
+      } else {
+        rc = enqueue_step(head);
+      }
+    }
+    if (n_gen == 0) (void)hipEventRecord(evg, s);
+    (void)hipEventRecord(ev1, s);
+  }
+  if (!rc) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = set_err(BFP_EIO, "decode: %s", hipGetErrorString(e));
+  }
+  if (!rc) {
+    float ms = 0.f, gms = 0.f;
+    (void)hipEventElapsedTime(&ms, ev0, ev1);
+    (void)hipEventElapsedTime(&gms, evg, ev1);
+    c->last_decode_ms = ms;
+    c->last_gen_ms = gms;
+  }
+  for (int k = 0; k < 2; ++k) {
+    if (ex[k]) (void)hipGraphExecDestroy(ex[k]);
+    if (gr[k]) (void)hipGraphDestroy(gr[k]);
+  }
+  if (ev0) (void)hipEventDestroy(ev0);
+  if (ev1) (void)hipEventDestroy(ev1);
+  if (evg) (void)hipEventDestroy(evg);
+  if (rc) return rc;
+  if (n_gen > 0)
+    HIP_TRY(hipMemcpy(tokens_out, dout, sizeof(int) * batch * n_gen, hipMemcpyDeviceToHost));
+  if (dhm) {
+    HIP_TRY(hipMemcpy(hist_m, dhm, (size_t)batch * steps * d.NL * d.D * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(hist_e, dhe, (size_t)batch * steps * d.NL * d.D / 16, hipMemcpyDeviceToHost));
+  }
+  return BFP_OK;
+}
+
+// Device time of the last bfp_decode: all steps, and the steps from
+// n_prompt on (the generated tokens).
+int bfp_decode_time(const bfp_ctx *c, float *total_ms, float *gen_ms) {
+  if (!c || !total_ms || !gen_ms) return set_err(BFP_EINVAL, "null argument");
+  *total_ms = c->last_decode_ms;
+  *gen_ms = c->last_gen_ms;
+  return BFP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,142 @@
+// float64 building blocks of the model-level simulator's leaf ops, in the
+// reduction orders numpy/OpenBLAS use (rtl/vc707/host/gen_smollm_blockfp_full.py
+// :236-258,274-281).  Compiled with -ffp-contract=off: each + and * rounds.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "bfp_device.h"
+
+namespace bfp {
+
+// ---------------------------------------------------------------- pairwise
+// numpy's float64 add-reduce of one contiguous block (n <= 8192): blocks of
+// <= 128 are summed with 8 accumulators, longer ranges split at
+// n2 = n/2 rounded down to a multiple of 8.  Leaves are numbered in
+// left-to-right order.
+__device__ inline double pw_leaf_sum(const double *a, int n) {
+  if (n < 8) {
+    double r = 0.0;
+    for (int i = 0; i < n; ++i) r += a[i];
+    return r;
+  }
+  double r0 = a[0], r1 = a[1], r2 = a[2], r3 = a[3], r4 = a[4], r5 = a[5], r6 = a[6], r7 = a[7];
+  int i = 8;
+  const int top = n - (n % 8);
+  for (; i < top; i += 8) {
+    r0 += a[i];
+    r1 += a[i + 1];
+    r2 += a[i + 2];
+    r3 += a[i + 3];
+    r4 += a[i + 4];
+    r5 += a[i + 5];
+    r6 += a[i + 6];
+    r7 += a[i + 7];
+  }
+  double res = ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7));
+  for (; i < n; ++i) res += a[i];
+  return res;
+}
+
+template <int DEPTH>
+__device__ inline void pw_find_leaf(int lo, int n, int want, int &k, int &flo, int &fn) {
+  if constexpr (DEPTH > 0) {
+    if (n > 128) {
+      int n2 = n / 2;
+      n2 -= n2 % 8;
+      pw_find_leaf<DEPTH - 1>(lo, n2, want, k, flo, fn);
+      pw_find_leaf<DEPTH - 1>(lo + n2, n - n2, want, k, flo, fn);
+      return;
+    }
+  }
+  if (k == want) {
+    flo = lo;
+    fn = n;
+  }
+  ++k;
+}
+
+template <int DEPTH>
+__device__ inline double pw_combine(int n, const double *leaf, int &k) {
+  if constexpr (DEPTH > 0) {
+    if (n > 128) {
+      int n2 = n / 2;
+      n2 -= n2 % 8;
+      double l = pw_combine<DEPTH - 1>(n2, leaf, k);
+      double r = pw_combine<DEPTH - 1>(n - n2, leaf, k);
+      return l + r;
+    }
+  }
+  return leaf[k++];
+}
+
+constexpr int PW_DEPTH = 6;        // n <= 128 * 2^6 = 8192
+constexpr int PW_MAX_LEAVES = 64;  // n <= 8192 has at most 64 leaves of >= 128 ... (>= 64 elements)
+
+// Sum of a[0..n) (a in LDS) in numpy order, plus numpy's initial 0.0.
+// Called by all threads of a workgroup (uses __syncthreads); leafbuf holds
+// PW_MAX_LEAVES doubles of LDS.  Returns the sum in every thread.
+__device__ inline double pairwise_sum_block(const double *a, int n, double *leafbuf) {
+  int k = 0, flo = 0, fn = 0;
+  const int t = threadIdx.x;
+  if (t < PW_MAX_LEAVES) {
+    pw_find_leaf<PW_DEPTH>(0, n, t, k, flo, fn);
+    if (t < k) leafbuf[t] = pw_leaf_sum(a + flo, fn);
+  }
+  __syncthreads();
+  int kk = 0;
+  double s = 0.0 + pw_combine<PW_DEPTH>(n, leafbuf, kk);
+  __syncthreads();
+  return s;
+}
+
+// ------------------------------------------------------------------ ddot
+// OpenBLAS 0.3.29 x86_64 ddot, SkylakeX micro-kernel, n = 64: four 8-lane
+// FMA accumulators over two blocks of 32, each folded 512->256 bit (lane l +
+// lane l+4), summed ((a0+a1)+a2)+a3, then 128-bit halves and a horizontal
+// add.  This is np.dot's order on SkylakeX/SapphireRapids hosts.
+__device__ inline double ddot64_skx(const double *x, const double *y) {
+  double acc[4][8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[r][l] = fma(x[8 * r + l], y[8 * r + l], 0.0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[r][l] = fma(x[32 + 8 * r + l], y[32 + 8 * r + l], acc[r][l]);
+  double s[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    double f0 = acc[0][l] + acc[0][l + 4];
+    double f1 = acc[1][l] + acc[1][l + 4];
+    double f2 = acc[2][l] + acc[2][l + 4];
+    double f3 = acc[3][l] + acc[3][l + 4];
+    s[l] = ((f0 + f1) + f2) + f3;
+  }
+  return (s[0] + s[2]) + (s[1] + s[3]);
+}
+
+// --------------------------------------------------------------- exp
+// np.exp is numpy's own SIMD exp (not correctly rounded for ~5% of inputs);
+// the device uses the ROCm device library's exp.  The two may differ in the
+// last bit; that reaches a BFP mantissa only at a rounding tie of the 16-bit
+// re-quantisation (about 2^-36 per element).
+__device__ __forceinline__ double exp_f64(double x) { return exp(x); }
+
+// -------------------------------------------------------- tile quantise
+// Quantise the 16 values held by lanes (lane & ~15) .. (lane | 15) of a
+// wave (one value per lane): returns this lane's mantissa and sets e to the
+// tile exponent.  All 64 lanes must participate.
+__device__ __forceinline__ int quantize16_lanes(double v, int &e) {
+  double a = fabs(v);
+  a = xor_max(a, 1);
+  a = xor_max(a, 2);
+  a = xor_max(a, 4);
+  a = xor_max(a, 8);
+  e = tile_exp_of(a);
+  return tile_mant_of(v, e);
+}
+
+__device__ __forceinline__ double bfp_val(int m, int e) { return ldexp((double)m, e - 15); }
+
+}  // namespace bfp

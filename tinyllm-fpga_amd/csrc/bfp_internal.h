@@ -53,8 +53,20 @@ int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_m
                   long long x_stride, int16_t *y_m, int8_t *y_e, long long y_stride, int waves,
                   hipStream_t stream);
 int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, void *P_e,
-         hipStream_t s);
-int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s);
+         hipStream_t s, int cstride = 1);
+int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s,
+                      int cstride = 1);
 int tile_quantize_f64(const double *v, size_t n, int16_t *m, int8_t *e, hipStream_t s);
 
+}  // namespace bfp
+
+namespace bfp {
+struct LayerArgs;
+struct HeadArgs;
+struct CtlArgs;
+struct EmbedArgs;
+int launch_layer(const LayerArgs &a, hipStream_t s);
+int launch_embed(const EmbedArgs &a, hipStream_t s);
+int launch_head(const HeadArgs &a, hipStream_t s);
+int launch_ctl(const CtlArgs &a, hipStream_t s);
 }  // namespace bfp

@@ -1,0 +1,77 @@
+// Device-side argument blocks of the fused decoder-layer and head kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bfp {
+
+enum Stage { ST_N1 = 0, ST_Q, ST_K, ST_V, ST_ATTN, ST_O, ST_H1, ST_N2, ST_G, ST_U, ST_MLP, ST_D,
+             ST_HOUT, ST_COUNT };
+
+// Per-sequence stage dump (BFP m/e of every intermediate of one layer
+// step, named as gen_smollm_blockfp_bfp.py:398-409 dumps them).  Sequence b
+// writes stage s at m[s] + b*mstride[s], e[s] + b*(mstride[s]/16).
+struct StageDump {
+  int16_t *m[ST_COUNT];
+  int8_t *e[ST_COUNT];
+  int mstride[ST_COUNT];
+};
+
+struct LayerArgs {
+  int D, H_Q, H_KV, HD, FFN, KV, max_ctx, batch;
+  double inv_sqrt_hd_div;   // math.sqrt(HD), the divisor of the scores
+  // weights of this layer, device layout
+  const uint4 *w_qkv_m;     // (D + 2KV) x D   rows: q | k | v
+  const int8_t *w_qkv_e;
+  const uint4 *w_o_m;       // D x D
+  const int8_t *w_o_e;
+  const uint4 *w_gu_m;      // 2FFN x D, chunks interleaved G0 U0 G1 U1 ...
+  const int8_t *w_gu_e;
+  const uint4 *w_d_m;       // D x FFN
+  const int8_t *w_d_e;
+  const double *g1, *g2;    // (D,) BFP-exact gammas
+  const double *rope;       // (max_ctx, HD/2, 2): cos, sin of theta_j(pos)
+  // activations, sequence b at base + b*len (m) and base + b*len/16 (e)
+  int16_t *h_m;   int8_t *h_e;     // D, layer input and output
+  int16_t *h1_m;  int8_t *h1_e;    // D
+  int16_t *qkv_m; int8_t *qkv_e;   // D + 2KV, pre-rope
+  int16_t *att_m; int8_t *att_e;   // D
+  int16_t *mlp_m; int8_t *mlp_e;   // FFN
+  // this layer's KV cache: sequence b, position t, kv head g at
+  // ((b*max_ctx + t)*H_KV + g)*HD mantissas and /16 exponents
+  int16_t *k_m; int8_t *k_e;
+  int16_t *v_m; int8_t *v_e;
+  const int *pos_ptr;       // device position (== kv_pos); read when non-null
+  int pos_const;
+  const StageDump *dump;    // device pointer or null
+  // h_out history for per-(step, layer) checks: ((b*hist_steps + pos)*NL + layer)*D
+  int16_t *hist_m; int8_t *hist_e;
+  int hist_steps, layer, NL;
+};
+
+struct HeadArgs {
+  int D, VOCAB, batch, rows_per_wg, n_wg;
+  const int16_t *h_m; const int8_t *h_e;   // final hidden (BFP)
+  const double *norm_w;                    // (D,) quantised final norm weight
+  const float *embed;                      // (VOCAB, D) raw float32 (exact in f64)
+  double *part_v; int *part_i;             // (batch, n_wg) per-workgroup argmax
+  double *logits;                          // optional (batch, VOCAB)
+};
+
+struct CtlArgs {
+  int batch, n_prompt, n_gen, n_wg, head;
+  int *state;                 // [0] = step; [1 + b] = next input token of sequence b
+  const int *prompt;          // (batch, n_prompt)
+  int *out;                   // (batch, n_gen)
+  const double *part_v; const int *part_i;
+  int *last;                  // (batch,) argmax of the last head evaluation
+};
+
+struct EmbedArgs {
+  int D, batch, VOCAB;
+  const float *embed;
+  const int *state;           // tokens at state[1 + b]
+  int16_t *h_m; int8_t *h_e;
+};
+
+}  // namespace bfp

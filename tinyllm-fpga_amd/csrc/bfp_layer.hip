@@ -1,0 +1,602 @@
+// Fused decoder-layer, head and driver kernels of the BFP decode datapath.
+//
+// One decode step of one layer is five launches (rtl/vc707/host/
+// gen_smollm_blockfp_full.py:261-293 is the sequence they implement):
+//   qkv   : n1 = rmsnorm(h, g1) (recomputed per workgroup) -> q|k|v matvec
+//   attn  : RoPE q,k (per head), KV-cache write, scores/softmax/AV in float64,
+//           attn re-quantised                    (one workgroup per q head)
+//   o_res : o = Wo attn, h1 = q(h + o)          (residual in the epilogue)
+//   gu    : n2 = rmsnorm(h1, g2) -> g, u (same 16 rows per workgroup) ->
+//           mlp = q(q(silu(g)) * u)              (SwiGLU in the epilogue)
+//   d_res : d = Wd mlp, h_out = q(h1 + d)
+// Every launch handles `batch` independent sequences (grid.y).
+#include <stdint.h>
+
+#include "bfp.h"
+#include "bfp_device.h"
+#include "bfp_f64.h"
+#include "bfp_internal.h"
+#include "bfp_layer.h"
+#include "bfp_mv.h"
+
+namespace bfp {
+
+__device__ __forceinline__ int cur_pos(const LayerArgs &a) {
+  return a.pos_ptr ? *a.pos_ptr : a.pos_const;
+}
+
+// rmsnorm_fp (full.py:236-238) of a BFP vector, re-quantised, into the
+// matvec's LDS input form.  v = pairwise_sum(x*x)/D + 1e-5, y = (x*g)/sqrt(v).
+// dbuf: D doubles of LDS, leaf: PW_MAX_LEAVES doubles.  All threads call.
+__device__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
+                             const double *__restrict__ g, int D, int *xs, int *xes, double *dbuf,
+                             double *leaf, int16_t *dm, int8_t *de) {
+  const int bs = blockDim.x, tid = threadIdx.x;
+  for (int i = tid; i < D; i += bs) {
+    double x = bfp_val(hm[i], he[i >> 4]);
+    dbuf[i] = x * x;
+  }
+  __syncthreads();
+  const double s = pairwise_sum_block(dbuf, D, leaf);
+  const double rt = sqrt(s / (double)D + 1e-5);
+  short *mq = reinterpret_cast<short *>(dbuf);   // dbuf is free again
+  for (int base = 0; base < D; base += bs) {
+    int i = base + tid;
+    bool ok = i < D;
+    double y = 0.0;
+    if (ok) y = (bfp_val(hm[i], he[i >> 4]) * g[i]) / rt;
+    int e;
+    int m = quantize16_lanes(y, e);
+    if (ok) {
+      mq[i] = (short)m;
+      if ((i & 15) == 0) xes[i >> 4] = e;
+      if (dm) {
+        dm[i] = (int16_t)m;
+        if ((i & 15) == 0) de[i >> 4] = (int8_t)e;
+      }
+    }
+  }
+  __syncthreads();
+  for (int p = tid; p < D / 2; p += bs) put_x_pair(xs, p >> 3, p & 7, mq[2 * p], mq[2 * p + 1]);
+}
+
+// ------------------------------------------------------------------- qkv
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
+  extern __shared__ double dsm[];
+  const int nT = a.D / 16;
+  double *dbuf = dsm;                                   // D
+  double *leaf = dsm + a.D;                             // PW_MAX_LEAVES
+  int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);   // nT*16
+  int *xes = xs + nT * 16;                              // nT
+  __shared__ int redM[NW * 16];
+  __shared__ long long redA[NW * 16];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int nq = a.D + 2 * a.KV;
+
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT);
+  int16_t *dm = nullptr;
+  int8_t *de = nullptr;
+  if (a.dump && c == 0) {
+    dm = a.dump->m[ST_N1] + b * a.dump->mstride[ST_N1];
+    de = a.dump->e[ST_N1] + b * (a.dump->mstride[ST_N1] / 16);
+  }
+  rmsnorm_to_x(a.h_m + b * a.D, a.h_e + b * (a.D / 16), a.g1, a.D, xs, xes, dbuf, leaf, dm, de);
+  __syncthreads();
+  long long A;
+  int M;
+  chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
+  if (threadIdx.x < 64) {
+    int m, e;
+    chunk_quant(A, M, m, e);
+    const int lane = threadIdx.x;
+    if (lane < 16) a.qkv_m[b * nq + c * 16 + lane] = (int16_t)m;
+    if (lane == 0) a.qkv_e[b * (nq / 16) + c] = (int8_t)e;
+    if (a.dump && lane < 16) {
+      // V is not rotated: dump it here (Q and K are dumped post-RoPE by k_attn)
+      int row = c * 16 + lane;
+      if (row >= a.D + a.KV) {
+        int r = row - a.D - a.KV;
+        a.dump->m[ST_V][b * a.dump->mstride[ST_V] + r] = (int16_t)m;
+        if (lane == 0) a.dump->e[ST_V][b * (a.dump->mstride[ST_V] / 16) + r / 16] = (int8_t)e;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ attn
+// RoPE of one 64-wide head held one value per lane of a wave (lane l holds
+// element l, pre-rotation x), re-quantised: returns the lane's mantissa.
+__device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
+  const int l = threadIdx.x & 63;
+  const int j = l & 31;
+  double other = __shfl_xor(x, 32, 64);    // the partner element j+32 / j
+  double c = cs[2 * j], s = cs[2 * j + 1];
+  double out;
+  if (l < 32) {
+    out = x * c - other * s;                 // a*c - b*s
+  } else {
+    out = x * c + other * s;                 // b*c + a*s
+  }
+  return quantize16_lanes(out, e);
+}
+
+__global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
+  extern __shared__ double dsm[];
+  double *q = dsm;                  // 64
+  double *kc = dsm + 64;            // 64 (current position, post-rope)
+  double *vc = dsm + 128;           // 64
+  double *leaf = dsm + 192;         // PW_MAX_LEAVES
+  double *sc = leaf + PW_MAX_LEAVES;   // max_ctx
+  __shared__ double red[4];
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int grp = a.H_Q / a.H_KV, g = hq / grp;
+  const int HD = 64;
+  const int pos = cur_pos(a);
+  const int n = pos + 1;
+  const int nq = a.D + 2 * a.KV;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int16_t *qm = a.qkv_m + b * nq;
+  const int8_t *qe = a.qkv_e + b * (nq / 16);
+  const double *cs = a.rope + (long long)pos * HD;     // (HD/2) x (cos, sin)
+  const long long kv_tok = (long long)a.H_KV * HD;     // elements per position
+  int16_t *Km = a.k_m + (long long)b * a.max_ctx * kv_tok;
+  int8_t *Ke = a.k_e + (long long)b * a.max_ctx * (kv_tok / 16);
+  int16_t *Vm = a.v_m + (long long)b * a.max_ctx * kv_tok;
+  int8_t *Ve = a.v_e + (long long)b * a.max_ctx * (kv_tok / 16);
+  const bool writer = (hq % grp) == 0;
+
+  if (w == 0) {            // q head hq
+    int idx = hq * HD + l;
+    int e;
+    int m = rope_lane(bfp_val(qm[idx], qe[idx >> 4]), cs, e);
+    q[l] = bfp_val(m, e);
+    if (a.dump) {
+      a.dump->m[ST_Q][b * a.dump->mstride[ST_Q] + idx] = (int16_t)m;
+      if ((l & 15) == 0) a.dump->e[ST_Q][b * (a.dump->mstride[ST_Q] / 16) + (idx >> 4)] = (int8_t)e;
+    }
+  } else if (w == 1) {     // k head g
+    int idx = a.D + g * HD + l;
+    int e;
+    int m = rope_lane(bfp_val(qm[idx], qe[idx >> 4]), cs, e);
+    kc[l] = bfp_val(m, e);
+    long long o = ((long long)pos * a.H_KV + g) * HD + l;
+    if (writer) {
+      Km[o] = (int16_t)m;
+      if ((l & 15) == 0) Ke[o >> 4] = (int8_t)e;
+    }
+    if (a.dump && writer) {
+      int r = g * HD + l;
+      a.dump->m[ST_K][b * a.dump->mstride[ST_K] + r] = (int16_t)m;
+      if ((l & 15) == 0) a.dump->e[ST_K][b * (a.dump->mstride[ST_K] / 16) + (r >> 4)] = (int8_t)e;
+    }
+  } else if (w == 2) {     // v head g (not rotated)
+    int idx = a.D + a.KV + g * HD + l;
+    int m = qm[idx], e = qe[idx >> 4];
+    vc[l] = bfp_val(m, e);
+    long long o = ((long long)pos * a.H_KV + g) * HD + l;
+    if (writer) {
+      Vm[o] = (int16_t)m;
+      if ((l & 15) == 0) Ve[o >> 4] = (int8_t)e;
+    }
+  }
+  __syncthreads();
+
+  // scores[t] = float(np.dot(q, K[t])) / sqrt(HD)   (full.py:277-278)
+  for (int t = tid; t < n; t += blockDim.x) {
+    double kt[64];
+    if (t == pos) {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) kt[i] = kc[i];
+    } else {
+      const long long o = ((long long)t * a.H_KV + g) * HD;
+      const int16_t *km = Km + o;
+      const int8_t *ke = Ke + (o >> 4);
+#pragma unroll
+      for (int i = 0; i < 64; ++i) kt[i] = bfp_val(km[i], ke[i >> 4]);
+    }
+    sc[t] = ddot64_skx(q, kt) / a.inv_sqrt_hd_div;
+  }
+  __syncthreads();
+  // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
+  double mx = -INFINITY;
+  for (int t = tid; t < n; t += blockDim.x) mx = fmax(mx, sc[t]);
+  for (int o = 32; o >= 1; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+  if (l == 0) red[w] = mx;
+  __syncthreads();
+  mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+  for (int t = tid; t < n; t += blockDim.x) sc[t] = exp_f64(sc[t] - mx);
+  __syncthreads();
+  const double sum = pairwise_sum_block(sc, n, leaf);
+  for (int t = tid; t < n; t += blockDim.x) sc[t] = sc[t] / sum;
+  __syncthreads();
+  // attn_h = sum_t p[t] * V[t]  in ascending t from 0.0 (full.py:280-281)
+  if (w == 0) {
+    double acc = 0.0;
+    for (int t = 0; t < n; ++t) {
+      double vt;
+      if (t == pos) {
+        vt = vc[l];
+      } else {
+        const long long o = ((long long)t * a.H_KV + g) * HD + l;
+        vt = bfp_val(Vm[o], Ve[o >> 4]);
+      }
+      acc = acc + sc[t] * vt;
+    }
+    int e;
+    int m = quantize16_lanes(acc, e);
+    int idx = hq * HD + l;
+    a.att_m[b * a.D + idx] = (int16_t)m;
+    if ((l & 15) == 0) a.att_e[b * (a.D / 16) + (idx >> 4)] = (int8_t)e;
+    if (a.dump) {
+      a.dump->m[ST_ATTN][b * a.dump->mstride[ST_ATTN] + idx] = (int16_t)m;
+      if ((l & 15) == 0)
+        a.dump->e[ST_ATTN][b * (a.dump->mstride[ST_ATTN] / 16) + (idx >> 4)] = (int8_t)e;
+    }
+  }
+}
+
+// ----------------------------------------------------------------- o_res
+// Residual epilogue: y = q(res + o) over the chunk (wave 0, lane r holds row r).
+__device__ __forceinline__ int residual_lane(int om, int oe, int rm, int re, int &e) {
+  double s = bfp_val(rm, re) + bfp_val(om, oe);
+  return quantize16_lanes(s, e);
+}
+
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_o_res(LayerArgs a) {
+  extern __shared__ int ism[];
+  const int nT = a.D / 16;
+  int *xs = ism;
+  int *xes = ism + nT * 16;
+  __shared__ int redM[NW * 16];
+  __shared__ long long redA[NW * 16];
+  const int c = blockIdx.x, b = blockIdx.y;
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT);
+  stage_x_bfp(xs, xes, a.att_m + b * a.D, a.att_e + b * (a.D / 16), nT);
+  __syncthreads();
+  long long A;
+  int M;
+  chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
+  if (threadIdx.x < 64) {
+    const int r = threadIdx.x & 15;
+    int om, oe;
+    chunk_quant(A, M, om, oe);
+    const int row = b * a.D + c * 16 + r;
+    const int tile = b * (a.D / 16) + c;
+    int e;
+    int m = residual_lane(om, oe, a.h_m[row], a.h_e[tile], e);
+    if (threadIdx.x < 16) {
+      a.h1_m[row] = (int16_t)m;
+      if (r == 0) a.h1_e[tile] = (int8_t)e;
+      if (a.dump) {
+        const StageDump *d = a.dump;
+        d->m[ST_O][b * d->mstride[ST_O] + c * 16 + r] = (int16_t)om;
+        d->m[ST_H1][b * d->mstride[ST_H1] + c * 16 + r] = (int16_t)m;
+        if (r == 0) {
+          d->e[ST_O][b * (d->mstride[ST_O] / 16) + c] = (int8_t)oe;
+          d->e[ST_H1][b * (d->mstride[ST_H1] / 16) + c] = (int8_t)e;
+        }
+      }
+    }
+  }
+}
+
+// -------------------------------------------------------------------- gu
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_gu(LayerArgs a) {
+  extern __shared__ double dsm[];
+  const int nT = a.D / 16;
+  double *dbuf = dsm;
+  double *leaf = dsm + a.D;
+  int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);
+  int *xes = xs + nT * 16;
+  __shared__ int redM[NW * 16];
+  __shared__ long long redA[NW * 16];
+  const int c = blockIdx.x, b = blockIdx.y;
+  ChunkRegs<TPT> RG, RU;
+  load_chunk<NW, TPT>(RG, a.w_gu_m + (long long)(2 * c) * nT * 32,
+                      a.w_gu_e + (long long)(2 * c) * nT * 16, nT);
+  load_chunk<NW, TPT>(RU, a.w_gu_m + (long long)(2 * c + 1) * nT * 32,
+                      a.w_gu_e + (long long)(2 * c + 1) * nT * 16, nT);
+  int16_t *dm = nullptr;
+  int8_t *de = nullptr;
+  if (a.dump && c == 0) {
+    dm = a.dump->m[ST_N2] + b * a.dump->mstride[ST_N2];
+    de = a.dump->e[ST_N2] + b * (a.dump->mstride[ST_N2] / 16);
+  }
+  rmsnorm_to_x(a.h1_m + b * a.D, a.h1_e + b * (a.D / 16), a.g2, a.D, xs, xes, dbuf, leaf, dm, de);
+  __syncthreads();
+  long long Ag, Au;
+  int Mg, Mu;
+  chunk_AM<NW, TPT>(RG, xs, xes, nT, redM, redA, Ag, Mg);
+  chunk_AM<NW, TPT>(RU, xs, xes, nT, redM, redA, Au, Mu);
+  if (threadIdx.x < 64) {
+    const int r = threadIdx.x & 15;
+    int gm, ge, um, ue;
+    chunk_quant(Ag, Mg, gm, ge);
+    chunk_quant(Au, Mu, um, ue);
+    // silu_fp: fp_quantize_vec(g / (1 + exp(-g)))   (full.py:241-242)
+    const double gv = bfp_val(gm, ge);
+    int se;
+    int sm = quantize16_lanes(gv / (1.0 + exp_f64(-gv)), se);
+    // mlp = fp_quantize_vec(silu * u)                (full.py:290)
+    int me;
+    int mm = quantize16_lanes(bfp_val(sm, se) * bfp_val(um, ue), me);
+    if (threadIdx.x < 16) {
+      const int row = b * a.FFN + c * 16 + r;
+      const int tile = b * (a.FFN / 16) + c;
+      a.mlp_m[row] = (int16_t)mm;
+      if (r == 0) a.mlp_e[tile] = (int8_t)me;
+      if (a.dump) {
+        const StageDump *d = a.dump;
+        d->m[ST_G][b * d->mstride[ST_G] + c * 16 + r] = (int16_t)gm;
+        d->m[ST_U][b * d->mstride[ST_U] + c * 16 + r] = (int16_t)um;
+        d->m[ST_MLP][b * d->mstride[ST_MLP] + c * 16 + r] = (int16_t)mm;
+        if (r == 0) {
+          d->e[ST_G][b * (d->mstride[ST_G] / 16) + c] = (int8_t)ge;
+          d->e[ST_U][b * (d->mstride[ST_U] / 16) + c] = (int8_t)ue;
+          d->e[ST_MLP][b * (d->mstride[ST_MLP] / 16) + c] = (int8_t)me;
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- d_res
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_d_res(LayerArgs a) {
+  extern __shared__ int ism[];
+  const int nT = a.FFN / 16;
+  int *xs = ism;
+  int *xes = ism + nT * 16;
+  __shared__ int redM[NW * 16];
+  __shared__ long long redA[NW * 16];
+  const int c = blockIdx.x, b = blockIdx.y;
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT);
+  stage_x_bfp(xs, xes, a.mlp_m + b * a.FFN, a.mlp_e + b * (a.FFN / 16), nT);
+  __syncthreads();
+  long long A;
+  int M;
+  chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
+  if (threadIdx.x < 64) {
+    const int r = threadIdx.x & 15;
+    int dmv, dev;
+    chunk_quant(A, M, dmv, dev);
+    const int row = b * a.D + c * 16 + r;
+    const int tile = b * (a.D / 16) + c;
+    int e;
+    int m = residual_lane(dmv, dev, a.h1_m[row], a.h1_e[tile], e);
+    if (threadIdx.x < 16) {
+      a.h_m[row] = (int16_t)m;
+      if (r == 0) a.h_e[tile] = (int8_t)e;
+      if (a.dump) {
+        const StageDump *d = a.dump;
+        d->m[ST_D][b * d->mstride[ST_D] + c * 16 + r] = (int16_t)dmv;
+        d->m[ST_HOUT][b * d->mstride[ST_HOUT] + c * 16 + r] = (int16_t)m;
+        if (r == 0) {
+          d->e[ST_D][b * (d->mstride[ST_D] / 16) + c] = (int8_t)dev;
+          d->e[ST_HOUT][b * (d->mstride[ST_HOUT] / 16) + c] = (int8_t)e;
+        }
+      }
+      if (a.hist_m) {
+        const int pos = cur_pos(a);
+        if (pos < a.hist_steps) {
+          long long o = (((long long)b * a.hist_steps + pos) * a.NL + a.layer) * a.D;
+          a.hist_m[o + c * 16 + r] = (int16_t)m;
+          if (r == 0) a.hist_e[(o >> 4) + c] = (int8_t)e;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ head
+// logits = ((h / sqrt(mean(h*h) + 1e-5)) * w) @ embed.T in float64
+// (full.py:438-440), with a per-workgroup first-index argmax.  Each row's
+// dot product: 16 lanes, lane l sums k = 64i + 4l + c (i ascending, c =
+// 0..3) with FMA, then a fixed 16-lane butterfly.  (BLAS dgemv's order is
+// host-specific; the argmax differs only if the top two logits are within
+// a few ulps.)
+__global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
+  extern __shared__ double dsm[];
+  double *hn = dsm;                    // D
+  double *leaf = dsm + a.D;            // PW_MAX_LEAVES
+  __shared__ double bv[16];
+  __shared__ int bi[16];
+  const int b = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
+  const int16_t *hm = a.h_m + b * a.D;
+  const int8_t *he = a.h_e + b * (a.D / 16);
+  for (int i = tid; i < a.D; i += blockDim.x) {
+    double x = bfp_val(hm[i], he[i >> 4]);
+    hn[i] = x * x;
+  }
+  __syncthreads();
+  const double s = pairwise_sum_block(hn, a.D, leaf);
+  const double rt = sqrt(s / (double)a.D + 1e-5);
+  for (int i = tid; i < a.D; i += blockDim.x) hn[i] = (bfp_val(hm[i], he[i >> 4]) / rt) * a.norm_w[i];
+  __syncthreads();
+
+  const int l16 = tid & 15, sub = tid >> 4;      // 16 row slots per pass
+  double best = -INFINITY;
+  int besti = 0x7fffffff;
+  const int r0 = wg * a.rows_per_wg;
+  for (int rr = sub; rr < a.rows_per_wg; rr += 16) {
+    const int row = r0 + rr;
+    const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)row * a.D);
+    double acc = 0.0;
+    for (int i = 0; i < a.D / 64; ++i) {
+      float4 f = e4[i * 16 + l16];
+      const double *hp = hn + i * 64 + 4 * l16;
+      acc = fma((double)f.x, hp[0], acc);
+      acc = fma((double)f.y, hp[1], acc);
+      acc = fma((double)f.z, hp[2], acc);
+      acc = fma((double)f.w, hp[3], acc);
+    }
+    acc += __shfl_xor(acc, 8, 64);
+    acc += __shfl_xor(acc, 4, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    acc += __shfl_xor(acc, 1, 64);
+    if (a.logits && l16 == 0) a.logits[(long long)b * a.VOCAB + row] = acc;
+    if (acc > best || (acc == best && row < besti)) {
+      best = acc;
+      besti = row;
+    }
+  }
+  // workgroup argmax, first index on ties
+  for (int o = 16; o < 64; o <<= 1) {
+    double ov = __shfl_xor(best, o, 64);
+    int oi = __shfl_xor(besti, o, 64);
+    if (ov > best || (ov == best && oi < besti)) {
+      best = ov;
+      besti = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    bv[tid >> 6] = best;
+    bi[tid >> 6] = besti;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int k = 1; k < (int)(blockDim.x >> 6); ++k)
+      if (bv[k] > best || (bv[k] == best && bi[k] < besti)) {
+        best = bv[k];
+        besti = bi[k];
+      }
+    a.part_v[b * a.n_wg + wg] = best;
+    a.part_i[b * a.n_wg + wg] = besti;
+  }
+}
+
+// Final argmax of each sequence and the token loop of full.py:432-443:
+// at step s >= n_prompt the argmax is appended; the next input is
+// prompt[s+1] while s+1 < n_prompt, prompt[n_prompt-1] again at
+// s+1 == n_prompt (the reference feeds generated[-1], still the last prompt
+// token), else the argmax.
+__global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
+  const int b = blockIdx.x, l = threadIdx.x;
+  const int s = a.state[0];
+  int nid = -1;
+  if (a.head) {
+    double best = -INFINITY;
+    int besti = 0x7fffffff;
+    for (int k = l; k < a.n_wg; k += 64) {
+      double v = a.part_v[b * a.n_wg + k];
+      int i = a.part_i[b * a.n_wg + k];
+      if (v > best || (v == best && i < besti)) {
+        best = v;
+        besti = i;
+      }
+    }
+    for (int o = 1; o < 64; o <<= 1) {
+      double ov = __shfl_xor(best, o, 64);
+      int oi = __shfl_xor(besti, o, 64);
+      if (ov > best || (ov == best && oi < besti)) {
+        best = ov;
+        besti = oi;
+      }
+    }
+    nid = besti;
+  }
+  if (l == 0) {
+    if (a.head) a.last[b] = nid;
+    if (a.head && s >= a.n_prompt && s - a.n_prompt < a.n_gen) a.out[b * a.n_gen + (s - a.n_prompt)] = nid;
+    int next;
+    if (s + 1 < a.n_prompt)
+      next = a.prompt[b * a.n_prompt + s + 1];
+    else if (s + 1 == a.n_prompt)
+      next = a.prompt[b * a.n_prompt + a.n_prompt - 1];
+    else
+      next = nid;
+    a.state[1 + b] = next;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_step_inc(int *state) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) state[0] += 1;
+}
+
+// Embedding lookup of the BFP table: embed_q[tid] = fp_quantize_vec(embed[tid])
+// (full.py:411-412), quantised on the fly from the float32 table.
+__global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
+  const int b = blockIdx.x;
+  int tok = a.state[1 + b];
+  tok = tok < 0 ? 0 : (tok >= a.VOCAB ? a.VOCAB - 1 : tok);
+  const float *row = a.embed + (long long)tok * a.D;
+  for (int base = 0; base < a.D; base += blockDim.x) {
+    int i = base + threadIdx.x;
+    bool ok = i < a.D;
+    double v = ok ? (double)row[i] : 0.0;
+    int e;
+    int m = quantize16_lanes(v, e);
+    if (ok) {
+      a.h_m[b * a.D + i] = (int16_t)m;
+      if ((i & 15) == 0) a.h_e[b * (a.D / 16) + (i >> 4)] = (int8_t)e;
+    }
+  }
+}
+
+// --------------------------------------------------------------- launchers
+typedef void (*lk_fn)(LayerArgs);
+
+// The (waves, tiles per lane) pairs default_waves() produces for
+// 4 <= in/16 <= 108, i.e. every supported D and FFN.
+#define BFP_LAYER_SHAPES(X, KER) \
+  X(KER, 1, 1) X(KER, 1, 2) X(KER, 1, 3) X(KER, 2, 2) X(KER, 2, 3) X(KER, 3, 3) X(KER, 4, 3) \
+  X(KER, 6, 3) X(KER, 8, 3) X(KER, 9, 3)
+#define BFP_CASE(KER, NW, TPT) \
+  if (nw == NW && tpt == TPT) return KER<NW, TPT>;
+
+static lk_fn pick_qkv(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_qkv) return nullptr; }
+static lk_fn pick_ores(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_o_res) return nullptr; }
+static lk_fn pick_gu(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_gu) return nullptr; }
+static lk_fn pick_dres(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_d_res) return nullptr; }
+
+static void shape_for(int nT, int &nw, int &tpt) {
+  nw = default_waves(nT);
+  tpt = (nT + 4 * nw - 1) / (4 * nw);
+}
+
+int launch_layer(const LayerArgs &a, hipStream_t s) {
+  const int nTD = a.D / 16, nTF = a.FFN / 16;
+  int nw, tpt;
+  shape_for(nTD, nw, tpt);
+  const int nq = a.D + 2 * a.KV;
+  const size_t sh_norm = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
+  lk_fn f = pick_qkv(nw, tpt);
+  lk_fn fo = pick_ores(nw, tpt), fg = pick_gu(nw, tpt);
+  if (!f || !fo || !fg) return set_err(BFP_EINVAL, "no layer kernel for D=%d", a.D);
+  hipLaunchKernelGGL(f, dim3(nq / 16, a.batch), dim3(64 * nw), sh_norm, s, a);
+  const size_t sh_attn = (size_t)(192 + PW_MAX_LEAVES + a.max_ctx) * 8;
+  hipLaunchKernelGGL(k_attn, dim3(a.H_Q, a.batch), dim3(256), sh_attn, s, a);
+  hipLaunchKernelGGL(fo, dim3(a.D / 16, a.batch), dim3(64 * nw), (size_t)nTD * 17 * 4, s, a);
+  hipLaunchKernelGGL(fg, dim3(a.FFN / 16, a.batch), dim3(64 * nw), sh_norm, s, a);
+  int nwf, tptf;
+  shape_for(nTF, nwf, tptf);
+  f = pick_dres(nwf, tptf);
+  if (!f) return set_err(BFP_EINVAL, "no down-proj kernel for FFN=%d", a.FFN);
+  hipLaunchKernelGGL(f, dim3(a.D / 16, a.batch), dim3(64 * nwf), (size_t)nTF * 17 * 4, s, a);
+  return launch_status("layer");
+}
+
+int launch_embed(const EmbedArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed, dim3(a.batch), dim3(256), 0, s, a);
+  return launch_status("embed");
+}
+
+int launch_head(const HeadArgs &a, hipStream_t s) {
+  size_t sh = (size_t)(a.D + PW_MAX_LEAVES) * 8;
+  hipLaunchKernelGGL(k_head_logits, dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
+  return launch_status("head");
+}
+
+int launch_ctl(const CtlArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(k_ctl, dim3(a.batch), dim3(64), 0, s, a);
+  hipLaunchKernelGGL(k_step_inc, dim3(1), dim3(64), 0, s, a.state);
+  return launch_status("ctl");
+}
+
+}  // namespace bfp

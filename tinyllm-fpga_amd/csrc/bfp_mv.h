@@ -1,0 +1,155 @@
+// The exact-integer BFP matvec engine for one 16-row output chunk, shared by
+// the standalone matvec and the fused layer kernels.
+//
+// Semantics: rtl/vc707/host/gen_smollm_blockfp_full.py:217-233.  Per row o
+// and input tile t: S = sum_k x_m[t,k] W_m[o,t,k] (exact), E = x_e[t] +
+// W_e[o,t]; M = max_t E; A = sum_t floor(S / 2^(M-E)) for M-E <= 47, clipped
+// to +-2^47; y_o = A * 2^(M-30), re-quantised over the 16 rows of the chunk.
+//
+// Work split inside a workgroup of NW waves: lane (w, lane) takes row
+// r = lane % 16 and tile lane tq = lane / 16, and owns tiles
+// t = tq + 4*(w + NW*j), j < TPT, so each 16-byte-per-lane load of a wave
+// covers four full 256-byte half-tile planes of the device layout.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bfp_device.h"
+
+namespace bfp {
+
+template <int TPT>
+struct ChunkRegs {
+  uint4 a[TPT], b[TPT];
+  int e[TPT];
+};
+
+template <int NW, int TPT>
+__device__ __forceinline__ void load_chunk(ChunkRegs<TPT> &R, const uint4 *__restrict__ pm,
+                                           const int8_t *__restrict__ pe, int nT) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int t = tq + 4 * (w + NW * j);
+    if (t < nT) {
+      R.a[j] = pm[t * 32 + r];
+      R.b[j] = pm[t * 32 + 16 + r];
+      R.e[j] = pe[t * 16 + r];
+    } else {
+      R.a[j] = make_uint4(0, 0, 0, 0);
+      R.b[j] = make_uint4(0, 0, 0, 0);
+      R.e[j] = 0;
+    }
+  }
+}
+
+// LDS form of the input vector: per tile 8 dwords of packed (xh, xh) int16
+// pairs then 8 dwords of (xl, xl) pairs, with x = 256*xh + xl.
+__device__ __forceinline__ void put_x_pair(int *xs, int t, int k, int lo, int hi) {
+  xs[t * 16 + k] = ((lo >> 8) & 0xffff) | ((hi >> 8) << 16);
+  xs[t * 16 + 8 + k] = (lo & 0xff) | ((hi & 0xff) << 16);
+}
+
+// Stage a BFP vector from global memory (all threads; caller syncs).
+__device__ __forceinline__ void stage_x_bfp(int *xs, int *xes, const int16_t *__restrict__ xm,
+                                            const int8_t *__restrict__ xe, int nT) {
+  const int *x32 = reinterpret_cast<const int *>(xm);
+  for (int p = threadIdx.x; p < nT * 8; p += blockDim.x) {
+    int v = x32[p];
+    put_x_pair(xs, p >> 3, p & 7, (int)(short)(v & 0xffff), v >> 16);
+  }
+  for (int p = threadIdx.x; p < nT; p += blockDim.x) xes[p] = xe[p];
+}
+
+// Row (A, M) of the chunk.  Every thread of the workgroup must call it (it
+// synchronises when NW > 1).  On return the lanes of wave 0 hold their row
+// r's (A, M); other waves hold partial values.
+template <int NW, int TPT>
+__device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs, const int *xes,
+                                         int nT, int *redM, long long *redA, long long &A_out,
+                                         int &M_out) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+  typedef short s2 __attribute__((ext_vector_type(2)));
+#define BFP_DOT2(a, b, acc) \
+  __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, (a)), __builtin_bit_cast(s2, (b)), (acc), false)
+  long long S[TPT];
+  int E[TPT];
+  int M = -(1 << 29);
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int t = tq + 4 * (w + NW * j);
+    if (t < nT) {
+      const int4 *xp = reinterpret_cast<const int4 *>(xs + t * 16);
+      int4 h0 = xp[0], h1 = xp[1], l0 = xp[2], l1 = xp[3];
+      int ah = 0, al = 0;
+      ah = BFP_DOT2(R.a[j].x, h0.x, ah);
+      al = BFP_DOT2(R.a[j].x, l0.x, al);
+      ah = BFP_DOT2(R.a[j].y, h0.y, ah);
+      al = BFP_DOT2(R.a[j].y, l0.y, al);
+      ah = BFP_DOT2(R.a[j].z, h0.z, ah);
+      al = BFP_DOT2(R.a[j].z, l0.z, al);
+      ah = BFP_DOT2(R.a[j].w, h0.w, ah);
+      al = BFP_DOT2(R.a[j].w, l0.w, al);
+      ah = BFP_DOT2(R.b[j].x, h1.x, ah);
+      al = BFP_DOT2(R.b[j].x, l1.x, al);
+      ah = BFP_DOT2(R.b[j].y, h1.y, ah);
+      al = BFP_DOT2(R.b[j].y, l1.y, al);
+      ah = BFP_DOT2(R.b[j].z, h1.z, ah);
+      al = BFP_DOT2(R.b[j].z, l1.z, al);
+      ah = BFP_DOT2(R.b[j].w, h1.w, ah);
+      al = BFP_DOT2(R.b[j].w, l1.w, al);
+      S[j] = (long long)ah * 256 + al;
+      E[j] = xes[t] + R.e[j];
+      M = E[j] > M ? E[j] : M;
+    } else {
+      S[j] = 0;
+      E[j] = -(1 << 29);
+    }
+  }
+#undef BFP_DOT2
+  M = xor_max(M, 16);
+  M = xor_max(M, 32);
+  if (NW > 1) {
+    if (tq == 0) redM[w * 16 + r] = M;
+    __syncthreads();
+    M = redM[r];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) M = redM[i * 16 + r] > M ? redM[i * 16 + r] : M;
+  }
+  long long A = 0;
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int sh = M - E[j];
+    if (sh <= ALIGN_MAX) A += S[j] >> sh;
+  }
+  A = xor_sum(A, 16);
+  A = xor_sum(A, 32);
+  if (NW > 1) {
+    if (tq == 0) redA[w * 16 + r] = A;
+    __syncthreads();
+    if (w == 0) {
+      A = redA[r];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) A += redA[i * 16 + r];
+    }
+    __syncthreads();   // redM/redA may be reused by a following chunk
+  }
+  A = A < SAT_LO ? SAT_LO : (A > SAT_HI ? SAT_HI : A);
+  A_out = A;
+  M_out = M;
+}
+
+// Quantise the chunk's 16 rows (wave 0; lanes r and r+16k hold row r).
+__device__ __forceinline__ void chunk_quant(long long A, int M, int &m, int &e) {
+  int L = row_log2(A, M);
+  L = xor_max(L, 1);
+  L = xor_max(L, 2);
+  L = xor_max(L, 4);
+  L = xor_max(L, 8);
+  e = chunk_exp_from_lmax(L);
+  m = rne_shr_clip(A, e + 15 - M);
+}
+
+}  // namespace bfp
