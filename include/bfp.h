@@ -132,6 +132,14 @@ int bfp_load_weights(bfp_ctx *ctx, int which, int layer, const float *fp32, cons
 /* Zero the KV cache (the reference starts every run from zeros, full.py:426-428). */
 int bfp_reset_kv(bfp_ctx *ctx);
 
+/* Copy KV-cache positions [t0, t0+n) of one layer and sequence between the
+ * device and host buffers: k_m/v_m are n x H_KV*HD int16 (post-RoPE K, raw
+ * V, as full.py:270-272 stores them), k_e/v_e n x H_KV*HD/16 int8.
+ * write != 0 uploads (e.g. the preloaded cache of gen_smollm_blockfp_bfp.py
+ * :209-216, or a saved cache), write == 0 reads back. */
+int bfp_kv_io(bfp_ctx *ctx, int layer, int seq, int t0, int n, int16_t *k_m, int8_t *k_e,
+              int16_t *v_m, int8_t *v_e, int write);
+
 /* Per-stage BFP outputs of one layer step, as gen_smollm_blockfp_bfp.py:398-409
  * dumps them (Q and K after RoPE).  Host buffers of batch x len mantissas and
  * batch x len/16 exponents; NULL entries are skipped.  Stage order:

@@ -1,0 +1,93 @@
+"""GPU against vectors written by the reference's own code (no oracle in the
+loop): the single-layer baker's stage dumps with its preloaded KV cache,
+BASELINE config 1 (reference fwd_layer, 8 positions) and BASELINE config 3
+(30 layers, 8-token prompt, 64 greedy tokens: token ids and a digest of every
+layer's output at every step)."""
+import hashlib
+
+import numpy as np
+import pytest
+
+from refcases import GOLDEN, baker_case
+
+pytestmark = pytest.mark.gpu
+
+STAGES = ["N1", "Q", "K", "V", "ATTN", "O", "H1", "N2", "G", "U", "MLP", "D", "HOUT"]
+
+
+@pytest.mark.parametrize("name", ["small", "full"])
+def test_baker_stages_on_gpu(gpu, name):
+    import bfp.api as api
+    from bfp import Dims
+    from bfp.model import BfpModel
+    c = baker_case(name)
+    cfg, f = c["cfg"], c["fixture"]
+    print(f"[gpu-ref] baker {name} {cfg}", flush=True)
+    d = Dims(D=cfg["D"], H_Q=cfg["H_Q"], H_KV=cfg["H_KV"], HD=cfg["HD"], FFN=cfg["FFN"], NL=1,
+             MAX_CTX=cfg["MAX_CTX"], VOCAB=256)
+    gm = BfpModel(d)
+    for n, W in c["W"].items():                 # float64 weights quantised on the device
+        m, e = api.quantize_W(W)
+        gm.load_tensor(n, 0, m=m, e=e)
+    for n in ("g1", "g2"):
+        m, e = api.tile_quantize(c[n])
+        gm.load_tensor(n, 0, m=m, e=e)
+    MC = cfg["MAX_CTX"]
+    kq = [api.tile_quantize(c["kv"]["k"][t].reshape(-1)) for t in range(MC)]
+    vq = [api.tile_quantize(c["kv"]["v"][t].reshape(-1)) for t in range(MC)]
+    gm.kv_io(0, 0, 0, MC, k=(np.stack([q[0].reshape(-1) for q in kq]), np.stack([q[1] for q in kq])),
+             v=(np.stack([q[0].reshape(-1) for q in vq]), np.stack([q[1] for q in vq])))
+    hm, he = f["HIN_m"], f["HIN_e"]
+    out_m, out_e, st = gm.layer_step_bfp(0, cfg["POS"], hm[None, :], he[None, :], dump=True)
+    for tag in STAGES:
+        key = tag if tag != "HOUT" else "HOUT"
+        gm_, ge_ = st[tag]
+        assert (ge_[0] == f[f"{key}_e"]).all(), f"stage {tag} exponents"
+        assert (gm_[0] == f[f"{key}_m"]).all(), f"stage {tag} mantissas"
+    assert (out_m[0] == f["HOUT_m"]).all() and (out_e[0] == f["HOUT_e"]).all()
+    gm.close()
+
+
+def test_config1_on_gpu(gpu):
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    import bfp.api as api
+    f = np.load(GOLDEN / "ref_layer_cfg1.npz")
+    d = Dims(NL=1, MAX_CTX=16, VOCAB=256)
+    fm = synth.make_model(d, seed=int(f["seed"]))
+    xs = synth.make_layer_inputs(d, 8, seed=int(f["seed"]))
+    gm = BfpModel(d)
+    gm.load_fp32(fm)
+    for p in range(8):
+        m, e = api.tile_quantize(xs[p])
+        om_, oe_, _ = gm.layer_step_bfp(0, p, m.reshape(1, -1), e.reshape(1, -1))
+        assert (om_[0] == f["hout_m"][p]).all() and (oe_[0] == f["hout_e"][p]).all(), p
+    (km, ke), (vm, ve) = gm.kv_io(0, 0, 0, 8)
+    assert (km == f["k_m"]).all() and (ke == f["k_e"]).all()
+    assert (vm == f["v_m"]).all() and (ve == f["v_e"]).all()
+    gm.close()
+
+
+def test_config3_decode_on_gpu(gpu):
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    path = GOLDEN / "ref_decode_cfg3.npz"
+    f = np.load(path)
+    prompt = f["prompt"]
+    n_gen = len(f["tokens"])
+    d = Dims(MAX_CTX=len(prompt) + n_gen)
+    print("[gpu-ref] config 3: building the 30-layer model", flush=True)
+    fm = synth.make_model(d, seed=int(f["seed"]))
+    gm = BfpModel(d)
+    gm.load_fp32(fm)
+    print("[gpu-ref] config 3: decoding", flush=True)
+    toks, (hm, he) = gm.decode(prompt[None, :], n_gen, hist=True)
+    for s in range(len(prompt) + n_gen):
+        h = hashlib.sha256()
+        for li in range(d.NL):
+            h.update(hm[0, s, li].tobytes())
+            h.update(he[0, s, li].tobytes())
+        assert h.hexdigest() == str(f["digests"][s]), f"step {s}: layer outputs differ"
+        assert (hm[0, s, d.NL - 1] == f["last_m"][s]).all()
+    assert list(toks[0]) == [int(t) for t in f["tokens"]]
+    gm.close()

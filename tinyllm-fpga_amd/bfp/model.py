@@ -87,6 +87,20 @@ class BfpModel:
     def reset_kv(self):
         call("bfp_reset_kv", self._h)
 
+    def kv_io(self, layer, seq, t0, n, k=None, v=None):
+        """Read (k, v None) or write KV positions [t0, t0+n): each a pair
+        (m (n, H_KV*HD) int16, e (n, H_KV*HD/16) int8)."""
+        d = self.dims
+        if k is None:
+            km = np.zeros((n, d.KV), np.int16)
+            ke = np.zeros((n, d.KV // 16), np.int8)
+            vm, ve = np.zeros_like(km), np.zeros_like(ke)
+            call("bfp_kv_io", self._h, layer, seq, t0, n, _p(km), _p(ke), _p(vm), _p(ve), 0)
+            return (km, ke), (vm, ve)
+        km, ke = _c16(k[0]).reshape(n, d.KV), _c8(k[1]).reshape(n, d.KV // 16)
+        vm, ve = _c16(v[0]).reshape(n, d.KV), _c8(v[1]).reshape(n, d.KV // 16)
+        call("bfp_kv_io", self._h, layer, seq, t0, n, _p(km), _p(ke), _p(vm), _p(ve), 1)
+
     # ----------------------------------------------------------- layer step
     def _stage_len(self, name):
         d = self.dims

@@ -347,6 +347,36 @@ int bfp_reset_kv(bfp_ctx *c) {
   return BFP_OK;
 }
 
+int bfp_kv_io(bfp_ctx *c, int layer, int seq, int t0, int n, int16_t *k_m, int8_t *k_e,
+              int16_t *v_m, int8_t *v_e, int write) {
+  if (!c || !k_m || !k_e || !v_m || !v_e) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  if (layer < 0 || layer >= d.NL || seq < 0 || seq >= c->max_batch || t0 < 0 || n < 0 ||
+      t0 + n > c->max_ctx)
+    return set_err(BFP_ERANGE, "kv_io: layer %d seq %d positions [%d, %d) out of range", layer, seq,
+                   t0, t0 + n);
+  if (n == 0) return BFP_OK;
+  HIP_TRY(hipSetDevice(c->device));
+  const size_t KV = (size_t)d.H_KV * d.HD;
+  const size_t om = layer * c->s_kv_m + ((size_t)seq * c->max_ctx + t0) * KV;
+  const size_t oe = layer * c->s_kv_e + ((size_t)seq * c->max_ctx + t0) * KV / 16;
+  const size_t bm = (size_t)n * KV * 2, be = (size_t)n * KV / 16;
+  hipStream_t s = c->stream;
+  if (write) {
+    HIP_TRY(hipMemcpyAsync(c->k_m + om, k_m, bm, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(c->k_e + oe, k_e, be, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(c->v_m + om, v_m, bm, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(c->v_e + oe, v_e, be, hipMemcpyHostToDevice, s));
+  } else {
+    HIP_TRY(hipMemcpyAsync(k_m, c->k_m + om, bm, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(k_e, c->k_e + oe, be, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(v_m, c->v_m + om, bm, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(v_e, c->v_e + oe, be, hipMemcpyDeviceToHost, s));
+  }
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
 // fwd_layer (full.py:261-293) for `batch` sequences at position pos
 // (kv_pos = pos).  h in/out are host arrays (batch x D mantissas, batch x
 // D/16 exponents); dump (optional) receives every stage.
