@@ -47,8 +47,8 @@ def test_layer_8_positions(gpu, cfg):
         hm, he = sim.tile_quantize(h)
         out_m, out_e, st = gm.layer_step_bfp(0, p, hm.reshape(1, -1), he.reshape(1, -1), dump=True)
         _check_stages(st, dump, 0, p, str(cfg["D"]))
-        wm, we = sim.tile_quantize(want)
-        assert (out_m[0] == wm.reshape(-1)).all() and (out_e[0] == we).all()
+        # the returned tile is the raw quantisation: its values are the reference's
+        assert (sim.tile_decode(out_m[0].reshape(-1, 16), out_e[0]) == want).all()
     gm.close()
 
 

@@ -32,7 +32,7 @@ def test_matvec_baseline_shapes(gpu, n_out, n_in):
     W, x = _synth(n_out, n_in, seed=n_out + n_in)
     Wm, We = _oracle_quantize_W(W)
     xm, xe = sim.tile_quantize(x)
-    want = sim.tile_quantize(sim.matvec_hw_golden(xm, xe, Wm, We))
+    want = sim.matvec_bfp(xm, xe, Wm, We)
     P = api.PackedMatrix.from_float(W)                 # device quantize_W
     gm, ge = P.unpack()
     assert (gm == Wm).all() and (ge == We).all()
@@ -49,7 +49,7 @@ def test_matvec_wave_shapes(gpu, waves):
         W, x = _synth(n_out, n_in, seed=7 * waves)
         Wm, We = _oracle_quantize_W(W)
         xm, xe = sim.tile_quantize(x)
-        want_m, want_e = sim.tile_quantize(sim.matvec_hw_golden(xm, xe, Wm, We))
+        want_m, want_e = sim.matvec_bfp(xm, xe, Wm, We)
         ym, ye = api.PackedMatrix(Wm, We).matvec_bfp(xm, xe, waves=waves)
         assert (ye == want_e).all() and (ym == want_m.reshape(-1)).all()
 
@@ -71,7 +71,7 @@ def test_matvec_integer_edges(gpu, n_out, n_in, espread):
     Wm[min(17, n_out - 1)] = 0
     if n_out >= 32:
         Wm[16:32] = 0              # an all-zero output chunk -> e = -127
-    want_m, want_e = sim.tile_quantize(sim.matvec_hw_golden(xm, xe, Wm, We))
+    want_m, want_e = sim.matvec_bfp(xm, xe, Wm, We)
     ym, ye = api.matvec_bfp(xm, xe, Wm, We)
     assert (ye == want_e).all() and (ym == want_m.reshape(-1)).all()
 
@@ -104,8 +104,34 @@ def test_matvec_batched_ring(gpu):
     ym, ye = ym.cpu().numpy().reshape(n_mats, -1), ye.cpu().numpy().reshape(n_mats, -1)
     for i in range(n_mats):
         Wm, We = _oracle_quantize_W(W[i % ring])
-        want_m, want_e = sim.tile_quantize(sim.matvec_hw_golden(xq[i][0], xq[i][1], Wm, We))
+        want_m, want_e = sim.matvec_bfp(xq[i][0], xq[i][1], Wm, We)
         assert (ye[i] == want_e).all() and (ym[i] == want_m.reshape(-1)).all()
+
+
+def _neg_full_scale_case():
+    """One output row with A = -(2^20 - 1) at M = 30: y = -1048575 rounds to
+    mantissa -32768 at e = 20 (raw); re-quantised it is (-16384, 21)."""
+    xm = np.zeros((2, 16), np.int16)
+    xe = np.array([15, 0], np.int8)
+    Wm = np.zeros((16, 2, 16), np.int16)
+    We = np.zeros((16, 2), np.int8)
+    xm[0, 0], xm[0, 1] = 32, 31
+    Wm[0, 0, 0], Wm[0, 0, 1] = -32767, -1
+    We[0, 0] = 15
+    Wm[3, 0, 0] = 3                # an odd mantissa elsewhere in the chunk
+    We[3, 0] = 15
+    return xm, xe, Wm, We
+
+
+def test_matvec_neg_full_scale_raw(gpu):
+    import bfp.api as api
+    xm, xe, Wm, We = _neg_full_scale_case()
+    m, e = sim.matvec_bfp(xm, xe, Wm, We)
+    assert m[0, 0] == -32768 and e[0] == 20
+    ym, ye = api.matvec_bfp(xm, xe, Wm, We)
+    assert (ym == m.reshape(-1)).all() and (ye == e).all()
+    # the decoded values are the reference's float64 output
+    assert (api.matvec_hw_golden(xm, xe, Wm, We) == sim.matvec_hw_golden(xm, xe, Wm, We)).all()
 
 
 def test_tile_quantize_and_decode(gpu):

@@ -131,6 +131,20 @@ def test_matvec_shift_drop_boundary():
     assert M[0] == 100 and A[0] == 1 - 1
 
 
+def test_requantise_neg_full_scale():
+    """Re-quantising a decoded tile whose max magnitude is the mantissa
+    -32768 gives (round_half_even(m/2), e+1): the form fwd_layer's next
+    matvec sees (full.py:264,283,287,291 quantise decoded values)."""
+    m = np.zeros((1, 16), np.int16)
+    m[0, :5] = [-32768, 3, -3, 5, 16383]
+    e = np.array([4], np.int8)
+    m2, e2 = sim.tile_quantize(sim.tile_decode(m, e))
+    assert e2[0] == 5
+    assert list(m2[0, :5]) == [-16384, 2, -2, 2, 8192]
+    bm, be = bi.quantize_vec(bi.decode_vec(m.tolist(), e.tolist()))
+    assert be == [5] and bm[0][:5] == [-16384, 2, -2, 2, 8192]
+
+
 def test_epilogue_int_random():
     rng = random.Random(5)
     for _ in range(300):

@@ -74,6 +74,14 @@ def lib():
     """Load (once) and return the configured ctypes library."""
     global _LIB
     if _LIB is None:
+        # One HIP runtime per process: torch ships its own libamdhip64 (same
+        # SONAME as /opt/rocm's) and loads it by file name, so it must be in
+        # the process before libbfp.so resolves its libamdhip64.so.7 -- the
+        # other order maps two runtimes and torch then sees no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not LIB_PATH.exists():
             raise ImportError(f"{LIB_PATH} is missing: build it with "
                               "`python tinyllm-fpga_amd/build.py` (no CPU fallback exists)")

@@ -124,17 +124,43 @@ __device__ inline double ddot64_skx(const double *x, const double *y) {
 __device__ __forceinline__ double exp_f64(double x) { return exp(x); }
 
 // -------------------------------------------------------- tile quantise
+// Canonical BFP form.  Each stage of the reference hands float64 values
+// (the decoded "raw" quantisation) to the next op.  Where the next op is a
+// matvec, those values are quantised again with tile_quantize
+// (full.py:264,283,287,291), and so are the stage dumps
+// (gen_smollm_blockfp_bfp.py:393-409).  Re-quantising is the identity except
+// for a tile whose largest magnitude is the mantissa -32768: it becomes
+// e+1 with every mantissa round-half-even(m/2) -- which changes the values of
+// odd mantissas.  So the pipeline carries raw tiles between stages and
+// forms the canonical tile only for matvec inputs and dumps.  16 lanes (one
+// mantissa each) call it.
+__device__ __forceinline__ void canon16_lanes(int &m, int &e) {
+  int hit = (m == -32768) ? 1 : 0;
+  hit |= __shfl_xor(hit, 1, 64);
+  hit |= __shfl_xor(hit, 2, 64);
+  hit |= __shfl_xor(hit, 4, 64);
+  hit |= __shfl_xor(hit, 8, 64);
+  if (hit && e < 127) {
+    e += 1;
+    int q = m >> 1;                     // floor(m / 2)
+    m = (m & 1) ? q + (q & 1) : q;      // ties to even
+  }
+}
+
 // Quantise the 16 values held by lanes (lane & ~15) .. (lane | 15) of a
 // wave (one value per lane): returns this lane's mantissa and sets e to the
-// tile exponent.  All 64 lanes must participate.
-__device__ __forceinline__ int quantize16_lanes(double v, int &e) {
+// tile exponent (tile_quantize, full.py:90-97; canonical form when
+// `canonical`).  All 64 lanes must participate.
+__device__ __forceinline__ int quantize16_lanes(double v, int &e, bool canonical = false) {
   double a = fabs(v);
   a = xor_max(a, 1);
   a = xor_max(a, 2);
   a = xor_max(a, 4);
   a = xor_max(a, 8);
   e = tile_exp_of(a);
-  return tile_mant_of(v, e);
+  int m = tile_mant_of(v, e);
+  if (canonical) canon16_lanes(m, e);
+  return m;
 }
 
 __device__ __forceinline__ double bfp_val(int m, int e) { return ldexp((double)m, e - 15); }

@@ -21,6 +21,13 @@
 
 namespace bfp {
 
+// Canonical copy (m, e) of a raw tile held one mantissa per lane.
+__device__ __forceinline__ void canon_copy(int m, int e, int &cm, int &ce) {
+  cm = m;
+  ce = e;
+  canon16_lanes(cm, ce);
+}
+
 __device__ __forceinline__ int cur_pos(const LayerArgs &a) {
   return a.pos_ptr ? *a.pos_ptr : a.pos_const;
 }
@@ -46,7 +53,7 @@ __device__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__res
     double y = 0.0;
     if (ok) y = (bfp_val(hm[i], he[i >> 4]) * g[i]) / rt;
     int e;
-    int m = quantize16_lanes(y, e);
+    int m = quantize16_lanes(y, e, true);   // tile_quantize(rmsnorm_fp(.)): canonical
     if (ok) {
       mq[i] = (short)m;
       if ((i & 15) == 0) xes[i >> 4] = e;
@@ -93,13 +100,15 @@ __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
     const int lane = threadIdx.x;
     if (lane < 16) a.qkv_m[b * nq + c * 16 + lane] = (int16_t)m;
     if (lane == 0) a.qkv_e[b * (nq / 16) + c] = (int8_t)e;
-    if (a.dump && lane < 16) {
+    if (a.dump) {
       // V is not rotated: dump it here (Q and K are dumped post-RoPE by k_attn)
+      int cm, ce;
+      canon_copy(m, e, cm, ce);
       int row = c * 16 + lane;
-      if (row >= a.D + a.KV) {
+      if (lane < 16 && row >= a.D + a.KV) {
         int r = row - a.D - a.KV;
-        a.dump->m[ST_V][b * a.dump->mstride[ST_V] + r] = (int16_t)m;
-        if (lane == 0) a.dump->e[ST_V][b * (a.dump->mstride[ST_V] / 16) + r / 16] = (int8_t)e;
+        a.dump->m[ST_V][b * a.dump->mstride[ST_V] + r] = (int16_t)cm;
+        if (lane == 0) a.dump->e[ST_V][b * (a.dump->mstride[ST_V] / 16) + r / 16] = (int8_t)ce;
       }
     }
   }
@@ -153,8 +162,10 @@ __global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
     int m = rope_lane(bfp_val(qm[idx], qe[idx >> 4]), cs, e);
     q[l] = bfp_val(m, e);
     if (a.dump) {
-      a.dump->m[ST_Q][b * a.dump->mstride[ST_Q] + idx] = (int16_t)m;
-      if ((l & 15) == 0) a.dump->e[ST_Q][b * (a.dump->mstride[ST_Q] / 16) + (idx >> 4)] = (int8_t)e;
+      int cm, ce;
+      canon_copy(m, e, cm, ce);
+      a.dump->m[ST_Q][b * a.dump->mstride[ST_Q] + idx] = (int16_t)cm;
+      if ((l & 15) == 0) a.dump->e[ST_Q][b * (a.dump->mstride[ST_Q] / 16) + (idx >> 4)] = (int8_t)ce;
     }
   } else if (w == 1) {     // k head g
     int idx = a.D + g * HD + l;
@@ -167,9 +178,11 @@ __global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
       if ((l & 15) == 0) Ke[o >> 4] = (int8_t)e;
     }
     if (a.dump && writer) {
+      int cm, ce;
+      canon_copy(m, e, cm, ce);
       int r = g * HD + l;
-      a.dump->m[ST_K][b * a.dump->mstride[ST_K] + r] = (int16_t)m;
-      if ((l & 15) == 0) a.dump->e[ST_K][b * (a.dump->mstride[ST_K] / 16) + (r >> 4)] = (int8_t)e;
+      a.dump->m[ST_K][b * a.dump->mstride[ST_K] + r] = (int16_t)cm;
+      if ((l & 15) == 0) a.dump->e[ST_K][b * (a.dump->mstride[ST_K] / 16) + (r >> 4)] = (int8_t)ce;
     }
   } else if (w == 2) {     // v head g (not rotated)
     int idx = a.D + a.KV + g * HD + l;
@@ -225,7 +238,7 @@ __global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
       acc = acc + sc[t] * vt;
     }
     int e;
-    int m = quantize16_lanes(acc, e);
+    int m = quantize16_lanes(acc, e, true);   // tile_quantize(fp_quantize_vec(attn))
     int idx = hq * HD + l;
     a.att_m[b * a.D + idx] = (int16_t)m;
     if ((l & 15) == 0) a.att_e[b * (a.D / 16) + (idx >> 4)] = (int8_t)e;
@@ -268,16 +281,21 @@ __global__ __launch_bounds__(64 * NW) void k_o_res(LayerArgs a) {
     const int tile = b * (a.D / 16) + c;
     int e;
     int m = residual_lane(om, oe, a.h_m[row], a.h_e[tile], e);
+    int com = om, coe = oe, chm = m, che = e;
+    if (a.dump) {
+      canon16_lanes(com, coe);
+      canon16_lanes(chm, che);
+    }
     if (threadIdx.x < 16) {
       a.h1_m[row] = (int16_t)m;
       if (r == 0) a.h1_e[tile] = (int8_t)e;
       if (a.dump) {
         const StageDump *d = a.dump;
-        d->m[ST_O][b * d->mstride[ST_O] + c * 16 + r] = (int16_t)om;
-        d->m[ST_H1][b * d->mstride[ST_H1] + c * 16 + r] = (int16_t)m;
+        d->m[ST_O][b * d->mstride[ST_O] + c * 16 + r] = (int16_t)com;
+        d->m[ST_H1][b * d->mstride[ST_H1] + c * 16 + r] = (int16_t)chm;
         if (r == 0) {
-          d->e[ST_O][b * (d->mstride[ST_O] / 16) + c] = (int8_t)oe;
-          d->e[ST_H1][b * (d->mstride[ST_H1] / 16) + c] = (int8_t)e;
+          d->e[ST_O][b * (d->mstride[ST_O] / 16) + c] = (int8_t)coe;
+          d->e[ST_H1][b * (d->mstride[ST_H1] / 16) + c] = (int8_t)che;
         }
       }
     }
@@ -324,7 +342,11 @@ __global__ __launch_bounds__(64 * NW) void k_gu(LayerArgs a) {
     int sm = quantize16_lanes(gv / (1.0 + exp_f64(-gv)), se);
     // mlp = fp_quantize_vec(silu * u)                (full.py:290)
     int me;
-    int mm = quantize16_lanes(bfp_val(sm, se) * bfp_val(um, ue), me);
+    int mm = quantize16_lanes(bfp_val(sm, se) * bfp_val(um, ue), me, true);   // D's input
+    if (a.dump) {
+      canon16_lanes(gm, ge);      // values of g and u are no longer needed
+      canon16_lanes(um, ue);
+    }
     if (threadIdx.x < 16) {
       const int row = b * a.FFN + c * 16 + r;
       const int tile = b * (a.FFN / 16) + c;
@@ -370,24 +392,29 @@ __global__ __launch_bounds__(64 * NW) void k_d_res(LayerArgs a) {
     const int tile = b * (a.D / 16) + c;
     int e;
     int m = residual_lane(dmv, dev, a.h1_m[row], a.h1_e[tile], e);
+    int cdm = dmv, cde = dev, chm = m, che = e;
+    if (a.dump || a.hist_m) {
+      canon16_lanes(cdm, cde);
+      canon16_lanes(chm, che);
+    }
     if (threadIdx.x < 16) {
       a.h_m[row] = (int16_t)m;
       if (r == 0) a.h_e[tile] = (int8_t)e;
       if (a.dump) {
         const StageDump *d = a.dump;
-        d->m[ST_D][b * d->mstride[ST_D] + c * 16 + r] = (int16_t)dmv;
-        d->m[ST_HOUT][b * d->mstride[ST_HOUT] + c * 16 + r] = (int16_t)m;
+        d->m[ST_D][b * d->mstride[ST_D] + c * 16 + r] = (int16_t)cdm;
+        d->m[ST_HOUT][b * d->mstride[ST_HOUT] + c * 16 + r] = (int16_t)chm;
         if (r == 0) {
-          d->e[ST_D][b * (d->mstride[ST_D] / 16) + c] = (int8_t)dev;
-          d->e[ST_HOUT][b * (d->mstride[ST_HOUT] / 16) + c] = (int8_t)e;
+          d->e[ST_D][b * (d->mstride[ST_D] / 16) + c] = (int8_t)cde;
+          d->e[ST_HOUT][b * (d->mstride[ST_HOUT] / 16) + c] = (int8_t)che;
         }
       }
       if (a.hist_m) {
         const int pos = cur_pos(a);
         if (pos < a.hist_steps) {
           long long o = (((long long)b * a.hist_steps + pos) * a.NL + a.layer) * a.D;
-          a.hist_m[o + c * 16 + r] = (int16_t)m;
-          if (r == 0) a.hist_e[(o >> 4) + c] = (int8_t)e;
+          a.hist_m[o + c * 16 + r] = (int16_t)chm;
+          if (r == 0) a.hist_e[(o >> 4) + c] = (int8_t)che;
         }
       }
     }

@@ -141,7 +141,8 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
   M_out = M;
 }
 
-// Quantise the chunk's 16 rows (wave 0; lanes r and r+16k hold row r).
+// Quantise the chunk's 16 rows (wave 0; lanes r and r+16k hold row r): the
+// raw tile_quantize of the exact outputs, as fp_quantize_vec forms it.
 __device__ __forceinline__ void chunk_quant(long long A, int M, int &m, int &e) {
   int L = row_log2(A, M);
   L = xor_max(L, 1);
