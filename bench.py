@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--reps", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
+    ap.add_argument("--decode-reps", type=int, default=3)
     ap.add_argument("--probe", action="store_true",
                     help="also time a 1 GiB device copy and a 2 GiB streaming read "
                          "(practical HBM ceiling; the copy calibrates rocprof counters)")
@@ -164,6 +166,62 @@ def cpu_baseline(seconds):
                       + ", ".join(done) + f" in {total_t:.1f} s"}
 
 
+def decode_leg(reps):
+    """30-layer SmolLM2-135M-shaped random-init model,
+    8-token prompt, 64 greedy tokens.  Timed with HIP events inside
+    bfp_decode (device time of the steps that emit the 64 tokens, and of all
+    72 steps); tokens checked against the reference's own run
+    (tests/golden/ref_decode_cfg3.npz)."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    n_prompt, n_gen = 8, 64
+    d = Dims(MAX_CTX=n_prompt + n_gen)
+    fm = synth.make_model(d, seed=0)
+    prompt = synth.make_prompt(d, n_prompt, seed=0)
+    gm = BfpModel(d)
+    gm.load_fp32(fm)
+    toks, _ = gm.decode(prompt[None, :], n_gen)          # warm-up + graph build
+    gen_ms, tot_ms, walls = [], [], []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        toks, _ = gm.decode(prompt[None, :], n_gen)
+        walls.append(time.perf_counter() - t0)
+        t, g = gm.decode_time_ms()
+        tot_ms.append(t)
+        gen_ms.append(g)
+    gm.close()
+    ref = ROOT / "tests" / "golden" / "ref_decode_cfg3.npz"
+    exact = None
+    if ref.exists():
+        f = np.load(ref)
+        exact = bool(list(toks[0]) == [int(t) for t in f["tokens"]]
+                     and list(prompt) == [int(t) for t in f["prompt"]])
+    g = min(gen_ms)
+    return {"workload": "config 3: 30 layers, prompt 8, 64 greedy tokens, batch 1",
+            "tokens_per_s": round(n_gen / (g * 1e-3), 1),
+            "ms_per_token": round(g / n_gen, 4),
+            "steps_per_s_all": round((n_prompt + n_gen) / (min(tot_ms) * 1e-3), 1),
+            "wall_s_per_decode": round(min(walls), 4),
+            "tokens_match_reference": exact}
+
+
+def cpu_decode_baseline(max_steps=3):
+    """The oracle's faithful decode loop (full.py:432-443 restated), timed
+    on the first max_steps steps of config 3 on this host (1 thread)."""
+    from oracle import bfp_sim as sim
+    from bfp import Dims, synth
+    d = Dims(MAX_CTX=72)
+    om = sim.build_model(synth.make_model(d, seed=0))
+    prompt = [int(t) for t in synth.make_prompt(d, 8, seed=0)]
+    t0 = time.perf_counter()
+    sim.decode(om, prompt[:max_steps], 0, max_ctx=72)
+    dt = time.perf_counter() - t0
+    return {"value": round(max_steps / dt, 4), "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/bfp_sim.decode, first {max_steps} steps of config 3 "
+                      f"(30 layers) in {dt:.1f} s"}
+
+
 def stream_probe():
     """Practical HBM ceilings: a 1 GiB device-to-device copy (read + write
     bytes) and a streaming read (float32 sum over 2 GiB)."""
@@ -263,10 +321,15 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
     }
+    if not args.no_decode:
+        print("[bench] config 3 decode", file=sys.stderr, flush=True)
+        out["decode"] = decode_leg(args.decode_reps)
     if args.probe:
         out["stream_ceiling"] = stream_probe()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if not args.no_decode:
+            out["decode"]["cpu_baseline"] = cpu_decode_baseline()
     print(json.dumps(out), flush=True)
 
 
