@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
+    ap.add_argument("--decode-only", action="store_true", help="run only the config-3 decode leg")
     ap.add_argument("--decode-reps", type=int, default=3)
     ap.add_argument("--probe", action="store_true",
                     help="also time a 1 GiB device copy and a 2 GiB streaming read "
@@ -125,6 +126,19 @@ class ShapeCase:
             wm, we = sim.tile_quantize(sim.matvec_hw_golden(xm, xe, Wm, We))
             ok &= bool((ym[r] == wm.reshape(-1)).all() and (ye[r] == we).all())
         return ok
+
+
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE x calibration + WRITE_SIZE), or None."""
+    path = ROOT / "profiles" / "bfp_matvec_sweep.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return int(parts[2])
+    return None
 
 
 def kernel_config(n_in):
@@ -258,6 +272,9 @@ def main():
         sys.exit(1)
     from bfp import _lib
     _lib.lib()
+    if args.decode_only:
+        print(json.dumps({"decode": decode_leg(args.decode_reps)}), flush=True)
+        return
     print(f"[bench] building device rings for {len(SHAPES)} shapes x {args.reps} reps",
           file=sys.stderr, flush=True)
     cases = [ShapeCase(o, i, args.reps, seed=17 + k) for k, (o, i) in enumerate(SHAPES)]
@@ -319,7 +336,9 @@ def main():
         "per_shape": per_shape,
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(kname),
+                     "alg_bytes_per_launch": int(gbytes / nl)},
     }
     if not args.no_decode:
         print("[bench] config 3 decode", file=sys.stderr, flush=True)
