@@ -109,6 +109,49 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
 int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
                  const int16_t *x_m, const int8_t *x_e, int16_t *y_m, int8_t *y_e);
 
+/* ------------------------------------------------------- RTL-exact ops */
+/* The FPGA engines' bit-exact leaf ops (rtl/vc707/src/smollm/*_bfp.sv as
+ * specified by rtl/vc707/host/gen_*_bfp_golden.py).  Not on the
+ * model-level simulator's token path; per-op semantics of the hardware. */
+
+/* EXP_LUT[1024] (sim/gen_exp_lut.py:36-42), SILU_LUT[65536] indexed by the
+ * int16 code & 0xFFFF (sim/gen_swiglu_lut.py:27-44), FREQ_TURNS_Q31[hd/2]
+ * (sim/gen_rope_freq_table.py:31-37), built on the host; NULL skips one. */
+int bfp_rtl_tables(uint16_t *exp_lut, int16_t *silu_lut, uint32_t *freq_q31, int head_dim,
+                   double base);
+/* matvec_bfp_engine.sv (gen_matvec_bfp_golden.py:53-108): sequential
+ * tile alignment, 48-bit saturating accumulator, per-row (m, e).  W in the
+ * reference layout; y_e has one exponent per row. */
+int bfp_rtl_matvec_d(const int16_t *x_m, const int8_t *x_e, const int16_t *W_m, const int8_t *W_e,
+                     int n_out, int n_in, int16_t *y_m, int8_t *y_e, void *stream);
+/* requant_mant + chunk emax (smollm_layer_bfp.sv:1387-1396,1672-1693):
+ * per-lane exponents -> one exponent per 16 lanes. */
+int bfp_rtl_requant_d(const int16_t *m, const int8_t *e, int n, int16_t *out_m, int8_t *out_e,
+                      void *stream);
+/* rmsnorm_bfp.sv (gen_rmsnorm_bfp_golden.py:42-142) of batch vectors of D;
+ * gamma shared. */
+int bfp_rtl_rmsnorm_d(const int16_t *x_m, const int8_t *x_e, const int16_t *g_m, const int8_t *g_e,
+                      int D, int batch, int16_t *y_m, int8_t *y_e, void *stream);
+/* rope_bfp.sv + cordic_sincos.sv (gen_rope_bfp_golden.py:37-121) of n_heads
+ * 64-wide heads (x_e per 16-tile); y_e has one exponent per element. */
+int bfp_rtl_rope_d(const int16_t *x_m, const int8_t *x_e, int pos, int n_heads,
+                   const uint32_t *freq_q31, int16_t *y_m, int8_t *y_e, void *stream);
+/* softmax_bfp.sv (gen_softmax_bfp_golden.py:33-78): batch problems of n
+ * <= 4096 mantissas at x_m + b*stride sharing exponent x_e[b]; y_e[b]. */
+int bfp_rtl_softmax_d(const int16_t *x_m, const int8_t *x_e, int n, int batch, int stride,
+                      const uint16_t *exp_lut, int16_t *y_m, int8_t *y_e, void *stream);
+/* swiglu_bfp.sv (gen_swiglu_bfp_golden.py:43-78). */
+int bfp_rtl_swiglu_d(const int16_t *g_m, const int8_t *g_e, const int16_t *u_m, const int8_t *u_e,
+                     int n, const int16_t *silu_lut, int16_t *y_m, int8_t *y_e, void *stream);
+/* residual_bfp.sv (gen_residual_bfp_golden.py:23-48). */
+int bfp_rtl_residual_d(const int16_t *a_m, const int8_t *a_e, const int16_t *b_m,
+                       const int8_t *b_e, int n, int16_t *y_m, int8_t *y_e, void *stream);
+/* The decode head's bfp_gt running argmax (smollm_decode_head_bfp.sv:
+ * 253-274,322-324,399-430) over batch rows of n (m, e) pairs (one exponent
+ * per element); work: 3*batch*n/16 int32 of device scratch. */
+int bfp_rtl_argmax_d(const int16_t *m, const int8_t *e, int n, int batch, int32_t *work,
+                     int32_t *idx, void *stream);
+
 /* ------------------------------------------------------------- model */
 /* A context owns one GPU's copy of the model (BFP weights in the device
  * layout, float64 gammas, the float32 tied embedding, the RoPE table), the

@@ -1,0 +1,354 @@
+"""CPU oracle for the RTL-exact BFP leaf ops -- TEST INFRASTRUCTURE ONLY
+(same import rule as oracle/bfp_sim.py).
+
+The reference's hardware leaf ops are specified bit-for-bit by their Python
+golden generators under rtl/vc707/host/ and the LUT generators under
+rtl/vc707/sim/.  Each function below restates one of them with Python
+integers (the goldens are Python-int arithmetic) and cites the lines it
+follows.  Unlike the model-level simulator, these ops keep per-lane or
+per-element exponents and truncating shifts.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+TILE = 16
+ACC_W = 48
+
+
+def _low16(v: int) -> int:
+    """Two's-complement low 16 bits as a signed int (`sh & 0xFFFF`, sign fix)."""
+    m = v & 0xFFFF
+    return m - 0x10000 if m & 0x8000 else m
+
+
+def _clamp8(e: int) -> int:
+    return max(-128, min(127, e))
+
+
+def _lead(v: int) -> int:
+    return abs(v).bit_length() - 1 if v else 0
+
+
+def _norm16(v: int, lead: int):
+    """Leading-bit normalise: shift = lead - 14, mantissa = low 16 bits of
+    the shifted value.  Returns (m, shift)."""
+    sh = lead - 14
+    return _low16(v >> sh if sh >= 0 else v << (-sh)), sh
+
+
+# ------------------------------------------------------------------ matvec
+def rtl_matvec(x_m, x_e, W_m, W_e):
+    """matvec_bfp_engine.sv golden (gen_matvec_bfp_golden.py:53-108): per
+    row, tiles folded in order -- the side with the smaller exponent is
+    arithmetic-shifted right (zeroed past 47), added, and saturated to 48
+    bits; then a leading-bit normalise gives a per-row (m, e)."""
+    hi, lo = (1 << (ACC_W - 1)) - 1, -(1 << (ACC_W - 1))
+    n_out, nt = W_e.shape
+    out_m = np.zeros(n_out, np.int16)
+    out_e = np.zeros(n_out, np.int8)
+    for i in range(n_out):
+        acc = acc_e = 0
+        for t in range(nt):
+            s = int(np.dot(x_m[t].astype(np.int64), W_m[i, t].astype(np.int64)))
+            te = int(x_e[t]) + int(W_e[i, t])
+            if t == 0:
+                acc, acc_e = s, te
+                continue
+            d = te - acc_e
+            if d > 0:
+                acc = 0 if d > ACC_W - 1 else acc >> d
+                acc_e = te
+            elif d < 0:
+                s = 0 if -d > ACC_W - 1 else s >> (-d)
+            acc = max(lo, min(hi, acc + s))
+        m, sh = _norm16(acc, _lead(acc))
+        out_m[i] = m
+        out_e[i] = _clamp8(acc_e + sh - 15)
+    return out_m, out_e
+
+
+def rtl_requant(m, e):
+    """Per-lane exponents of a 16-lane chunk -> one tile exponent
+    (smollm_layer_bfp.sv:1387-1396 requant_mant, :1672-1693 emax):
+    emax = max(e); m >>> (emax - e), 0 when the shift is >= 16."""
+    m = np.asarray(m, np.int64).reshape(-1, TILE)
+    e = np.asarray(e, np.int64).reshape(-1, TILE)
+    emax = e.max(axis=1)
+    sh = emax[:, None] - e
+    out = np.where(sh >= 16, 0, m >> np.clip(sh, 0, 15))
+    return out.astype(np.int16).reshape(-1), emax.astype(np.int8)
+
+
+# ----------------------------------------------------------------- rmsnorm
+RMS_SEED_Q12_12 = {31: 2365, 30: 3344, 29: 4730, 28: 6689, 27: 9459, 26: 13377,
+                   25: 18919, 24: 26755, 23: 37837, 22: 53510, 21: 75674, 20: 107020,
+                   19: 151349, 18: 214040, 17: 302698, 16: 428079, 15: 605396,
+                   14: 856159, 13: 1210791, 12: 1712317, 11: 2421583, 10: 3424635,
+                   9: 4843165, 8: 6849270, 7: 9686330, 6: 13698540}
+"""rsqrt seed LUT of rmsnorm_bfp.sv, by msb of v (gen_rmsnorm_bfp_golden.py:34-38);
+other msbs seed with 2^24 - 1."""
+EPS_Q30 = 10737
+
+
+def rtl_rmsnorm(x_m, x_e, g_m, g_e):
+    """rmsnorm_bfp.sv golden (gen_rmsnorm_bfp_golden.py:42-142)."""
+    x_m = np.asarray(x_m, np.int64).reshape(-1, TILE)
+    g_m = np.asarray(g_m, np.int64).reshape(-1, TILE)
+    nt = x_m.shape[0]
+    D = nt * TILE
+    inv_d = (1 << 32) // D
+    sums = [int((x_m[t] * x_m[t]).sum()) for t in range(nt)]
+    exps = [2 * int(x_e[t]) for t in range(nt)]
+    acc, acc_e = sums[0], exps[0]
+    for t in range(1, nt):
+        d = exps[t] - acc_e
+        if d > 0:
+            acc = 0 if d > ACC_W - 1 else acc >> d
+            acc_e = exps[t]
+            acc += sums[t]
+        elif d < 0:
+            acc += (sums[t] >> -d) if -d <= ACC_W - 1 else 0
+        else:
+            acc += sums[t]
+    mean = (acc * inv_d) >> 32
+    lead = _lead(mean)
+    if (acc_e + lead) & 1:
+        lead -= 1
+    v = (mean >> (lead - 30) if lead >= 30 else mean << (30 - lead)) + EPS_Q30
+    inv = RMS_SEED_Q12_12.get(_lead(v), (1 << 24) - 1)
+    C = (3 * (1 << 30)) // 2
+    for _ in range(3):
+        vy2 = (v * inv * inv) >> 24
+        corr = 0 if vy2 >= (1 << 32) else max(0, C - (vy2 >> 1))
+        inv = min((inv * corr + (1 << 29)) >> 30, (1 << 24) - 1)
+    e_inv = (30 - acc_e - lead) >> 1
+    out_m = np.zeros(D, np.int16)
+    out_e = np.zeros(nt, np.int8)
+    for t in range(nt):
+        prods = [int(x_m[t, k]) * int(g_m[t, k]) * inv for k in range(TILE)]
+        ml = max([_lead(p) for p in prods if p] or [0])
+        for k in range(TILE):
+            out_m[t * TILE + k], sh = _norm16(prods[k], ml)
+        out_e[t] = _clamp8(int(x_e[t]) + int(g_e[t]) + e_inv + (ml - 14) - 27)
+    return out_m, out_e
+
+
+# -------------------------------------------------------------------- rope
+PI_HALF_Q27 = 210828714
+PI_Q27 = 421657428
+PI_OVER_8_Q29 = 210828714
+K_Q3_27 = 81504109
+ATAN_Q3_27 = [105414357, 62229729, 32880480, 16690645, 8377711, 4192939, 2096981, 1048555,
+              524285, 262144, 131072, 65536, 32768, 16384, 8192, 4096]
+"""CORDIC constants of cordic_sincos.sv (gen_rope_bfp_golden.py:28-34)."""
+
+
+def rope_freq_turns(base=10000.0, head_dim=64):
+    """FREQ_TURNS_Q31 (sim/gen_rope_freq_table.py:31-37): round(freq/(2 pi)
+    * 2^31) with freq = 1/base^(2j/head_dim)."""
+    out = []
+    for j in range(head_dim // 2):
+        f = 1.0 / (base ** (2.0 * j / head_dim))
+        out.append(round(f / (2.0 * math.pi) * (1 << 31)))
+    return out
+
+
+def cordic_sincos(a):
+    """16-iteration Q3.27 CORDIC (gen_rope_bfp_golden.py:37-60) -> Q1.15
+    (cos, sin)."""
+    if a > PI_HALF_Q27:
+        z, neg = PI_Q27 - a, True
+    elif a < -PI_HALF_Q27:
+        z, neg = -PI_Q27 - a, True
+    else:
+        z, neg = a, False
+    x, y = K_Q3_27, 0
+    for i in range(16):
+        xs, ys = x >> i, y >> i
+        if z >= 0:
+            x, y, z = x - ys, y + xs, z - ATAN_Q3_27[i]
+        else:
+            x, y, z = x + ys, y - xs, z + ATAN_Q3_27[i]
+    xr, yr = (x + 2048) >> 12, (y + 2048) >> 12
+    if xr > 32767:
+        c = -32767 if neg else 32767
+    elif xr < -32768:
+        c = 32767 if neg else -32768
+    else:
+        c = -xr if neg else xr
+    s = max(-32768, min(32767, yr))
+    return c, s
+
+
+def _wrap31(v):
+    v &= (1 << 31) - 1
+    return v - (1 << 31) if v & (1 << 30) else v
+
+
+def rope_angle_q27(pos, freq_q31):
+    """Angle of pair j at pos in Q3.27 (gen_rope_bfp_golden.py:77-83)."""
+    turns = _wrap31(pos * freq_q31)
+    return _wrap31((turns * PI_OVER_8_Q29) >> 29)
+
+
+def rtl_rope(x_m, x_e, pos, freq):
+    """rope_bfp.sv golden (gen_rope_bfp_golden.py:72-121) for one 64-wide
+    head: pair (j, j+32) aligned to its larger exponent (>>, 0 when >= 16),
+    rotated by the CORDIC (cos, sin), re-normalised per element.  Returns
+    (m (64,), e (64,)) -- one exponent per element."""
+    x_m = np.asarray(x_m, np.int64).reshape(-1)
+    x_e = np.asarray(x_e, np.int64).reshape(-1)
+    hd = x_m.size
+    h2 = hd // 2
+    prod = [0] * hd
+    ee = [0] * hd
+    for j in range(h2):
+        c, s = cordic_sincos(rope_angle_q27(pos, freq[j]))
+        a, b = int(x_m[j]), int(x_m[j + h2])
+        ea, eb = int(x_e[j // TILE]), int(x_e[(j + h2) // TILE])
+        em = max(ea, eb)
+        aa = a >> (em - ea) if em - ea < 16 else 0
+        ba = b >> (em - eb) if em - eb < 16 else 0
+        prod[j] = aa * c - ba * s
+        prod[j + h2] = ba * c + aa * s
+        ee[j] = ee[j + h2] = em
+    out_m = np.zeros(hd, np.int16)
+    out_e = np.zeros(hd, np.int8)
+    for k in range(hd):
+        out_m[k], sh = _norm16(prod[k], _lead(prod[k]))
+        out_e[k] = _clamp8(ee[k] + sh - 15)
+    return out_m, out_e
+
+
+# ----------------------------------------------------------------- softmax
+def exp_lut():
+    """EXP_LUT[i] = round(exp((i - 1023)/128) * 32768), clamped to uint16
+    (sim/gen_exp_lut.py:36-42)."""
+    return [min(65535, max(0, round(math.exp((i - 1023) / 128.0) * 32768))) for i in range(1024)]
+
+
+def rtl_softmax(x_m, e_shared, n, lut):
+    """softmax_bfp.sv golden (gen_softmax_bfp_golden.py:33-78): LUT exp of
+    the shifted difference to the max, 4-step Newton-Raphson reciprocal,
+    one shared output exponent.  Returns (m (n,), e)."""
+    xs = [int(v) for v in np.asarray(x_m).reshape(-1)[:n]]
+    mx = max(xs)
+    sh = e_shared - 8
+    vals = []
+    for v in xs:
+        d = v - mx
+        ds = d << sh if sh >= 0 else d >> (-sh)
+        idx = 1023 if ds >= 0 else (0 if ds <= -1023 else ds + 1023)
+        vals.append(int(lut[idx]))
+    tot = sum(vals)
+    y = 1 << (31 - _lead(tot))
+    for _ in range(4):
+        y = (y * ((1 << 33) - tot * y)) >> 32
+    prods = [v * y for v in vals]
+    ml = max([_lead(p) for p in prods if p] or [0])
+    out = np.array([_norm16(p, ml)[0] for p in prods], np.int16)
+    return out, _clamp8(ml - 14 - 17)
+
+
+def rtl_score_prealign(s_m, s_e, n):
+    """The layer's pre-align of QK scores before the softmax
+    (smollm_layer_bfp.sv:2038-2053): each score (per-timestep exponent)
+    shifted to the shared max exponent (0 when >= 16); the shared exponent
+    drops by 3 for 1/sqrt(64)."""
+    s_m = [int(v) for v in np.asarray(s_m).reshape(-1)[:n]]
+    s_e = [int(v) for v in np.asarray(s_e).reshape(-1)[:n]]
+    es = max(s_e)
+    m = [0 if es - e >= 16 else v >> (es - e) for v, e in zip(s_m, s_e)]
+    return np.array(m, np.int16), es - 3
+
+
+# ------------------------------------------------------------------ swiglu
+SILU_LUT_SCALE_LOG2 = 5
+
+
+def silu_lut():
+    """SILU_LUT over all 65536 int16 codes (sim/gen_swiglu_lut.py:27-44):
+    x = code/32768 * 32, silu(x) = x * (1/(1 + exp(-x))), back to Q at
+    scale 32 with round-half-even, clipped.  Indexed by code & 0xFFFF."""
+    code = np.arange(65536, dtype=np.uint16).view(np.int16).astype(np.float64)
+    g = code / 32768.0 * 32.0
+    s = g * (1.0 / (1.0 + np.exp(-g)))
+    return np.clip(np.round(s * 32768.0 / 32.0).astype(np.int64), -32768, 32767).astype(np.int16)
+
+
+def rtl_swiglu(g_m, g_e, u_m, u_e, lut):
+    """swiglu_bfp.sv golden (gen_swiglu_bfp_golden.py:43-78)."""
+    g_m = np.asarray(g_m, np.int64).reshape(-1, TILE)
+    u_m = np.asarray(u_m, np.int64).reshape(-1, TILE)
+    nt = g_m.shape[0]
+    out_m = np.zeros(nt * TILE, np.int16)
+    out_e = np.zeros(nt, np.int8)
+    for t in range(nt):
+        sh = int(g_e[t]) - SILU_LUT_SCALE_LOG2
+        prods = []
+        for k in range(TILE):
+            mg = int(g_m[t, k])
+            idx = mg << sh if sh >= 0 else mg >> (-sh)
+            idx = max(-32768, min(32767, idx))
+            prods.append(int(lut[idx & 0xFFFF]) * int(u_m[t, k]))
+        ml = max([_lead(p) for p in prods if p] or [0])
+        for k in range(TILE):
+            out_m[t * TILE + k], s = _norm16(prods[k], ml)
+        out_e[t] = _clamp8(int(u_e[t]) + (ml - 14) - 10)
+    return out_m, out_e
+
+
+# ---------------------------------------------------------------- residual
+def rtl_residual(a_m, a_e, b_m, b_e):
+    """residual_bfp.sv golden (gen_residual_bfp_golden.py:23-48)."""
+    a_m = np.asarray(a_m, np.int64).reshape(-1, TILE)
+    b_m = np.asarray(b_m, np.int64).reshape(-1, TILE)
+    nt = a_m.shape[0]
+    out_m = np.zeros(nt * TILE, np.int16)
+    out_e = np.zeros(nt, np.int8)
+    for t in range(nt):
+        ea, eb = int(a_e[t]), int(b_e[t])
+        em = max(ea, eb)
+        sums = []
+        for k in range(TILE):
+            av = int(a_m[t, k]) >> (em - ea) if em - ea < 16 else 0
+            bv = int(b_m[t, k]) >> (em - eb) if em - eb < 16 else 0
+            sums.append(av + bv)
+        ml = max([_lead(s) for s in sums if s] or [0])
+        for k in range(TILE):
+            out_m[t * TILE + k], sh = _norm16(sums[k], ml)
+        out_e[t] = _clamp8(em + ml - 14)
+    return out_m, out_e
+
+
+# ------------------------------------------------------------------ argmax
+def bfp_gt(ma, ea, mb, eb):
+    """(ma, ea) > (mb, eb) after aligning to the larger exponent
+    (smollm_decode_head_bfp.sv:253-274)."""
+    de = ea - eb
+    if de == 0:
+        return ma > mb
+    if de > 0:
+        return ma > (0 if de >= 16 else mb >> de)
+    return (0 if -de >= 16 else ma >> -de) > mb
+
+
+def rtl_argmax(m, e):
+    """The decode head's running argmax (smollm_decode_head_bfp.sv:322-324,
+    399-430): per 16-lane chunk, a local best starting at lane 0 replaced on
+    strict bfp_gt; chunks folded into a global best that starts at
+    (-32768, -128), also on strict bfp_gt.  m, e: one per row."""
+    m = [int(v) for v in np.asarray(m).reshape(-1)]
+    e = [int(v) for v in np.asarray(e).reshape(-1)]
+    best_m, best_e, best_i = -32768, -128, 0
+    for c in range(len(m) // TILE):
+        lm, le, li = m[c * TILE], e[c * TILE], 0
+        for k in range(1, TILE):
+            if bfp_gt(m[c * TILE + k], e[c * TILE + k], lm, le):
+                lm, le, li = m[c * TILE + k], e[c * TILE + k], k
+        if bfp_gt(lm, le, best_m, best_e):
+            best_m, best_e, best_i = lm, le, c * TILE + li
+    return best_i

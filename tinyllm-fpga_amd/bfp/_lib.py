@@ -55,6 +55,15 @@ SIGNATURES = {
     "bfp_matvec_ring_d": (i32, [vp, vp, i32, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64,
                                 i32, vp]),
     "bfp_matvec_h": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+    "bfp_rtl_tables": (i32, [vp, vp, vp, i32, C.c_double]),
+    "bfp_rtl_matvec_d": (i32, [vp, vp, vp, vp, i32, i32, vp, vp, vp]),
+    "bfp_rtl_requant_d": (i32, [vp, vp, i32, vp, vp, vp]),
+    "bfp_rtl_rmsnorm_d": (i32, [vp, vp, vp, vp, i32, i32, vp, vp, vp]),
+    "bfp_rtl_rope_d": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+    "bfp_rtl_softmax_d": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp]),
+    "bfp_rtl_swiglu_d": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, vp]),
+    "bfp_rtl_residual_d": (i32, [vp, vp, vp, vp, i32, vp, vp, vp]),
+    "bfp_rtl_argmax_d": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "bfp_create": (vp, [C.POINTER(DimsC), i32, i32]),
     "bfp_destroy": (None, [vp]),
     "bfp_get_dims": (i32, [vp, C.POINTER(DimsC)]),
