@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-3 decode leg")
     ap.add_argument("--decode-reps", type=int, default=3)
+    ap.add_argument("--long", action="store_true", help="also run config 4 (long context)")
+    ap.add_argument("--batch64", action="store_true", help="also run config 5 (batch 64)")
     ap.add_argument("--probe", action="store_true",
                     help="also time a 1 GiB device copy and a 2 GiB streaming read "
                          "(practical HBM ceiling; the copy calibrates rocprof counters)")
@@ -220,6 +222,57 @@ def decode_leg(reps):
             "tokens_match_reference": exact}
 
 
+def long_context_leg():
+    """30 layers, 48-token prompt, greedy decode through
+    position 2047 (2000 new tokens); tokens/s overall and per position
+    window from per-step HIP events."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    n_prompt, n_gen = 48, 2000
+    d = Dims(MAX_CTX=2048)
+    gm = BfpModel(d)
+    gm.load_fp32(synth.make_model(d, seed=0))
+    prompt = synth.make_prompt(d, n_prompt, seed=4)
+    gm.decode(prompt[None, :], 16)                       # warm-up
+    gm.decode(prompt[None, :], n_gen, step_times=True)
+    st = gm.step_times_ms()
+    t, g = gm.decode_time_ms()
+    gm.close()
+    win = {}
+    for lo, hi in ((48, 112), (496, 560), (1008, 1072), (1984, 2048)):
+        win[f"pos_{lo}_{hi - 1}"] = round((hi - lo) / (float(st[lo:hi].sum()) * 1e-3), 1)
+    return {"workload": "config 4: 30 layers, prompt 48, decode to position 2047 (2000 tokens)",
+            "tokens_per_s": round(n_gen / (g * 1e-3), 1), "ms_per_token_mean": round(g / n_gen, 4),
+            "tokens_per_s_by_position": win}
+
+
+def batch_leg():
+    """64 independent sequences, 8-token prompts, 128
+    greedy tokens each; aggregate tokens/s.  Sequence 0 uses config 3's
+    prompt: its first 64 tokens must equal the reference's config-3 tokens."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    B, n_prompt, n_gen = 64, 8, 128
+    d = Dims(MAX_CTX=n_prompt + n_gen)
+    gm = BfpModel(d, max_batch=B)
+    gm.load_fp32(synth.make_model(d, seed=0))
+    prompts = np.stack([synth.make_prompt(d, n_prompt, seed=0)] +
+                       [synth.make_prompt(d, n_prompt, seed=1000 + b) for b in range(1, B)])
+    gm.decode(prompts, 4)                                # warm-up
+    toks, _ = gm.decode(prompts, n_gen)
+    t, g = gm.decode_time_ms()
+    gm.close()
+    ref = ROOT / "tests" / "golden" / "ref_decode_cfg3.npz"
+    exact = None
+    if ref.exists():
+        exact = bool(list(toks[0][:64]) == [int(x) for x in np.load(ref)["tokens"]])
+    return {"workload": "config 5: 64 sequences, prompt 8, 128 greedy tokens each",
+            "tokens_per_s": round(B * n_gen / (g * 1e-3), 1),
+            "ms_per_step": round(g / n_gen, 4), "seq0_matches_reference": exact}
+
+
 def cpu_decode_baseline(max_steps=3):
     """The oracle's faithful decode loop (full.py:432-443 restated), timed
     on the first max_steps steps of config 3 on this host (1 thread)."""
@@ -273,7 +326,12 @@ def main():
     from bfp import _lib
     _lib.lib()
     if args.decode_only:
-        print(json.dumps({"decode": decode_leg(args.decode_reps)}), flush=True)
+        res = {"decode": decode_leg(args.decode_reps)}
+        if args.long:
+            res["long_context"] = long_context_leg()
+        if args.batch64:
+            res["batch64"] = batch_leg()
+        print(json.dumps(res), flush=True)
         return
     print(f"[bench] building device rings for {len(SHAPES)} shapes x {args.reps} reps",
           file=sys.stderr, flush=True)
@@ -343,6 +401,10 @@ def main():
     if not args.no_decode:
         print("[bench] config 3 decode", file=sys.stderr, flush=True)
         out["decode"] = decode_leg(args.decode_reps)
+        if args.long:
+            out["long_context"] = long_context_leg()
+        if args.batch64:
+            out["batch64"] = batch_leg()
     if args.probe:
         out["stream_ceiling"] = stream_probe()
     if not args.no_cpu:

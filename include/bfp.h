@@ -211,12 +211,16 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * output at every step, (batch, n_prompt + n_gen, NL, D) / (..., D/16).
  * The KV cache is overwritten from position 0. */
 #define BFP_DECODE_NO_GRAPH 1
+#define BFP_DECODE_STEP_TIMES 2   /* record one HIP event per step */
 int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int batch,
                int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags);
 
 /* Device time (HIP events) of the last bfp_decode: all steps, and the steps
  * from n_prompt on. */
 int bfp_decode_time(const bfp_ctx *ctx, float *total_ms, float *gen_ms);
+/* Per-step device times of the last decode run with BFP_DECODE_STEP_TIMES;
+ * copies up to n values, returns the number of steps recorded. */
+int bfp_decode_step_times(const bfp_ctx *ctx, float *ms, int n);
 
 #ifdef __cplusplus
 }

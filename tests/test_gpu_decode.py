@@ -95,3 +95,38 @@ def test_decode_errors(gpu):
     with pytest.raises(BfpError):
         gm.decode(np.array([[1, 2]]), d.MAX_CTX)       # beyond the KV capacity
     gm.close()
+
+
+def test_decode_long_context(gpu):
+    """BASELINE config 4's positions on a 2-layer model: a 48-token prompt,
+    then greedy decode through position 2047 (KV cache of 2048 positions,
+    softmax over up to 2048 scores), every layer output at every step
+    against the oracle."""
+    cfg = dict(TINY, MAX_CTX=2048)
+    d, om, gm = _setup(cfg, seed=11)
+    from bfp import synth
+    prompt = synth.make_prompt(d, 48, seed=11)
+    n_gen = 2048 - 48
+    print("[decode] long context: oracle", flush=True)
+    want, whm, whe = _oracle_decode(om, prompt, n_gen)
+    print("[decode] long context: gpu", flush=True)
+    toks, (hm, he) = gm.decode(prompt[None, :], n_gen, hist=True)
+    bad = [s for s in range(2048) if not ((hm[0, s] == whm[s]).all() and (he[0, s] == whe[s]).all())]
+    assert not bad, f"steps with differing layer outputs: {bad[:10]}"
+    assert list(toks[0]) == list(want)
+    gm.close()
+
+
+def test_decode_batch64_matches_single(gpu):
+    """64 independent sequences in one decode equal their single-sequence
+    decodes (and sequence 0 the oracle)."""
+    d, om, gm = _setup(TINY, seed=12, max_batch=64)
+    from bfp import synth
+    prompts = np.stack([synth.make_prompt(d, 8, seed=100 + b) for b in range(64)])
+    toks, _ = gm.decode(prompts, 12)
+    for b in (0, 1, 31, 63):
+        single, _ = gm.decode(prompts[b:b + 1], 12)
+        assert list(single[0]) == list(toks[b]), b
+    want, _, _ = _oracle_decode(om, prompts[0], 12)
+    assert list(toks[0]) == list(want)
+    gm.close()

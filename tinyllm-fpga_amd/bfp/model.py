@@ -153,7 +153,7 @@ class BfpModel:
         return am, lg
 
     # --------------------------------------------------------------- decode
-    def decode(self, prompts, n_gen, hist=False, graph=True):
+    def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False):
         """Greedy decode (full.py:426-443) of a batch of prompts
         (batch, n_prompt).  Returns (tokens (batch, n_gen), hist) where hist
         is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16))."""
@@ -166,9 +166,18 @@ class BfpModel:
             steps = n_prompt + n_gen
             hm = np.zeros((batch, steps, d.NL, d.D), np.int16)
             he = np.zeros((batch, steps, d.NL, d.D // 16), np.int8)
+        flags = (0 if graph else 1) | (2 if step_times else 0)
         call("bfp_decode", self._h, _p(P), n_prompt, n_gen, batch, _p(toks),
-             _p(hm) if hist else None, _p(he) if hist else None, 0 if graph else 1)
+             _p(hm) if hist else None, _p(he) if hist else None, flags)
         return toks[:, :n_gen], ((hm, he) if hist else None)
+
+    def step_times_ms(self):
+        """Per-step device times of the last decode(step_times=True)."""
+        n = lib().bfp_decode_step_times(self._h, None, 0)
+        out = np.zeros(max(n, 0), np.float32)
+        if n > 0:
+            lib().bfp_decode_step_times(self._h, _p(out), n)
+        return out
 
     def decode_time_ms(self):
         t, g = C.c_float(), C.c_float()

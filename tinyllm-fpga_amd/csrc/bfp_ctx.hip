@@ -38,6 +38,7 @@ struct bfp_ctx {
   StageDump *dump_dev = nullptr;
   std::vector<void *> allocs;
   float last_decode_ms = 0.f, last_gen_ms = 0.f;
+  std::vector<float> step_ms;   // per-step device time of the last decode (BFP_DECODE_STEP_TIMES)
 
   int alloc(void **p, size_t bytes) {
     *p = nullptr;
@@ -533,6 +534,12 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     }
   }
   hipEvent_t ev0 = nullptr, ev1 = nullptr, evg = nullptr;
+  const bool per_step = (flags & BFP_DECODE_STEP_TIMES) != 0;
+  std::vector<hipEvent_t> sev;
+  if (per_step) {
+    sev.resize(steps + 1, nullptr);
+    for (auto &e : sev) (void)hipEventCreate(&e);
+  }
   if (!rc) {
     (void)hipEventCreate(&ev0);
     (void)hipEventCreate(&ev1);
@@ -541,6 +548,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     for (int step = 0; step < steps && !rc; ++step) {
       const bool head = step >= n_prompt - 1;
       if (step == n_prompt) (void)hipEventRecord(evg, s);
+      if (per_step) (void)hipEventRecord(sev[step], s);
       if (use_graph) {
         hipError_t e = hipGraphLaunch(ex[head ? 1 : 0], s);
         if (e != hipSuccess) rc = set_err(BFP_EIO, "graph launch: %s", hipGetErrorString(e));
@@ -549,6 +557,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
       }
     }
     if (n_gen == 0) (void)hipEventRecord(evg, s);
+    if (per_step) (void)hipEventRecord(sev[steps], s);
     (void)hipEventRecord(ev1, s);
   }
   if (!rc) {
@@ -561,7 +570,14 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     (void)hipEventElapsedTime(&gms, evg, ev1);
     c->last_decode_ms = ms;
     c->last_gen_ms = gms;
+    c->step_ms.clear();
+    if (per_step) {
+      c->step_ms.resize(steps);
+      for (int k = 0; k < steps; ++k) (void)hipEventElapsedTime(&c->step_ms[k], sev[k], sev[k + 1]);
+    }
   }
+  for (auto &e : sev)
+    if (e) (void)hipEventDestroy(e);
   for (int k = 0; k < 2; ++k) {
     if (ex[k]) (void)hipGraphExecDestroy(ex[k]);
     if (gr[k]) (void)hipGraphDestroy(gr[k]);
