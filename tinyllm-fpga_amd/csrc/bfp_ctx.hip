@@ -595,6 +595,15 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   return BFP_OK;
 }
 
+// Per-step device times of the last bfp_decode run with BFP_DECODE_STEP_TIMES:
+// copies min(n, steps) values and returns how many were recorded.
+int bfp_decode_step_times(const bfp_ctx *c, float *ms, int n) {
+  if (!c || (!ms && n > 0)) return set_err(BFP_EINVAL, "null argument");
+  const int k = (int)c->step_ms.size();
+  for (int i = 0; i < k && i < n; ++i) ms[i] = c->step_ms[i];
+  return k;
+}
+
 // Device time of the last bfp_decode: all steps, and the steps from
 // n_prompt on (the generated tokens).
 int bfp_decode_time(const bfp_ctx *c, float *total_ms, float *gen_ms) {
