@@ -110,7 +110,7 @@ int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
                  const int16_t *x_m, const int8_t *x_e, int16_t *y_m, int8_t *y_e);
 
 /* ------------------------------------------------------- RTL-exact ops */
-/* The FPGA engines' bit-exact leaf ops (rtl/vc707/src/smollm/*_bfp.sv as
+/* The FPGA engines' bit-exact leaf ops (rtl/vc707/src/smollm/<op>_bfp.sv as
  * specified by rtl/vc707/host/gen_*_bfp_golden.py).  Not on the
  * model-level simulator's token path; per-op semantics of the hardware. */
 
