@@ -219,6 +219,10 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
     delete c;
     return nullptr;
   }
+  if (prepare_layer_kernels(c->max_ctx)) {
+    delete c;
+    return nullptr;
+  }
   // s_kv_m counts elements; the mantissa arrays are int16
   if (hipMemcpy(c->rope, rope.data(), sizeof(double) * rope.size(), hipMemcpyHostToDevice) !=
           hipSuccess ||

@@ -116,6 +116,40 @@ __device__ inline double ddot64_skx(const double *x, const double *y) {
   return (s[0] + s[2]) + (s[1] + s[3]);
 }
 
+// The same dot product with the second operand a BFP 64-vector: mantissas
+// km (8 x uint4, 8 int16 each), the 4 tile exponents packed little-endian
+// in ke4.  Each element is decoded exactly
+// (m * 2^(e-15)) before its FMA, so the result equals ddot64_skx(x, y).
+__device__ inline double ddot64_skx_bfp(const double *x, const uint4 *__restrict__ km, int ke4) {
+  double acc[4][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint4 u = km[4 * h + r];
+      const int ex = (int)(signed char)((ke4 >> (8 * (2 * h + (r >> 1)))) & 0xff);
+      const double s = ldexp(1.0, ex - 15);
+      const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const int m = (int)(short)((w[l >> 1] >> (16 * (l & 1))) & 0xffff);
+        const double y = (double)m * s;
+        acc[r][l] = fma(x[32 * h + 8 * r + l], y, h == 0 ? 0.0 : acc[r][l]);
+      }
+    }
+  }
+  double s4[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    double f0 = acc[0][l] + acc[0][l + 4];
+    double f1 = acc[1][l] + acc[1][l + 4];
+    double f2 = acc[2][l] + acc[2][l + 4];
+    double f3 = acc[3][l] + acc[3][l + 4];
+    s4[l] = ((f0 + f1) + f2) + f3;
+  }
+  return (s4[0] + s4[2]) + (s4[1] + s4[3]);
+}
+
 // --------------------------------------------------------------- exp
 // np.exp is numpy's own SIMD exp (not correctly rounded for ~5% of inputs);
 // the device uses the ROCm device library's exp.  The two may differ in the

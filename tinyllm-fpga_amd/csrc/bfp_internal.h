@@ -66,6 +66,7 @@ struct HeadArgs;
 struct CtlArgs;
 struct EmbedArgs;
 int launch_layer(const LayerArgs &a, hipStream_t s);
+int prepare_layer_kernels(int max_ctx);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);
 int launch_ctl(const CtlArgs &a, hipStream_t s);

@@ -131,14 +131,51 @@ __device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
   return quantize16_lanes(out, e);
 }
 
-__global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
+// Attention of one q head (full.py:268-283) in one workgroup of ATT_WAVES
+// waves:
+//  1. waves 0-2: RoPE of q (head hq) and k (group g), v of group g; the
+//     writer workgroup of the group stores k, v at slot pos of the KV cache;
+//  2. all threads: scores[t] = np.dot(q, K[t]) / sqrt(HD), one position per
+//     thread, in OpenBLAS's SkylakeX ddot order;
+//  3. softmax: exp(s - max) / pairwise_sum (numpy's order);
+//  4. attn = sum_t p[t] * V[t] in ascending t from 0.0 (numpy's
+//     `attn[h] += p[t] * V[t]` loop, full.py:280-281).  The products are
+//     independent and are formed by waves 1.. into an LDS double buffer of
+//     TB positions while wave 0 runs the (inherently sequential) add chain
+//     over the previous block, one dimension per lane.  V is prefetched into
+//     registers ATT_DEPTH blocks ahead.
+constexpr int ATT_WAVES = 8;
+
+size_t attn_lds_bytes(int max_ctx, int ppw) {
+  const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
+  return (256 + sc_len) * 8 + (size_t)(ATT_WAVES - 1) * ppw * 64 * 8 * 2;
+}
+
+// One K row of the cache (64 mantissas, 4 tile exponents) in registers.
+struct KRow {
+  uint4 m[8];
+  int e4;
+};
+__device__ __forceinline__ void load_krow(KRow &r, const int16_t *Km, const int8_t *Ke, long long o) {
+  const uint4 *p = reinterpret_cast<const uint4 *>(Km + o);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.m[i] = p[i];
+  r.e4 = *reinterpret_cast<const int *>(Ke + (o >> 4));
+}
+
+template <int PPW>
+__global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
+  constexpr int TB = (ATT_WAVES - 1) * PPW;   // positions per AV block (even)
+  constexpr int ATT_DEPTH = PPW;               // V blocks in flight
+  constexpr int NT = 64 * ATT_WAVES;
   extern __shared__ double dsm[];
   double *q = dsm;                  // 64
   double *kc = dsm + 64;            // 64 (current position, post-rope)
   double *vc = dsm + 128;           // 64
-  double *leaf = dsm + 192;         // PW_MAX_LEAVES
-  double *sc = leaf + PW_MAX_LEAVES;   // max_ctx
-  __shared__ double red[4];
+  double *leaf = dsm + 192;         // PW_MAX_LEAVES (= 64)
+  double *sc = dsm + 256;           // max_ctx, rounded up to even
+  double2 *buf = reinterpret_cast<double2 *>(sc + ((a.max_ctx + 1) & ~1));   // 2 x TB/2 x 64
+  __shared__ double red[ATT_WAVES];
   const int hq = blockIdx.x, b = blockIdx.y;
   const int grp = a.H_Q / a.H_KV, g = hq / grp;
   const int HD = 64;
@@ -155,6 +192,25 @@ __global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
   int16_t *Vm = a.v_m + (long long)b * a.max_ctx * kv_tok;
   int8_t *Ve = a.v_e + (long long)b * a.max_ctx * (kv_tok / 16);
   const bool writer = (hq % grp) == 0;
+
+  // V prefetch ring of the AV phase (filled after the scores).  Producer
+  // wave pw (waves 1..) owns positions k*TB + pw*PPW + pp, pp < PPW, of
+  // block k; lane (pp = l/8, c = l%8) holds dimensions 8c..8c+7 of its
+  // position: one 16-byte mantissa load and one exponent byte per block.
+  // Every wave issues the same loads on every path (positions past the end
+  // are clamped to a valid row and their products zeroed; wave 0 loads a
+  // copy it does not use), so the compiler can count ATT_DEPTH blocks of
+  // loads in flight instead of draining them.
+  const int pw = w >= 1 ? w - 1 : 0, pp = l >> 3, pc = l & 7;
+  uint4 rm[ATT_DEPTH];
+  int re[ATT_DEPTH];
+  auto load_blk = [&](int k, uint4 &m, int &e) {
+    int t = k * TB + pw * PPW + (pp < PPW ? pp : 0);
+    t = t < n ? t : n - 1;
+    const long long o = ((long long)t * a.H_KV + g) * HD + 8 * pc;
+    m = *reinterpret_cast<const uint4 *>(Vm + o);
+    e = Ve[o >> 4];
+  };
 
   if (w == 0) {            // q head hq
     int idx = hq * HD + l;
@@ -196,47 +252,89 @@ __global__ __launch_bounds__(256) void k_attn(LayerArgs a) {
   }
   __syncthreads();
 
-  // scores[t] = float(np.dot(q, K[t])) / sqrt(HD)   (full.py:277-278)
-  for (int t = tid; t < n; t += blockDim.x) {
-    double kt[64];
-    if (t == pos) {
-#pragma unroll
-      for (int i = 0; i < 64; ++i) kt[i] = kc[i];
-    } else {
-      const long long o = ((long long)t * a.H_KV + g) * HD;
-      const int16_t *km = Km + o;
-      const int8_t *ke = Ke + (o >> 4);
-#pragma unroll
-      for (int i = 0; i < 64; ++i) kt[i] = bfp_val(km[i], ke[i >> 4]);
+  // scores[t] = float(np.dot(q, K[t])) / sqrt(HD)   (full.py:277-278), one
+  // position per thread, two rows in flight.  Row pos is read from global
+  // memory like the others (the writer may not have stored it yet) and its
+  // score is recomputed from LDS afterwards by the same thread.
+  {
+    KRow ra, rb;
+    const int last = n - 1;
+    load_krow(ra, Km, Ke, ((long long)(tid < n ? tid : last) * a.H_KV + g) * HD);
+    for (int t = tid; t < n; t += 2 * NT) {
+      const int t1 = t + NT, t2 = t + 2 * NT;
+      load_krow(rb, Km, Ke, ((long long)(t1 < n ? t1 : last) * a.H_KV + g) * HD);
+      sc[t] = ddot64_skx_bfp(q, ra.m, ra.e4) / a.inv_sqrt_hd_div;
+      load_krow(ra, Km, Ke, ((long long)(t2 < n ? t2 : last) * a.H_KV + g) * HD);
+      const double s1 = ddot64_skx_bfp(q, rb.m, rb.e4) / a.inv_sqrt_hd_div;
+      if (t1 < n) sc[t1] = s1;
     }
-    sc[t] = ddot64_skx(q, kt) / a.inv_sqrt_hd_div;
+    if (tid == pos % NT) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
   }
+#pragma unroll
+  for (int d = 0; d < ATT_DEPTH; ++d) load_blk(d, rm[d], re[d]);   // overlaps the softmax
   __syncthreads();
   // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
   double mx = -INFINITY;
-  for (int t = tid; t < n; t += blockDim.x) mx = fmax(mx, sc[t]);
+  for (int t = tid; t < n; t += NT) mx = fmax(mx, sc[t]);
   for (int o = 32; o >= 1; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
   if (l == 0) red[w] = mx;
   __syncthreads();
-  mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
-  for (int t = tid; t < n; t += blockDim.x) sc[t] = exp_f64(sc[t] - mx);
+  mx = red[0];
+#pragma unroll
+  for (int i = 1; i < ATT_WAVES; ++i) mx = fmax(mx, red[i]);
+  for (int t = tid; t < n; t += NT) sc[t] = exp_f64(sc[t] - mx);
   __syncthreads();
   const double sum = pairwise_sum_block(sc, n, leaf);
-  for (int t = tid; t < n; t += blockDim.x) sc[t] = sc[t] / sum;
+  for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
   __syncthreads();
-  // attn_h = sum_t p[t] * V[t]  in ascending t from 0.0 (full.py:280-281)
-  if (w == 0) {
-    double acc = 0.0;
-    for (int t = 0; t < n; ++t) {
-      double vt;
-      if (t == pos) {
-        vt = vc[l];
-      } else {
-        const long long o = ((long long)t * a.H_KV + g) * HD + l;
-        vt = bfp_val(Vm[o], Ve[o >> 4]);
+
+  // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281).
+  // Iteration k: waves 1.. write the products of block k into buf[k & 1]
+  // (element (tt, dim) at double tt*64 + dim) and refill their ring slot
+  // with block k + ATT_DEPTH; wave 0 adds block k-1 from buf[(k-1) & 1],
+  // one dimension per lane.
+  const int nb = (n + TB - 1) / TB;
+  double acc = 0.0;
+  for (int k0 = 0; k0 <= nb; k0 += ATT_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < ATT_DEPTH; ++d) {
+      const int k = k0 + d;               // iterations past nb do unused work
+      if (w >= 1) {
+        const int tt = pw * PPW + pp;
+        const int t = k * TB + tt;
+        const int tc = t < n ? t : n - 1;
+        const double pt = sc[tc];
+        const double s = ldexp(1.0, re[d] - 15);
+        const unsigned wv[4] = {rm[d].x, rm[d].y, rm[d].z, rm[d].w};
+        double pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int mi = (int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
+          const double vcur = vc[8 * pc + i];
+          const double v = (t == pos) ? vcur : (double)mi * s;
+          pr[i] = t < n ? pt * v : 0.0;
+        }
+        if (pp < PPW) {
+          double2 *bp = buf + (k & 1) * (TB / 2) * 64 + tt * 32 + 4 * pc;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bp[i] = make_double2(pr[2 * i], pr[2 * i + 1]);
+        }
       }
-      acc = acc + sc[t] * vt;
+      load_blk(k + ATT_DEPTH, rm[d], re[d]);
+      if (w == 0 && k >= 1 && k <= nb) {
+        const double *bb = reinterpret_cast<const double *>(buf + ((k - 1) & 1) * (TB / 2) * 64) + l;
+        const int cnt = min(TB, n - (k - 1) * TB);
+        if (cnt == TB) {
+#pragma unroll
+          for (int i = 0; i < TB; ++i) acc = acc + bb[i * 64];
+        } else {
+          for (int i = 0; i < cnt; ++i) acc = acc + bb[i * 64];
+        }
+      }
+      __syncthreads();
     }
+  }
+  if (w == 0) {
     int e;
     int m = quantize16_lanes(acc, e, true);   // tile_quantize(fp_quantize_vec(attn))
     int idx = hq * HD + l;
@@ -582,6 +680,28 @@ static lk_fn pick_ores(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_o_res) re
 static lk_fn pick_gu(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_gu) return nullptr; }
 static lk_fn pick_dres(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_d_res) return nullptr; }
 
+// Attention variant by context capacity: products per producer wave and
+// AV block (2 -> 14 positions, 4 -> 28, 8 -> 56); dynamic LDS may exceed
+// 64 KiB at long contexts.
+static int attn_ppw(int max_ctx) { return max_ctx <= 128 ? 2 : (max_ctx <= 512 ? 4 : 8); }
+static lk_fn attn_kernel(int ppw) { return ppw == 2 ? k_attn<2> : (ppw == 4 ? k_attn<4> : k_attn<8>); }
+
+// Per device, before the first launch (outside any stream capture).
+int prepare_layer_kernels(int max_ctx) {
+  const int ppw = attn_ppw(max_ctx);
+  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel(ppw)),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)attn_lds_bytes(max_ctx, ppw)));
+  return BFP_OK;
+}
+
+static int launch_attn(const LayerArgs &a, hipStream_t s) {
+  const int ppw = attn_ppw(a.max_ctx);
+  hipLaunchKernelGGL(attn_kernel(ppw), dim3(a.H_Q, a.batch), dim3(64 * ATT_WAVES),
+                     attn_lds_bytes(a.max_ctx, ppw), s, a);
+  return BFP_OK;
+}
+
 static void shape_for(int nT, int &nw, int &tpt) {
   nw = default_waves(nT);
   tpt = (nT + 4 * nw - 1) / (4 * nw);
@@ -597,8 +717,7 @@ int launch_layer(const LayerArgs &a, hipStream_t s) {
   lk_fn fo = pick_ores(nw, tpt), fg = pick_gu(nw, tpt);
   if (!f || !fo || !fg) return set_err(BFP_EINVAL, "no layer kernel for D=%d", a.D);
   hipLaunchKernelGGL(f, dim3(nq / 16, a.batch), dim3(64 * nw), sh_norm, s, a);
-  const size_t sh_attn = (size_t)(192 + PW_MAX_LEAVES + a.max_ctx) * 8;
-  hipLaunchKernelGGL(k_attn, dim3(a.H_Q, a.batch), dim3(256), sh_attn, s, a);
+  BFP_TRY(launch_attn(a, s));
   hipLaunchKernelGGL(fo, dim3(a.D / 16, a.batch), dim3(64 * nw), (size_t)nTD * 17 * 4, s, a);
   hipLaunchKernelGGL(fg, dim3(a.FFN / 16, a.batch), dim3(64 * nw), sh_norm, s, a);
   int nwf, tptf;
