@@ -71,6 +71,27 @@ def test_layer_batched_sequences(gpu):
     gm.close()
 
 
+@pytest.mark.parametrize("cfg,batch", [(MID, 5), (FULL, 6)], ids=["mid-b5", "full-b6"])
+def test_layer_multi_sequence_path(gpu, cfg, batch):
+    """Batches of 4 or more run the multi-sequence kernels (separate norm,
+    weight chunks reused across a group of sequences): every stage of every
+    sequence still equals its own oracle run."""
+    d, om, gm = _setup(cfg, seed=7, max_batch=batch)
+    rng = np.random.default_rng(9)
+    kvs = [sim.new_kv(om.dims, d.MAX_CTX) for _ in range(batch)]
+    for p in range(4):
+        hs = [sim.fp_quantize_vec(rng.standard_normal(d.D) * (0.5 + b)) for b in range(batch)]
+        q = [sim.tile_quantize(h) for h in hs]
+        hm = np.stack([x[0].reshape(-1) for x in q])
+        he = np.stack([x[1] for x in q])
+        out_m, out_e, st = gm.layer_step_bfp(0, p, hm, he, dump=True)
+        for b in range(batch):
+            dump = {}
+            sim.fwd_layer(hs[b], om.layers[0], pos=p, kv=kvs[b], kv_pos=p, dims=om.dims, dump=dump)
+            _check_stages(st, dump, b, p, f"seq{b}")
+    gm.close()
+
+
 def test_fwd_layer_float_api(gpu):
     """The reference-named float64 entry point."""
     d, om, gm = _setup(SMALL, seed=3)

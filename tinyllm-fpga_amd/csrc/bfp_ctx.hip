@@ -27,6 +27,9 @@ struct bfp_ctx {
   // activations (max_batch sequences)
   int16_t *h_m = nullptr, *h1_m = nullptr, *qkv_am = nullptr, *att_m = nullptr, *mlp_m = nullptr;
   int8_t *h_e = nullptr, *h1_e = nullptr, *qkv_ae = nullptr, *att_e = nullptr, *mlp_e = nullptr;
+  int16_t *xn_m = nullptr;   // RMSNorm output, multi-sequence layer path
+  int8_t *xn_e = nullptr;
+  double *hn = nullptr;      // normed final hidden, batch > 1 head
   // KV cache: NL x max_batch x max_ctx x KV
   int16_t *k_m = nullptr, *v_m = nullptr;
   int8_t *k_e = nullptr, *v_e = nullptr;
@@ -89,6 +92,22 @@ void rope_table(std::vector<double> &t, int max_ctx, int HD) {
     }
 }
 
+// Workgroups of the head for `batch` sequences, and the most any batch uses.
+int head_nwg(const bfp_ctx *c, int batch) {
+  return head_workgroups(c->d.VOCAB, c->d.D, c->head_rows, batch);
+}
+int head_part_max(const bfp_ctx *c) {
+  const int a = head_nwg(c, 1), b = head_nwg(c, 2);
+  return a > b ? a : b;
+}
+
+HeadArgs head_args(bfp_ctx *c, int batch, double *logits) {
+  const bfp_dims &d = c->d;
+  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, head_nwg(c, batch), c->h_m, c->h_e, c->norm_w,
+              c->embed, c->part_v, c->part_i, logits, c->hn};
+  return ha;
+}
+
 LayerArgs layer_args(bfp_ctx *c, int layer, int batch) {
   const bfp_dims &d = c->d;
   LayerArgs a;
@@ -123,6 +142,8 @@ LayerArgs layer_args(bfp_ctx *c, int layer, int batch) {
   a.att_e = c->att_e;
   a.mlp_m = c->mlp_m;
   a.mlp_e = c->mlp_e;
+  a.xn_m = c->xn_m;
+  a.xn_e = c->xn_e;
   a.k_m = c->k_m + layer * c->s_kv_m;
   a.k_e = c->k_e + layer * c->s_kv_e;
   a.v_m = c->v_m + layer * c->s_kv_m;
@@ -211,15 +232,18 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->k_e, c->s_kv_e * d.NL)) ||
       (rc = c->alloc((void **)&c->v_m, 2 * c->s_kv_m * d.NL)) ||
       (rc = c->alloc((void **)&c->v_e, c->s_kv_e * d.NL)) ||
-      (rc = c->alloc((void **)&c->part_v, sizeof(double) * B * c->head_wg)) ||
-      (rc = c->alloc((void **)&c->part_i, sizeof(int) * B * c->head_wg)) ||
+      (rc = c->alloc((void **)&c->xn_m, 2 * B * d.D)) ||
+      (rc = c->alloc((void **)&c->xn_e, B * d.D / 16)) ||
+      (rc = c->alloc((void **)&c->hn, sizeof(double) * B * d.D)) ||
+      (rc = c->alloc((void **)&c->part_v, sizeof(double) * B * head_part_max(c))) ||
+      (rc = c->alloc((void **)&c->part_i, sizeof(int) * B * head_part_max(c))) ||
       (rc = c->alloc((void **)&c->state, sizeof(int) * (B + 1))) ||
       (rc = c->alloc((void **)&c->last, sizeof(int) * B)) ||
       (rc = c->alloc((void **)&c->dump_dev, sizeof(StageDump)))) {
     delete c;
     return nullptr;
   }
-  if (prepare_layer_kernels(c->max_ctx)) {
+  if (prepare_layer_kernels(c->max_ctx, d.D, d.FFN) || prepare_head_kernels(d.D)) {
     delete c;
     return nullptr;
   }
@@ -443,8 +467,7 @@ int bfp_head(bfp_ctx *c, int batch, const int16_t *h_m, const int8_t *h_e, doubl
   if (logits) BFP_TRY(tmp.alloc((void **)&dl, sizeof(double) * batch * d.VOCAB));
   HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)batch * d.D * 2, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)batch * d.D / 16, hipMemcpyHostToDevice, s));
-  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, c->head_wg, c->h_m, c->h_e, c->norm_w,
-              c->embed, c->part_v, c->part_i, dl};
+  HeadArgs ha = head_args(c, batch, dl);
   BFP_TRY(launch_head(ha, s));
   // reuse the controller's reduction with an empty prompt schedule
   std::vector<int> st(batch + 1, 0);
@@ -453,7 +476,7 @@ int bfp_head(bfp_ctx *c, int batch, const int16_t *h_m, const int8_t *h_e, doubl
   int *dprompt, *dout;
   BFP_TRY(tmp.alloc((void **)&dprompt, sizeof(int) * batch));
   BFP_TRY(tmp.alloc((void **)&dout, sizeof(int) * batch));
-  CtlArgs ca{batch, 1, 0, c->head_wg, 1, c->state, dprompt, dout, c->part_v, c->part_i, c->last};
+  CtlArgs ca{batch, 1, 0, ha.n_wg, 1, c->state, dprompt, dout, c->part_v, c->part_i, c->last};
   BFP_TRY(launch_ctl(ca, s));
   HIP_TRY(hipMemcpyAsync(argmax, c->last, sizeof(int) * batch, hipMemcpyDeviceToHost, s));
   if (logits)
@@ -501,9 +524,8 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   HIP_TRY(hipMemcpyAsync(c->state, st.data(), sizeof(int) * (batch + 1), hipMemcpyHostToDevice, s));
 
   EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
-  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, c->head_wg, c->h_m, c->h_e, c->norm_w,
-              c->embed, c->part_v, c->part_i, nullptr};
-  CtlArgs ca{batch, n_prompt, n_gen, c->head_wg, 0, c->state, dprompt, dout, c->part_v,
+  HeadArgs ha = head_args(c, batch, nullptr);
+  CtlArgs ca{batch, n_prompt, n_gen, ha.n_wg, 0, c->state, dprompt, dout, c->part_v,
              c->part_i, c->last};
   auto enqueue_step = [&](bool head) -> int {
     BFP_TRY(launch_embed(ea, s));

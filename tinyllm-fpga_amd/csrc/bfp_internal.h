@@ -66,7 +66,9 @@ struct HeadArgs;
 struct CtlArgs;
 struct EmbedArgs;
 int launch_layer(const LayerArgs &a, hipStream_t s);
-int prepare_layer_kernels(int max_ctx);
+int prepare_layer_kernels(int max_ctx, int D, int FFN);
+int prepare_head_kernels(int D);
+int head_workgroups(int vocab, int D, int rows_single, int batch);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);
 int launch_ctl(const CtlArgs &a, hipStream_t s);

@@ -37,6 +37,7 @@ struct LayerArgs {
   int16_t *qkv_m; int8_t *qkv_e;   // D + 2KV, pre-rope
   int16_t *att_m; int8_t *att_e;   // D
   int16_t *mlp_m; int8_t *mlp_e;   // FFN
+  int16_t *xn_m;  int8_t *xn_e;    // D, RMSNorm output (multi-sequence path)
   // this layer's KV cache: sequence b, position t, kv head g at
   // ((b*max_ctx + t)*H_KV + g)*HD mantissas and /16 exponents
   int16_t *k_m; int8_t *k_e;
@@ -56,7 +57,12 @@ struct HeadArgs {
   const float *embed;                      // (VOCAB, D) raw float32 (exact in f64)
   double *part_v; int *part_i;             // (batch, n_wg) per-workgroup argmax
   double *logits;                          // optional (batch, VOCAB)
+  double *hn;                              // (batch, D) normed hidden, batch > 1 path
 };
+
+// Rows per workgroup of the batch > 1 head: 16 row slots x 2 rows for
+// D <= 576, x 1 row above (register budget).
+inline int head_rows_multi(int D) { return D <= 576 ? 32 : 16; }
 
 struct CtlArgs {
   int batch, n_prompt, n_gen, n_wg, head;

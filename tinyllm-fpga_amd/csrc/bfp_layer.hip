@@ -67,6 +67,144 @@ __device__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__res
   for (int p = tid; p < D / 2; p += bs) put_x_pair(xs, p >> 3, p & 7, mq[2 * p], mq[2 * p + 1]);
 }
 
+// ------------------------------------------------------------- epilogues
+// Run by wave 0 (threads < 64) of a chunk's workgroup after chunk_AM: lane
+// r + 16k holds row r of chunk c of sequence b (b may differ between the
+// four 16-lane groups); only groups with wr set store.
+
+// q|k|v rows: raw BFP out (V dumped here; Q and K post-RoPE by k_attn).
+__device__ __forceinline__ void epi_qkv(const LayerArgs &a, int b, int c, long long A, int M,
+                                        bool wr) {
+  const int nq = a.D + 2 * a.KV;
+  int m, e;
+  chunk_quant(A, M, m, e);
+  const int lane = threadIdx.x & 15;
+  if (wr) a.qkv_m[b * nq + c * 16 + lane] = (int16_t)m;
+  if (wr && lane == 0) a.qkv_e[b * (nq / 16) + c] = (int8_t)e;
+  if (a.dump) {
+    // V is not rotated: dump it here (Q and K are dumped post-RoPE by k_attn)
+    int cm, ce;
+    canon_copy(m, e, cm, ce);
+    int row = c * 16 + lane;
+    if (wr && row >= a.D + a.KV) {
+      int r = row - a.D - a.KV;
+      a.dump->m[ST_V][b * a.dump->mstride[ST_V] + r] = (int16_t)cm;
+      if (lane == 0) a.dump->e[ST_V][b * (a.dump->mstride[ST_V] / 16) + r / 16] = (int8_t)ce;
+    }
+  }
+}
+
+// Residual epilogue: y = q(res + o) over the chunk (wave 0, lane r holds row r).
+__device__ __forceinline__ int residual_lane(int om, int oe, int rm, int re, int &e) {
+  double s = bfp_val(rm, re) + bfp_val(om, oe);
+  return quantize16_lanes(s, e);
+}
+
+// o = Wo attn; h1 = q(h + o)   (full.py:284-285)
+__device__ __forceinline__ void epi_ores(const LayerArgs &a, int b, int c, long long A, int M,
+                                         bool wr) {
+  const int r = threadIdx.x & 15;
+  int om, oe;
+  chunk_quant(A, M, om, oe);
+  const int row = b * a.D + c * 16 + r;
+  const int tile = b * (a.D / 16) + c;
+  int e;
+  int m = residual_lane(om, oe, a.h_m[row], a.h_e[tile], e);
+  int com = om, coe = oe, chm = m, che = e;
+  if (a.dump) {
+    canon16_lanes(com, coe);
+    canon16_lanes(chm, che);
+  }
+  if (wr) {
+    a.h1_m[row] = (int16_t)m;
+    if (r == 0) a.h1_e[tile] = (int8_t)e;
+    if (a.dump) {
+      const StageDump *d = a.dump;
+      d->m[ST_O][b * d->mstride[ST_O] + c * 16 + r] = (int16_t)com;
+      d->m[ST_H1][b * d->mstride[ST_H1] + c * 16 + r] = (int16_t)chm;
+      if (r == 0) {
+        d->e[ST_O][b * (d->mstride[ST_O] / 16) + c] = (int8_t)coe;
+        d->e[ST_H1][b * (d->mstride[ST_H1] / 16) + c] = (int8_t)che;
+      }
+    }
+  }
+}
+
+// g, u -> mlp = q(q(silu(g)) * u)   (full.py:241-242,288-290)
+__device__ __forceinline__ void epi_gu(const LayerArgs &a, int b, int c, long long Ag, int Mg,
+                                       long long Au, int Mu, bool wr) {
+  const int r = threadIdx.x & 15;
+  int gm, ge, um, ue;
+  chunk_quant(Ag, Mg, gm, ge);
+  chunk_quant(Au, Mu, um, ue);
+  // silu_fp: fp_quantize_vec(g / (1 + exp(-g)))   (full.py:241-242)
+  const double gv = bfp_val(gm, ge);
+  int se;
+  int sm = quantize16_lanes(gv / (1.0 + exp_f64(-gv)), se);
+  // mlp = fp_quantize_vec(silu * u)                (full.py:290)
+  int me;
+  int mm = quantize16_lanes(bfp_val(sm, se) * bfp_val(um, ue), me, true);   // D's input
+  if (a.dump) {
+    canon16_lanes(gm, ge);      // values of g and u are no longer needed
+    canon16_lanes(um, ue);
+  }
+  if (wr) {
+    const int row = b * a.FFN + c * 16 + r;
+    const int tile = b * (a.FFN / 16) + c;
+    a.mlp_m[row] = (int16_t)mm;
+    if (r == 0) a.mlp_e[tile] = (int8_t)me;
+    if (a.dump) {
+      const StageDump *d = a.dump;
+      d->m[ST_G][b * d->mstride[ST_G] + c * 16 + r] = (int16_t)gm;
+      d->m[ST_U][b * d->mstride[ST_U] + c * 16 + r] = (int16_t)um;
+      d->m[ST_MLP][b * d->mstride[ST_MLP] + c * 16 + r] = (int16_t)mm;
+      if (r == 0) {
+        d->e[ST_G][b * (d->mstride[ST_G] / 16) + c] = (int8_t)ge;
+        d->e[ST_U][b * (d->mstride[ST_U] / 16) + c] = (int8_t)ue;
+        d->e[ST_MLP][b * (d->mstride[ST_MLP] / 16) + c] = (int8_t)me;
+      }
+    }
+  }
+}
+
+// d = Wd mlp; h_out = q(h1 + d)   (full.py:291-293)
+__device__ __forceinline__ void epi_dres(const LayerArgs &a, int b, int c, long long A, int M,
+                                         bool wr) {
+  const int r = threadIdx.x & 15;
+  int dmv, dev;
+  chunk_quant(A, M, dmv, dev);
+  const int row = b * a.D + c * 16 + r;
+  const int tile = b * (a.D / 16) + c;
+  int e;
+  int m = residual_lane(dmv, dev, a.h1_m[row], a.h1_e[tile], e);
+  int cdm = dmv, cde = dev, chm = m, che = e;
+  if (a.dump || a.hist_m) {
+    canon16_lanes(cdm, cde);
+    canon16_lanes(chm, che);
+  }
+  if (wr) {
+    a.h_m[row] = (int16_t)m;
+    if (r == 0) a.h_e[tile] = (int8_t)e;
+    if (a.dump) {
+      const StageDump *d = a.dump;
+      d->m[ST_D][b * d->mstride[ST_D] + c * 16 + r] = (int16_t)cdm;
+      d->m[ST_HOUT][b * d->mstride[ST_HOUT] + c * 16 + r] = (int16_t)chm;
+      if (r == 0) {
+        d->e[ST_D][b * (d->mstride[ST_D] / 16) + c] = (int8_t)cde;
+        d->e[ST_HOUT][b * (d->mstride[ST_HOUT] / 16) + c] = (int8_t)che;
+      }
+    }
+    if (a.hist_m) {
+      const int pos = cur_pos(a);
+      if (pos < a.hist_steps) {
+        long long o = (((long long)b * a.hist_steps + pos) * a.NL + a.layer) * a.D;
+        a.hist_m[o + c * 16 + r] = (int16_t)chm;
+        if (r == 0) a.hist_e[(o >> 4) + c] = (int8_t)che;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------- qkv
 template <int NW, int TPT>
 __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
@@ -94,24 +232,7 @@ __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
   long long A;
   int M;
   chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
-  if (threadIdx.x < 64) {
-    int m, e;
-    chunk_quant(A, M, m, e);
-    const int lane = threadIdx.x;
-    if (lane < 16) a.qkv_m[b * nq + c * 16 + lane] = (int16_t)m;
-    if (lane == 0) a.qkv_e[b * (nq / 16) + c] = (int8_t)e;
-    if (a.dump) {
-      // V is not rotated: dump it here (Q and K are dumped post-RoPE by k_attn)
-      int cm, ce;
-      canon_copy(m, e, cm, ce);
-      int row = c * 16 + lane;
-      if (lane < 16 && row >= a.D + a.KV) {
-        int r = row - a.D - a.KV;
-        a.dump->m[ST_V][b * a.dump->mstride[ST_V] + r] = (int16_t)cm;
-        if (lane == 0) a.dump->e[ST_V][b * (a.dump->mstride[ST_V] / 16) + r / 16] = (int8_t)ce;
-      }
-    }
-  }
+  if (threadIdx.x < 64) epi_qkv(a, b, c, A, M, threadIdx.x < 16);
 }
 
 // ------------------------------------------------------------------ attn
@@ -349,12 +470,6 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
 }
 
 // ----------------------------------------------------------------- o_res
-// Residual epilogue: y = q(res + o) over the chunk (wave 0, lane r holds row r).
-__device__ __forceinline__ int residual_lane(int om, int oe, int rm, int re, int &e) {
-  double s = bfp_val(rm, re) + bfp_val(om, oe);
-  return quantize16_lanes(s, e);
-}
-
 template <int NW, int TPT>
 __global__ __launch_bounds__(64 * NW) void k_o_res(LayerArgs a) {
   extern __shared__ int ism[];
@@ -371,33 +486,7 @@ __global__ __launch_bounds__(64 * NW) void k_o_res(LayerArgs a) {
   long long A;
   int M;
   chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
-  if (threadIdx.x < 64) {
-    const int r = threadIdx.x & 15;
-    int om, oe;
-    chunk_quant(A, M, om, oe);
-    const int row = b * a.D + c * 16 + r;
-    const int tile = b * (a.D / 16) + c;
-    int e;
-    int m = residual_lane(om, oe, a.h_m[row], a.h_e[tile], e);
-    int com = om, coe = oe, chm = m, che = e;
-    if (a.dump) {
-      canon16_lanes(com, coe);
-      canon16_lanes(chm, che);
-    }
-    if (threadIdx.x < 16) {
-      a.h1_m[row] = (int16_t)m;
-      if (r == 0) a.h1_e[tile] = (int8_t)e;
-      if (a.dump) {
-        const StageDump *d = a.dump;
-        d->m[ST_O][b * d->mstride[ST_O] + c * 16 + r] = (int16_t)com;
-        d->m[ST_H1][b * d->mstride[ST_H1] + c * 16 + r] = (int16_t)chm;
-        if (r == 0) {
-          d->e[ST_O][b * (d->mstride[ST_O] / 16) + c] = (int8_t)coe;
-          d->e[ST_H1][b * (d->mstride[ST_H1] / 16) + c] = (int8_t)che;
-        }
-      }
-    }
-  }
+  if (threadIdx.x < 64) epi_ores(a, b, c, A, M, threadIdx.x < 16);
 }
 
 // -------------------------------------------------------------------- gu
@@ -429,40 +518,7 @@ __global__ __launch_bounds__(64 * NW) void k_gu(LayerArgs a) {
   int Mg, Mu;
   chunk_AM<NW, TPT>(RG, xs, xes, nT, redM, redA, Ag, Mg);
   chunk_AM<NW, TPT>(RU, xs, xes, nT, redM, redA, Au, Mu);
-  if (threadIdx.x < 64) {
-    const int r = threadIdx.x & 15;
-    int gm, ge, um, ue;
-    chunk_quant(Ag, Mg, gm, ge);
-    chunk_quant(Au, Mu, um, ue);
-    // silu_fp: fp_quantize_vec(g / (1 + exp(-g)))   (full.py:241-242)
-    const double gv = bfp_val(gm, ge);
-    int se;
-    int sm = quantize16_lanes(gv / (1.0 + exp_f64(-gv)), se);
-    // mlp = fp_quantize_vec(silu * u)                (full.py:290)
-    int me;
-    int mm = quantize16_lanes(bfp_val(sm, se) * bfp_val(um, ue), me, true);   // D's input
-    if (a.dump) {
-      canon16_lanes(gm, ge);      // values of g and u are no longer needed
-      canon16_lanes(um, ue);
-    }
-    if (threadIdx.x < 16) {
-      const int row = b * a.FFN + c * 16 + r;
-      const int tile = b * (a.FFN / 16) + c;
-      a.mlp_m[row] = (int16_t)mm;
-      if (r == 0) a.mlp_e[tile] = (int8_t)me;
-      if (a.dump) {
-        const StageDump *d = a.dump;
-        d->m[ST_G][b * d->mstride[ST_G] + c * 16 + r] = (int16_t)gm;
-        d->m[ST_U][b * d->mstride[ST_U] + c * 16 + r] = (int16_t)um;
-        d->m[ST_MLP][b * d->mstride[ST_MLP] + c * 16 + r] = (int16_t)mm;
-        if (r == 0) {
-          d->e[ST_G][b * (d->mstride[ST_G] / 16) + c] = (int8_t)ge;
-          d->e[ST_U][b * (d->mstride[ST_U] / 16) + c] = (int8_t)ue;
-          d->e[ST_MLP][b * (d->mstride[ST_MLP] / 16) + c] = (int8_t)me;
-        }
-      }
-    }
-  }
+  if (threadIdx.x < 64) epi_gu(a, b, c, Ag, Mg, Au, Mu, threadIdx.x < 16);
 }
 
 // ----------------------------------------------------------------- d_res
@@ -482,41 +538,138 @@ __global__ __launch_bounds__(64 * NW) void k_d_res(LayerArgs a) {
   long long A;
   int M;
   chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
-  if (threadIdx.x < 64) {
-    const int r = threadIdx.x & 15;
-    int dmv, dev;
-    chunk_quant(A, M, dmv, dev);
-    const int row = b * a.D + c * 16 + r;
-    const int tile = b * (a.D / 16) + c;
-    int e;
-    int m = residual_lane(dmv, dev, a.h1_m[row], a.h1_e[tile], e);
-    int cdm = dmv, cde = dev, chm = m, che = e;
-    if (a.dump || a.hist_m) {
-      canon16_lanes(cdm, cde);
-      canon16_lanes(chm, che);
-    }
-    if (threadIdx.x < 16) {
-      a.h_m[row] = (int16_t)m;
-      if (r == 0) a.h_e[tile] = (int8_t)e;
-      if (a.dump) {
-        const StageDump *d = a.dump;
-        d->m[ST_D][b * d->mstride[ST_D] + c * 16 + r] = (int16_t)cdm;
-        d->m[ST_HOUT][b * d->mstride[ST_HOUT] + c * 16 + r] = (int16_t)chm;
-        if (r == 0) {
-          d->e[ST_D][b * (d->mstride[ST_D] / 16) + c] = (int8_t)cde;
-          d->e[ST_HOUT][b * (d->mstride[ST_HOUT] / 16) + c] = (int8_t)che;
-        }
-      }
-      if (a.hist_m) {
-        const int pos = cur_pos(a);
-        if (pos < a.hist_steps) {
-          long long o = (((long long)b * a.hist_steps + pos) * a.NL + a.layer) * a.D;
-          a.hist_m[o + c * 16 + r] = (int16_t)chm;
-          if (r == 0) a.hist_e[(o >> 4) + c] = (int8_t)che;
-        }
-      }
+  if (threadIdx.x < 64) epi_dres(a, b, c, A, M, threadIdx.x < 16);
+}
+
+
+// ------------------------------------------------- multi-sequence kernels
+// For batch >= MULTI_MIN_BATCH the layer runs as norm -> matvec kernels in
+// which a workgroup keeps its weight chunk in registers and loops over S
+// sequences (grid.y = sequence groups), so weights are fetched once per
+// group rather than once per sequence, and each RMSNorm is computed once per
+// sequence rather than once per chunk.  Same arithmetic as the fused
+// kernels: the outputs are bit-identical.
+
+// n = tile_quantize(rmsnorm_fp(x, gamma)) of sequence blockIdx.x into xn
+// (which = 1: h with g1 -> N1; which = 2: h1 with g2 -> N2).
+__global__ __launch_bounds__(256) void k_norm_seq(LayerArgs a, int which) {
+  extern __shared__ double dsm[];
+  const int nT = a.D / 16;
+  double *dbuf = dsm;
+  double *leaf = dsm + a.D;
+  int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);
+  int *xes = xs + nT * 16;
+  const int b = blockIdx.x;
+  const int16_t *hm = (which == 1 ? a.h_m : a.h1_m) + b * a.D;
+  const int8_t *he = (which == 1 ? a.h_e : a.h1_e) + b * (a.D / 16);
+  int16_t *om = a.xn_m + b * a.D;
+  int8_t *oe = a.xn_e + b * (a.D / 16);
+  rmsnorm_to_x(hm, he, which == 1 ? a.g1 : a.g2, a.D, xs, xes, dbuf, leaf, om, oe);
+  if (a.dump) {
+    __syncthreads();   // om/oe written by other threads of this workgroup
+    const int st = which == 1 ? ST_N1 : ST_N2;
+    for (int i = threadIdx.x; i < a.D; i += blockDim.x) {
+      a.dump->m[st][b * a.dump->mstride[st] + i] = om[i];
+      if ((i & 15) == 0) a.dump->e[st][b * (a.dump->mstride[st] / 16) + (i >> 4)] = oe[i >> 4];
     }
   }
+}
+
+constexpr int MSEQ = 8;   // sequences per workgroup of the multi-sequence matvecs
+
+// The epilogue of a multi-sequence chunk: wave 0, four sequences per pass
+// (one per 16-lane group).
+#define BFP_MULTI_EPI(CALL)                                                       \
+  if (threadIdx.x < 64) {                                                         \
+    const int r_ = threadIdx.x & 15;                                              \
+    for (int p_ = 0; p_ < ns; p_ += 4) {                                          \
+      const int s_ = p_ + (threadIdx.x >> 4);                                     \
+      const bool wr_ = s_ < ns;                                                   \
+      const int sc_ = wr_ ? s_ : 0;                                               \
+      const int b = b0 + sc_;                                                     \
+      CALL;                                                                       \
+    }                                                                             \
+  }
+
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_qkv_m(LayerArgs a) {
+  extern __shared__ int ism[];
+  const int nT = a.D / 16;
+  int *xs = ism;
+  int *xes = ism + MSEQ * nT * 16;
+  __shared__ int redM[NW * 16 * MSEQ];
+  __shared__ long long redA[NW * 16 * MSEQ];
+  __shared__ long long Ao[16 * MSEQ];
+  __shared__ int Mo[16 * MSEQ];
+  const int c = blockIdx.x, b0 = blockIdx.y * MSEQ, ns = min(MSEQ, a.batch - b0);
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT);
+  stage_x_bfp(xs, xes, a.xn_m + b0 * a.D, a.xn_e + b0 * (a.D / 16), ns * nT);
+  __syncthreads();
+  chunk_AM_multi<NW, TPT, MSEQ>(R, xs, xes, nT, ns, redM, redA, Ao, Mo);
+  BFP_MULTI_EPI(epi_qkv(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_))
+}
+
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_o_res_m(LayerArgs a) {
+  extern __shared__ int ism[];
+  const int nT = a.D / 16;
+  int *xs = ism;
+  int *xes = ism + MSEQ * nT * 16;
+  __shared__ int redM[NW * 16 * MSEQ];
+  __shared__ long long redA[NW * 16 * MSEQ];
+  __shared__ long long Ao[16 * MSEQ];
+  __shared__ int Mo[16 * MSEQ];
+  const int c = blockIdx.x, b0 = blockIdx.y * MSEQ, ns = min(MSEQ, a.batch - b0);
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT);
+  stage_x_bfp(xs, xes, a.att_m + b0 * a.D, a.att_e + b0 * (a.D / 16), ns * nT);
+  __syncthreads();
+  chunk_AM_multi<NW, TPT, MSEQ>(R, xs, xes, nT, ns, redM, redA, Ao, Mo);
+  BFP_MULTI_EPI(epi_ores(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_))
+}
+
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_gu_m(LayerArgs a) {
+  extern __shared__ int ism[];
+  const int nT = a.D / 16;
+  int *xs = ism;
+  int *xes = ism + MSEQ * nT * 16;
+  __shared__ int redM[NW * 16 * MSEQ];
+  __shared__ long long redA[NW * 16 * MSEQ];
+  __shared__ long long Aog[16 * MSEQ], Aou[16 * MSEQ];
+  __shared__ int Mog[16 * MSEQ], Mou[16 * MSEQ];
+  const int c = blockIdx.x, b0 = blockIdx.y * MSEQ, ns = min(MSEQ, a.batch - b0);
+  ChunkRegs<TPT> RG, RU;
+  load_chunk<NW, TPT>(RG, a.w_gu_m + (long long)(2 * c) * nT * 32,
+                      a.w_gu_e + (long long)(2 * c) * nT * 16, nT);
+  load_chunk<NW, TPT>(RU, a.w_gu_m + (long long)(2 * c + 1) * nT * 32,
+                      a.w_gu_e + (long long)(2 * c + 1) * nT * 16, nT);
+  stage_x_bfp(xs, xes, a.xn_m + b0 * a.D, a.xn_e + b0 * (a.D / 16), ns * nT);
+  __syncthreads();
+  chunk_AM_multi<NW, TPT, MSEQ>(RG, xs, xes, nT, ns, redM, redA, Aog, Mog);
+  chunk_AM_multi<NW, TPT, MSEQ>(RU, xs, xes, nT, ns, redM, redA, Aou, Mou);
+  BFP_MULTI_EPI(epi_gu(a, b, c, Aog[r_ * MSEQ + sc_], Mog[r_ * MSEQ + sc_], Aou[r_ * MSEQ + sc_],
+                       Mou[r_ * MSEQ + sc_], wr_))
+}
+
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void k_d_res_m(LayerArgs a) {
+  extern __shared__ int ism[];
+  const int nT = a.FFN / 16;
+  int *xs = ism;
+  int *xes = ism + MSEQ * nT * 16;
+  __shared__ int redM[NW * 16 * MSEQ];
+  __shared__ long long redA[NW * 16 * MSEQ];
+  __shared__ long long Ao[16 * MSEQ];
+  __shared__ int Mo[16 * MSEQ];
+  const int c = blockIdx.x, b0 = blockIdx.y * MSEQ, ns = min(MSEQ, a.batch - b0);
+  ChunkRegs<TPT> R;
+  load_chunk<NW, TPT>(R, a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT);
+  stage_x_bfp(xs, xes, a.mlp_m + b0 * a.FFN, a.mlp_e + b0 * (a.FFN / 16), ns * nT);
+  __syncthreads();
+  chunk_AM_multi<NW, TPT, MSEQ>(R, xs, xes, nT, ns, redM, redA, Ao, Mo);
+  BFP_MULTI_EPI(epi_dres(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_))
 }
 
 // ------------------------------------------------------------------ head
@@ -596,6 +749,151 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
   }
 }
 
+
+// Batch > 1 head: the final norm once per sequence (k_head_norm), then a GEMV
+// in which each workgroup keeps its 32 embedding rows in registers as
+// float64 and iterates over the sequences (16 at a time through LDS), so the
+// 113 MB table is read once per step rather than once per sequence.  Each
+// logit is summed in the same order as k_head_logits (lane l16 of a row's 16
+// lanes accumulates k = 64i + 4*l16 + c, then the same butterfly), so the
+// logits are bit-identical to the batch-1 kernel's.
+__global__ __launch_bounds__(256) void k_head_norm(HeadArgs a) {
+  extern __shared__ double dsm[];
+  double *hx = dsm;                    // D
+  double *leaf = dsm + a.D;            // PW_MAX_LEAVES
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int16_t *hm = a.h_m + b * a.D;
+  const int8_t *he = a.h_e + b * (a.D / 16);
+  for (int i = tid; i < a.D; i += blockDim.x) {
+    double x = bfp_val(hm[i], he[i >> 4]);
+    hx[i] = x * x;
+  }
+  __syncthreads();
+  const double s = pairwise_sum_block(hx, a.D, leaf);
+  const double rt = sqrt(s / (double)a.D + 1e-5);
+  for (int i = tid; i < a.D; i += blockDim.x)
+    a.hn[(long long)b * a.D + i] = (bfp_val(hm[i], he[i >> 4]) / rt) * a.norm_w[i];
+}
+
+constexpr int HEAD_SEQ_GROUP = 16;   // most sequences staged in LDS at once
+
+// Sequences per LDS stage for hidden size D (at most 96 KiB of LDS).
+static int head_seq_group(int D) {
+  int g = 98304 / (D * 8);
+  return g < 1 ? 1 : (g > HEAD_SEQ_GROUP ? HEAD_SEQ_GROUP : g);
+}
+
+template <int MAXD64, int R>
+__global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
+  extern __shared__ double hs[];       // sg x D
+  __shared__ double bv[4][HEAD_SEQ_GROUP];
+  __shared__ int bi[4][HEAD_SEQ_GROUP];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int slot = tid >> 4, l16 = tid & 15;
+  const int d64 = a.D / 64;
+  const int row0 = blockIdx.x * (16 * R);
+  double eD[R][4 * MAXD64];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    int row = row0 + slot + 16 * r;
+    row = row < a.VOCAB ? row : a.VOCAB - 1;
+    const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)row * a.D);
+#pragma unroll
+    for (int i = 0; i < MAXD64; ++i) {
+      float4 f = i < d64 ? e4[i * 16 + l16] : make_float4(0.f, 0.f, 0.f, 0.f);
+      eD[r][4 * i] = (double)f.x;
+      eD[r][4 * i + 1] = (double)f.y;
+      eD[r][4 * i + 2] = (double)f.z;
+      eD[r][4 * i + 3] = (double)f.w;
+    }
+  }
+  for (int b0 = 0; b0 < a.batch; b0 += sg) {
+    const int nb = min(sg, a.batch - b0);
+    __syncthreads();
+    {   // 16-byte loads, eight in flight per thread before the LDS stores
+      const double2 *src = reinterpret_cast<const double2 *>(a.hn + (long long)b0 * a.D);
+      double2 *dst = reinterpret_cast<double2 *>(hs);
+      const int n2 = nb * a.D / 2;
+      for (int p0 = tid; p0 < n2; p0 += 8 * 256) {
+        double2 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int p = p0 + k * 256;
+          v[k] = src[p < n2 ? p : n2 - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int p = p0 + k * 256;
+          if (p < n2) dst[p] = v[k];
+        }
+      }
+    }
+    __syncthreads();
+    for (int bb = 0; bb < nb; ++bb) {
+      const double *hp = hs + bb * a.D + 4 * l16;
+      double acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.0;
+#pragma unroll
+      for (int i = 0; i < MAXD64; ++i) {
+        if (i < d64) {
+          const double2 h01 = *reinterpret_cast<const double2 *>(hp + 64 * i);
+          const double2 h23 = *reinterpret_cast<const double2 *>(hp + 64 * i + 2);
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            acc[r] = fma(eD[r][4 * i], h01.x, acc[r]);
+            acc[r] = fma(eD[r][4 * i + 1], h01.y, acc[r]);
+            acc[r] = fma(eD[r][4 * i + 2], h23.x, acc[r]);
+            acc[r] = fma(eD[r][4 * i + 3], h23.y, acc[r]);
+          }
+        }
+      }
+      double best = -INFINITY;
+      int besti = 0x7fffffff;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        double v = acc[r];
+        v += __shfl_xor(v, 8, 64);
+        v += __shfl_xor(v, 4, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 1, 64);
+        const int row = row0 + slot + 16 * r;
+        if (row < a.VOCAB) {
+          if (a.logits && l16 == 0) a.logits[(long long)(b0 + bb) * a.VOCAB + row] = v;
+          if (v > best || (v == best && row < besti)) {
+            best = v;
+            besti = row;
+          }
+        }
+      }
+      for (int o = 16; o < 64; o <<= 1) {   // the wave's 4 row slots
+        double ov = __shfl_xor(best, o, 64);
+        int oi = __shfl_xor(besti, o, 64);
+        if (ov > best || (ov == best && oi < besti)) {
+          best = ov;
+          besti = oi;
+        }
+      }
+      if (l == 0) {
+        bv[w][bb] = best;
+        bi[w][bb] = besti;
+      }
+    }
+    __syncthreads();
+    if (tid < nb) {
+      double best = bv[0][tid];
+      int besti = bi[0][tid];
+      for (int k = 1; k < 4; ++k)
+        if (bv[k][tid] > best || (bv[k][tid] == best && bi[k][tid] < besti)) {
+          best = bv[k][tid];
+          besti = bi[k][tid];
+        }
+      a.part_v[(b0 + tid) * a.n_wg + blockIdx.x] = best;
+      a.part_i[(b0 + tid) * a.n_wg + blockIdx.x] = besti;
+    }
+  }
+}
+
 // Final argmax of each sequence and the token loop of full.py:432-443:
 // at step s >= n_prompt the argmax is appended; the next input is
 // prompt[s+1] while s+1 < n_prompt, prompt[n_prompt-1] again at
@@ -667,6 +965,9 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
 // --------------------------------------------------------------- launchers
 typedef void (*lk_fn)(LayerArgs);
 
+// Batches from this size on use the multi-sequence kernels.
+constexpr int MULTI_MIN_BATCH = 4;
+
 // The (waves, tiles per lane) pairs default_waves() produces for
 // 4 <= in/16 <= 108, i.e. every supported D and FFN.
 #define BFP_LAYER_SHAPES(X, KER) \
@@ -680,18 +981,41 @@ static lk_fn pick_ores(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_o_res) re
 static lk_fn pick_gu(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_gu) return nullptr; }
 static lk_fn pick_dres(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_d_res) return nullptr; }
 
+typedef void (*lkm_fn)(LayerArgs);
+static lkm_fn pick_qkv_m(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_qkv_m) return nullptr; }
+static lkm_fn pick_ores_m(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_o_res_m) return nullptr; }
+static lkm_fn pick_gu_m(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_gu_m) return nullptr; }
+static lkm_fn pick_dres_m(int nw, int tpt) { BFP_LAYER_SHAPES(BFP_CASE, k_d_res_m) return nullptr; }
+
 // Attention variant by context capacity: products per producer wave and
 // AV block (2 -> 14 positions, 4 -> 28, 8 -> 56); dynamic LDS may exceed
 // 64 KiB at long contexts.
+static void shape_for(int nT, int &nw, int &tpt) {
+  nw = default_waves(nT);
+  tpt = (nT + 4 * nw - 1) / (4 * nw);
+}
+
 static int attn_ppw(int max_ctx) { return max_ctx <= 128 ? 2 : (max_ctx <= 512 ? 4 : 8); }
 static lk_fn attn_kernel(int ppw) { return ppw == 2 ? k_attn<2> : (ppw == 4 ? k_attn<4> : k_attn<8>); }
 
-// Per device, before the first launch (outside any stream capture).
-int prepare_layer_kernels(int max_ctx) {
+// Per device, before the first launch (outside any stream capture): allow
+// the dynamic LDS the attention and multi-sequence kernels take.
+int prepare_layer_kernels(int max_ctx, int D, int FFN) {
   const int ppw = attn_ppw(max_ctx);
   HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel(ppw)),
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)attn_lds_bytes(max_ctx, ppw)));
+  int nw, tpt, nwf, tptf;
+  shape_for(D / 16, nw, tpt);
+  shape_for(FFN / 16, nwf, tptf);
+  const int shD = MSEQ * (D / 16) * 17 * 4, shF = MSEQ * (FFN / 16) * 17 * 4;
+  const void *fs[4] = {reinterpret_cast<const void *>(pick_qkv_m(nw, tpt)),
+                       reinterpret_cast<const void *>(pick_ores_m(nw, tpt)),
+                       reinterpret_cast<const void *>(pick_gu_m(nw, tpt)),
+                       reinterpret_cast<const void *>(pick_dres_m(nwf, tptf))};
+  const int sh[4] = {shD, shD, shD, shF};
+  for (int i = 0; i < 4; ++i)
+    if (fs[i]) HIP_TRY(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, sh[i]));
   return BFP_OK;
 }
 
@@ -702,12 +1026,30 @@ static int launch_attn(const LayerArgs &a, hipStream_t s) {
   return BFP_OK;
 }
 
-static void shape_for(int nT, int &nw, int &tpt) {
-  nw = default_waves(nT);
-  tpt = (nT + 4 * nw - 1) / (4 * nw);
+static int launch_layer_multi(const LayerArgs &a, hipStream_t s) {
+  const int nTD = a.D / 16, nTF = a.FFN / 16;
+  int nw, tpt, nwf, tptf;
+  shape_for(nTD, nw, tpt);
+  shape_for(nTF, nwf, tptf);
+  lkm_fn fq = pick_qkv_m(nw, tpt), fo = pick_ores_m(nw, tpt), fg = pick_gu_m(nw, tpt);
+  lkm_fn fd = pick_dres_m(nwf, tptf);
+  if (!fq || !fo || !fg || !fd) return set_err(BFP_EINVAL, "no layer kernel for D=%d FFN=%d", a.D, a.FFN);
+  const int nq = a.D + 2 * a.KV;
+  const size_t sh_norm = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
+  const int G = (a.batch + MSEQ - 1) / MSEQ;
+  const size_t shD = (size_t)MSEQ * nTD * 17 * 4, shF = (size_t)MSEQ * nTF * 17 * 4;
+  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 1);
+  hipLaunchKernelGGL(fq, dim3(nq / 16, G), dim3(64 * nw), shD, s, a);
+  BFP_TRY(launch_attn(a, s));
+  hipLaunchKernelGGL(fo, dim3(a.D / 16, G), dim3(64 * nw), shD, s, a);
+  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 2);
+  hipLaunchKernelGGL(fg, dim3(a.FFN / 16, G), dim3(64 * nw), shD, s, a);
+  hipLaunchKernelGGL(fd, dim3(a.D / 16, G), dim3(64 * nwf), shF, s, a);
+  return launch_status("layer");
 }
 
 int launch_layer(const LayerArgs &a, hipStream_t s) {
+  if (a.batch >= MULTI_MIN_BATCH && a.xn_m) return launch_layer_multi(a, s);
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   int nw, tpt;
   shape_for(nTD, nw, tpt);
@@ -733,9 +1075,38 @@ int launch_embed(const EmbedArgs &a, hipStream_t s) {
   return launch_status("embed");
 }
 
+// Head workgroups for `batch` sequences: the batch-1 kernel covers
+// rows_single rows per workgroup, the batch > 1 GEMV HEAD_ROWS_MULTI.
+int head_workgroups(int vocab, int D, int rows_single, int batch) {
+  const int rm = head_rows_multi(D);
+  return batch == 1 ? vocab / rows_single : (vocab + rm - 1) / rm;
+}
+
+int prepare_head_kernels(int D) {
+  const int sh = head_seq_group(D) * D * 8;
+  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<9, 2>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, sh));
+  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<27, 1>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, sh));
+  return BFP_OK;
+}
+
 int launch_head(const HeadArgs &a, hipStream_t s) {
   size_t sh = (size_t)(a.D + PW_MAX_LEAVES) * 8;
-  hipLaunchKernelGGL(k_head_logits, dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
+  if (a.batch == 1) {
+    hipLaunchKernelGGL(k_head_logits, dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
+    return launch_status("head");
+  }
+  if (!a.hn) return set_err(BFP_EINVAL, "head: no normed-hidden buffer for batch %d", a.batch);
+  if (a.n_wg != head_workgroups(a.VOCAB, a.D, a.rows_per_wg, a.batch))
+    return set_err(BFP_EINVAL, "head: %d workgroups for batch %d", a.n_wg, a.batch);
+  hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
+  const int sg = head_seq_group(a.D);
+  const size_t shg = (size_t)sg * a.D * 8;
+  if (a.D <= 576)
+    hipLaunchKernelGGL((k_head_gemv<9, 2>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
+  else
+    hipLaunchKernelGGL((k_head_gemv<27, 1>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
   return launch_status("head");
 }
 

@@ -51,15 +51,30 @@ __device__ __forceinline__ void put_x_pair(int *xs, int t, int k, int lo, int hi
   xs[t * 16 + 8 + k] = (lo & 0xff) | ((hi & 0xff) << 16);
 }
 
-// Stage a BFP vector from global memory (all threads; caller syncs).
+// Stage a BFP vector of nT tiles from global memory (all threads; caller
+// syncs).  Each thread issues its loads (addresses clamped in range) before
+// its first LDS store, so the staging costs one memory round trip when
+// nT*8 <= 4*blockDim.
 __device__ __forceinline__ void stage_x_bfp(int *xs, int *xes, const int16_t *__restrict__ xm,
                                             const int8_t *__restrict__ xe, int nT) {
   const int *x32 = reinterpret_cast<const int *>(xm);
-  for (int p = threadIdx.x; p < nT * 8; p += blockDim.x) {
-    int v = x32[p];
-    put_x_pair(xs, p >> 3, p & 7, (int)(short)(v & 0xffff), v >> 16);
+  const int n = nT * 8, bs = blockDim.x, tid = threadIdx.x;
+  const int ex = xe[tid < nT ? tid : 0];
+  for (int p0 = tid; p0 < n; p0 += 4 * bs) {
+    int v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int p = p0 + k * bs;
+      v[k] = x32[p < n ? p : n - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int p = p0 + k * bs;
+      if (p < n) put_x_pair(xs, p >> 3, p & 7, (int)(short)(v[k] & 0xffff), v[k] >> 16);
+    }
   }
-  for (int p = threadIdx.x; p < nT; p += blockDim.x) xes[p] = xe[p];
+  if (tid < nT) xes[tid] = ex;
+  for (int p = tid + bs; p < nT; p += bs) xes[p] = xe[p];
 }
 
 // Row (A, M) of the chunk.  Every thread of the workgroup must call it (it
@@ -139,6 +154,118 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
   A = A < SAT_LO ? SAT_LO : (A > SAT_HI ? SAT_HI : A);
   A_out = A;
   M_out = M;
+}
+
+// chunk_AM for up to S sequences at once: x of sequence s in LDS at
+// xs + s*nT*16 / xes + s*nT (ns <= S valid).  One pass over the weight
+// registers forms every sequence's tile sums, so the chunk's weights are
+// read once for the group.  Every thread must call it.  On return (after a
+// barrier) Ao[r*S + s], Mo[r*S + s] (LDS) hold row r's (A, M) for sequence s.
+template <int NW, int TPT, int S>
+__device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const int *xs,
+                                               const int *xes, int nT, int ns, int *redM,
+                                               long long *redA, long long *Ao, int *Mo) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+  typedef short s2 __attribute__((ext_vector_type(2)));
+#define BFP_DOT2(a, b, acc) \
+  __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, (a)), __builtin_bit_cast(s2, (b)), (acc), false)
+  long long Sv[TPT][S];
+  int E[TPT][S];
+  int M[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) M[s] = -(1 << 29);
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    const int t = tq + 4 * (w + NW * j);
+    const bool ok = t < nT;
+    const int tc = ok ? t : 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      Sv[j][s] = 0;
+      E[j][s] = -(1 << 29);
+      if (s < ns) {
+        const int4 *xp = reinterpret_cast<const int4 *>(xs + (s * nT + tc) * 16);
+        int4 h0 = xp[0], h1 = xp[1], l0 = xp[2], l1 = xp[3];
+        int ah = 0, al = 0;
+        ah = BFP_DOT2(R.a[j].x, h0.x, ah);
+        al = BFP_DOT2(R.a[j].x, l0.x, al);
+        ah = BFP_DOT2(R.a[j].y, h0.y, ah);
+        al = BFP_DOT2(R.a[j].y, l0.y, al);
+        ah = BFP_DOT2(R.a[j].z, h0.z, ah);
+        al = BFP_DOT2(R.a[j].z, l0.z, al);
+        ah = BFP_DOT2(R.a[j].w, h0.w, ah);
+        al = BFP_DOT2(R.a[j].w, l0.w, al);
+        ah = BFP_DOT2(R.b[j].x, h1.x, ah);
+        al = BFP_DOT2(R.b[j].x, l1.x, al);
+        ah = BFP_DOT2(R.b[j].y, h1.y, ah);
+        al = BFP_DOT2(R.b[j].y, l1.y, al);
+        ah = BFP_DOT2(R.b[j].z, h1.z, ah);
+        al = BFP_DOT2(R.b[j].z, l1.z, al);
+        ah = BFP_DOT2(R.b[j].w, h1.w, ah);
+        al = BFP_DOT2(R.b[j].w, l1.w, al);
+        if (ok) {
+          Sv[j][s] = (long long)ah * 256 + al;
+          E[j][s] = xes[s * nT + tc] + R.e[j];
+        }
+        M[s] = E[j][s] > M[s] ? E[j][s] : M[s];
+      }
+    }
+  }
+#undef BFP_DOT2
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    M[s] = xor_max(M[s], 16);
+    M[s] = xor_max(M[s], 32);
+  }
+  if (NW > 1) {
+    if (tq == 0)
+#pragma unroll
+      for (int s = 0; s < S; ++s) redM[(w * 16 + r) * S + s] = M[s];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      int m = redM[r * S + s];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) m = redM[(i * 16 + r) * S + s] > m ? redM[(i * 16 + r) * S + s] : m;
+      M[s] = m;
+    }
+  }
+  long long A[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    long long acc = 0;
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const int sh = M[s] - E[j][s];
+      if (sh <= ALIGN_MAX) acc += Sv[j][s] >> sh;
+    }
+    acc = xor_sum(acc, 16);
+    acc = xor_sum(acc, 32);
+    A[s] = acc;
+  }
+  if (NW > 1) {
+    if (tq == 0)
+#pragma unroll
+      for (int s = 0; s < S; ++s) redA[(w * 16 + r) * S + s] = A[s];
+    __syncthreads();
+    if (w == 0)
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        long long acc = redA[r * S + s];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) acc += redA[(i * 16 + r) * S + s];
+        A[s] = acc;
+      }
+  }
+  if (w == 0 && tq == 0)
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const long long a = A[s] < SAT_LO ? SAT_LO : (A[s] > SAT_HI ? SAT_HI : A[s]);
+      Ao[r * S + s] = a;
+      Mo[r * S + s] = M[s];
+    }
+  __syncthreads();
 }
 
 // Quantise the chunk's 16 rows (wave 0; lanes r and r+16k hold row r): the
