@@ -84,4 +84,51 @@ __device__ __forceinline__ T xor_sum(T v, int mask) {
   return v + __shfl_xor(v, mask, 64);
 }
 
+// Register-only cross-lane exchange for gfx950 (no LDS round trip).
+// peer<M>(v) returns, for M = 16 or 32, the value of lane i^M (permlane16 /
+// permlane32 swap); for M = 1, 2, 4, 8, the value of lane (i - M) mod 16 of
+// the same 16-lane row (DPP row rotate).  A row reduction that combines v
+// with peer<M>(v) for M = 8, 4, 2, 1 in that order, or with any order for an
+// order-free operation (max, or, integer add), gives every lane the same
+// result as the xor butterfly: after the steps for the larger masks the
+// values are symmetric under them, and rotate and xor partners differ only
+// by such masks (float addition is commutative).
+template <int M>
+__device__ __forceinline__ int peer_u32(int v) {
+  if constexpr (M == 16) {
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (int)((threadIdx.x & 16) ? p[0] : p[1]);
+  } else if constexpr (M == 32) {
+    auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (int)((threadIdx.x & 32) ? p[0] : p[1]);
+  } else {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8, "row rotate by 1, 2, 4 or 8");
+    return __builtin_amdgcn_update_dpp(0, v, 0x120 + M, 0xf, 0xf, false);
+  }
+}
+template <int M>
+__device__ __forceinline__ int peer(int v) {
+  return peer_u32<M>(v);
+}
+template <int M>
+__device__ __forceinline__ long long peer(long long v) {
+  const int lo = peer_u32<M>((int)(v & 0xffffffffLL));
+  const int hi = peer_u32<M>((int)(v >> 32));
+  return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+template <int M>
+__device__ __forceinline__ double peer(double v) {
+  const long long b = __double_as_longlong(v);
+  return __longlong_as_double(peer<M>(b));
+}
+template <int M, typename T>
+__device__ __forceinline__ T pmax(T v) {
+  const T o = peer<M>(v);
+  return o > v ? o : v;
+}
+template <int M, typename T>
+__device__ __forceinline__ T psum(T v) {
+  return v + peer<M>(v);
+}
+
 }  // namespace bfp

@@ -170,10 +170,10 @@ __device__ __forceinline__ double exp_f64(double x) { return exp(x); }
 // mantissa each) call it.
 __device__ __forceinline__ void canon16_lanes(int &m, int &e) {
   int hit = (m == -32768) ? 1 : 0;
-  hit |= __shfl_xor(hit, 1, 64);
-  hit |= __shfl_xor(hit, 2, 64);
-  hit |= __shfl_xor(hit, 4, 64);
-  hit |= __shfl_xor(hit, 8, 64);
+  hit |= peer<1>(hit);
+  hit |= peer<2>(hit);
+  hit |= peer<4>(hit);
+  hit |= peer<8>(hit);
   if (hit && e < 127) {
     e += 1;
     int q = m >> 1;                     // floor(m / 2)
@@ -187,10 +187,10 @@ __device__ __forceinline__ void canon16_lanes(int &m, int &e) {
 // `canonical`).  All 64 lanes must participate.
 __device__ __forceinline__ int quantize16_lanes(double v, int &e, bool canonical = false) {
   double a = fabs(v);
-  a = xor_max(a, 1);
-  a = xor_max(a, 2);
-  a = xor_max(a, 4);
-  a = xor_max(a, 8);
+  a = pmax<1>(a);
+  a = pmax<2>(a);
+  a = pmax<4>(a);
+  a = pmax<8>(a);
   e = tile_exp_of(a);
   int m = tile_mant_of(v, e);
   if (canonical) canon16_lanes(m, e);

@@ -34,24 +34,45 @@ __device__ __forceinline__ int cur_pos(const LayerArgs &a) {
 
 // rmsnorm_fp (full.py:236-238) of a BFP vector, re-quantised, into the
 // matvec's LDS input form.  v = pairwise_sum(x*x)/D + 1e-5, y = (x*g)/sqrt(v).
-// dbuf: D doubles of LDS, leaf: PW_MAX_LEAVES doubles.  All threads call.
+// dbuf: 3*D doubles of LDS (x*x, x, g), leaf: PW_MAX_LEAVES doubles.  Every
+// thread issues all of its global loads (h, its exponents, g) before using
+// any, so the prologue costs one memory round trip.  All threads call.
 __device__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
                              const double *__restrict__ g, int D, int *xs, int *xes, double *dbuf,
                              double *leaf, int16_t *dm, int8_t *de) {
   const int bs = blockDim.x, tid = threadIdx.x;
-  for (int i = tid; i < D; i += bs) {
-    double x = bfp_val(hm[i], he[i >> 4]);
-    dbuf[i] = x * x;
+  double *sq = dbuf, *xv = dbuf + D, *gv = dbuf + 2 * D;
+  for (int i0 = tid; i0 < D; i0 += 4 * bs) {
+    int m[4], e[4];
+    double gg[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      int i = i0 + k * bs;
+      i = i < D ? i : D - 1;
+      m[k] = hm[i];
+      e[k] = he[i >> 4];
+      gg[k] = g[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + k * bs;
+      if (i < D) {
+        const double x = bfp_val(m[k], e[k]);
+        sq[i] = x * x;
+        xv[i] = x;
+        gv[i] = gg[k];
+      }
+    }
   }
   __syncthreads();
-  const double s = pairwise_sum_block(dbuf, D, leaf);
+  const double s = pairwise_sum_block(sq, D, leaf);
   const double rt = sqrt(s / (double)D + 1e-5);
-  short *mq = reinterpret_cast<short *>(dbuf);   // dbuf is free again
+  short *mq = reinterpret_cast<short *>(sq);   // sq is free again
   for (int base = 0; base < D; base += bs) {
     int i = base + tid;
     bool ok = i < D;
     double y = 0.0;
-    if (ok) y = (bfp_val(hm[i], he[i >> 4]) * g[i]) / rt;
+    if (ok) y = (xv[i] * gv[i]) / rt;
     int e;
     int m = quantize16_lanes(y, e, true);   // tile_quantize(rmsnorm_fp(.)): canonical
     if (ok) {
@@ -101,15 +122,16 @@ __device__ __forceinline__ int residual_lane(int om, int oe, int rm, int re, int
 }
 
 // o = Wo attn; h1 = q(h + o)   (full.py:284-285)
+// rm, re: this lane's row of h (the residual), loaded by the caller.
 __device__ __forceinline__ void epi_ores(const LayerArgs &a, int b, int c, long long A, int M,
-                                         bool wr) {
+                                         bool wr, int rm, int re) {
   const int r = threadIdx.x & 15;
   int om, oe;
   chunk_quant(A, M, om, oe);
   const int row = b * a.D + c * 16 + r;
   const int tile = b * (a.D / 16) + c;
   int e;
-  int m = residual_lane(om, oe, a.h_m[row], a.h_e[tile], e);
+  int m = residual_lane(om, oe, rm, re, e);
   int com = om, coe = oe, chm = m, che = e;
   if (a.dump) {
     canon16_lanes(com, coe);
@@ -168,15 +190,16 @@ __device__ __forceinline__ void epi_gu(const LayerArgs &a, int b, int c, long lo
 }
 
 // d = Wd mlp; h_out = q(h1 + d)   (full.py:291-293)
+// rm, re: this lane's row of h1 (the residual), loaded by the caller.
 __device__ __forceinline__ void epi_dres(const LayerArgs &a, int b, int c, long long A, int M,
-                                         bool wr) {
+                                         bool wr, int rm, int re) {
   const int r = threadIdx.x & 15;
   int dmv, dev;
   chunk_quant(A, M, dmv, dev);
   const int row = b * a.D + c * 16 + r;
   const int tile = b * (a.D / 16) + c;
   int e;
-  int m = residual_lane(dmv, dev, a.h1_m[row], a.h1_e[tile], e);
+  int m = residual_lane(dmv, dev, rm, re, e);
   int cdm = dmv, cde = dev, chm = m, che = e;
   if (a.dump || a.hist_m) {
     canon16_lanes(cdm, cde);
@@ -210,8 +233,8 @@ template <int NW, int TPT>
 __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
   extern __shared__ double dsm[];
   const int nT = a.D / 16;
-  double *dbuf = dsm;                                   // D
-  double *leaf = dsm + a.D;                             // PW_MAX_LEAVES
+  double *dbuf = dsm;                                   // 3*D
+  double *leaf = dsm + 3 * a.D;                         // PW_MAX_LEAVES
   int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);   // nT*16
   int *xes = xs + nT * 16;                              // nT
   __shared__ int redM[NW * 16];
@@ -241,7 +264,7 @@ __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
 __device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
   const int l = threadIdx.x & 63;
   const int j = l & 31;
-  double other = __shfl_xor(x, 32, 64);    // the partner element j+32 / j
+  double other = peer<32>(x);              // the partner element j+32 / j
   double c = cs[2 * j], s = cs[2 * j + 1];
   double out;
   if (l < 32) {
@@ -333,6 +356,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
     e = Ve[o >> 4];
   };
 
+  // the first K row of this thread's scores, in flight during the RoPE phase
+  KRow ra, rb;
+  load_krow(ra, Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
+
   if (w == 0) {            // q head hq
     int idx = hq * HD + l;
     int e;
@@ -378,9 +405,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
   // memory like the others (the writer may not have stored it yet) and its
   // score is recomputed from LDS afterwards by the same thread.
   {
-    KRow ra, rb;
     const int last = n - 1;
-    load_krow(ra, Km, Ke, ((long long)(tid < n ? tid : last) * a.H_KV + g) * HD);
     for (int t = tid; t < n; t += 2 * NT) {
       const int t1 = t + NT, t2 = t + 2 * NT;
       load_krow(rb, Km, Ke, ((long long)(t1 < n ? t1 : last) * a.H_KV + g) * HD);
@@ -397,7 +422,12 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
   // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
   double mx = -INFINITY;
   for (int t = tid; t < n; t += NT) mx = fmax(mx, sc[t]);
-  for (int o = 32; o >= 1; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+  mx = fmax(mx, peer<32>(mx));
+  mx = fmax(mx, peer<16>(mx));
+  mx = fmax(mx, peer<8>(mx));
+  mx = fmax(mx, peer<4>(mx));
+  mx = fmax(mx, peer<2>(mx));
+  mx = fmax(mx, peer<1>(mx));
   if (l == 0) red[w] = mx;
   __syncthreads();
   mx = red[0];
@@ -481,12 +511,14 @@ __global__ __launch_bounds__(64 * NW) void k_o_res(LayerArgs a) {
   const int c = blockIdx.x, b = blockIdx.y;
   ChunkRegs<TPT> R;
   load_chunk<NW, TPT>(R, a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT);
+  const int res_m = a.h_m[b * a.D + c * 16 + (threadIdx.x & 15)];   // residual, prefetched
+  const int res_e = a.h_e[b * (a.D / 16) + c];
   stage_x_bfp(xs, xes, a.att_m + b * a.D, a.att_e + b * (a.D / 16), nT);
   __syncthreads();
   long long A;
   int M;
   chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
-  if (threadIdx.x < 64) epi_ores(a, b, c, A, M, threadIdx.x < 16);
+  if (threadIdx.x < 64) epi_ores(a, b, c, A, M, threadIdx.x < 16, res_m, res_e);
 }
 
 // -------------------------------------------------------------------- gu
@@ -494,8 +526,8 @@ template <int NW, int TPT>
 __global__ __launch_bounds__(64 * NW) void k_gu(LayerArgs a) {
   extern __shared__ double dsm[];
   const int nT = a.D / 16;
-  double *dbuf = dsm;
-  double *leaf = dsm + a.D;
+  double *dbuf = dsm;             // 3*D
+  double *leaf = dsm + 3 * a.D;
   int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);
   int *xes = xs + nT * 16;
   __shared__ int redM[NW * 16];
@@ -533,12 +565,14 @@ __global__ __launch_bounds__(64 * NW) void k_d_res(LayerArgs a) {
   const int c = blockIdx.x, b = blockIdx.y;
   ChunkRegs<TPT> R;
   load_chunk<NW, TPT>(R, a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT);
+  const int res_m = a.h1_m[b * a.D + c * 16 + (threadIdx.x & 15)];   // residual, prefetched
+  const int res_e = a.h1_e[b * (a.D / 16) + c];
   stage_x_bfp(xs, xes, a.mlp_m + b * a.FFN, a.mlp_e + b * (a.FFN / 16), nT);
   __syncthreads();
   long long A;
   int M;
   chunk_AM<NW, TPT>(R, xs, xes, nT, redM, redA, A, M);
-  if (threadIdx.x < 64) epi_dres(a, b, c, A, M, threadIdx.x < 16);
+  if (threadIdx.x < 64) epi_dres(a, b, c, A, M, threadIdx.x < 16, res_m, res_e);
 }
 
 
@@ -555,8 +589,8 @@ __global__ __launch_bounds__(64 * NW) void k_d_res(LayerArgs a) {
 __global__ __launch_bounds__(256) void k_norm_seq(LayerArgs a, int which) {
   extern __shared__ double dsm[];
   const int nT = a.D / 16;
-  double *dbuf = dsm;
-  double *leaf = dsm + a.D;
+  double *dbuf = dsm;             // 3*D
+  double *leaf = dsm + 3 * a.D;
   int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);
   int *xes = xs + nT * 16;
   const int b = blockIdx.x;
@@ -626,7 +660,8 @@ __global__ __launch_bounds__(64 * NW) void k_o_res_m(LayerArgs a) {
   stage_x_bfp(xs, xes, a.att_m + b0 * a.D, a.att_e + b0 * (a.D / 16), ns * nT);
   __syncthreads();
   chunk_AM_multi<NW, TPT, MSEQ>(R, xs, xes, nT, ns, redM, redA, Ao, Mo);
-  BFP_MULTI_EPI(epi_ores(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_))
+  BFP_MULTI_EPI(epi_ores(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_,
+                         a.h_m[b * a.D + c * 16 + r_], a.h_e[b * (a.D / 16) + c]))
 }
 
 template <int NW, int TPT>
@@ -669,10 +704,61 @@ __global__ __launch_bounds__(64 * NW) void k_d_res_m(LayerArgs a) {
   stage_x_bfp(xs, xes, a.mlp_m + b0 * a.FFN, a.mlp_e + b0 * (a.FFN / 16), ns * nT);
   __syncthreads();
   chunk_AM_multi<NW, TPT, MSEQ>(R, xs, xes, nT, ns, redM, redA, Ao, Mo);
-  BFP_MULTI_EPI(epi_dres(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_))
+  BFP_MULTI_EPI(epi_dres(a, b, c, Ao[r_ * MSEQ + sc_], Mo[r_ * MSEQ + sc_], wr_,
+                         a.h1_m[b * a.D + c * 16 + r_], a.h1_e[b * (a.D / 16) + c]))
 }
 
 // ------------------------------------------------------------------ head
+// One step of a (value, index) argmax over lanes: larger value wins, the
+// lower index on ties (a total order, so any combining order gives the
+// first index of the maximum).
+template <int M>
+__device__ __forceinline__ void argmax_step(double &best, int &besti) {
+  const double ov = peer<M>(best);
+  const int oi = peer<M>(besti);
+  if (ov > best || (ov == best && oi < besti)) {
+    best = ov;
+    besti = oi;
+  }
+}
+
+// The decode head's final norm (full.py:438): hn = (h / sqrt(mean(h*h) +
+// 1e-5)) * w, float64, not re-quantised.  work: 3*D doubles of LDS, leaf:
+// PW_MAX_LEAVES; hn may alias work (LDS) or be global.  Loads are issued in
+// one batch per thread.  All threads call.
+__device__ void final_norm(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
+                           const double *__restrict__ w, int D, double *work, double *leaf,
+                           double *hn) {
+  const int bs = blockDim.x, tid = threadIdx.x;
+  double *sq = work, *xv = work + D, *wv = work + 2 * D;
+  for (int i0 = tid; i0 < D; i0 += 4 * bs) {
+    int m[4], e[4];
+    double ww[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      int i = i0 + k * bs;
+      i = i < D ? i : D - 1;
+      m[k] = hm[i];
+      e[k] = he[i >> 4];
+      ww[k] = w[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + k * bs;
+      if (i < D) {
+        const double x = bfp_val(m[k], e[k]);
+        sq[i] = x * x;
+        xv[i] = x;
+        wv[i] = ww[k];
+      }
+    }
+  }
+  __syncthreads();
+  const double s = pairwise_sum_block(sq, D, leaf);
+  const double rt = sqrt(s / (double)D + 1e-5);
+  for (int i = tid; i < D; i += bs) hn[i] = (xv[i] / rt) * wv[i];
+}
+
 // logits = ((h / sqrt(mean(h*h) + 1e-5)) * w) @ embed.T in float64
 // (full.py:438-440), with a per-workgroup first-index argmax.  Each row's
 // dot product: 16 lanes, lane l sums k = 64i + 4l + c (i ascending, c =
@@ -681,21 +767,12 @@ __global__ __launch_bounds__(64 * NW) void k_d_res_m(LayerArgs a) {
 // a few ulps.)
 __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
   extern __shared__ double dsm[];
-  double *hn = dsm;                    // D
-  double *leaf = dsm + a.D;            // PW_MAX_LEAVES
+  double *hn = dsm;                    // 3*D: the final norm's work space, then hn (D)
+  double *leaf = dsm + 3 * a.D;        // PW_MAX_LEAVES
   __shared__ double bv[16];
   __shared__ int bi[16];
   const int b = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
-  const int16_t *hm = a.h_m + b * a.D;
-  const int8_t *he = a.h_e + b * (a.D / 16);
-  for (int i = tid; i < a.D; i += blockDim.x) {
-    double x = bfp_val(hm[i], he[i >> 4]);
-    hn[i] = x * x;
-  }
-  __syncthreads();
-  const double s = pairwise_sum_block(hn, a.D, leaf);
-  const double rt = sqrt(s / (double)a.D + 1e-5);
-  for (int i = tid; i < a.D; i += blockDim.x) hn[i] = (bfp_val(hm[i], he[i >> 4]) / rt) * a.norm_w[i];
+  final_norm(a.h_m + b * a.D, a.h_e + b * (a.D / 16), a.norm_w, a.D, dsm, leaf, hn);
   __syncthreads();
 
   const int l16 = tid & 15, sub = tid >> 4;      // 16 row slots per pass
@@ -714,10 +791,10 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
       acc = fma((double)f.z, hp[2], acc);
       acc = fma((double)f.w, hp[3], acc);
     }
-    acc += __shfl_xor(acc, 8, 64);
-    acc += __shfl_xor(acc, 4, 64);
-    acc += __shfl_xor(acc, 2, 64);
-    acc += __shfl_xor(acc, 1, 64);
+    acc = psum<8>(acc);
+    acc = psum<4>(acc);
+    acc = psum<2>(acc);
+    acc = psum<1>(acc);
     if (a.logits && l16 == 0) a.logits[(long long)b * a.VOCAB + row] = acc;
     if (acc > best || (acc == best && row < besti)) {
       best = acc;
@@ -725,14 +802,8 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
     }
   }
   // workgroup argmax, first index on ties
-  for (int o = 16; o < 64; o <<= 1) {
-    double ov = __shfl_xor(best, o, 64);
-    int oi = __shfl_xor(besti, o, 64);
-    if (ov > best || (ov == best && oi < besti)) {
-      best = ov;
-      besti = oi;
-    }
-  }
+  argmax_step<16>(best, besti);
+  argmax_step<32>(best, besti);
   if ((tid & 63) == 0) {
     bv[tid >> 6] = best;
     bi[tid >> 6] = besti;
@@ -759,20 +830,9 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
 // logits are bit-identical to the batch-1 kernel's.
 __global__ __launch_bounds__(256) void k_head_norm(HeadArgs a) {
   extern __shared__ double dsm[];
-  double *hx = dsm;                    // D
-  double *leaf = dsm + a.D;            // PW_MAX_LEAVES
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const int16_t *hm = a.h_m + b * a.D;
-  const int8_t *he = a.h_e + b * (a.D / 16);
-  for (int i = tid; i < a.D; i += blockDim.x) {
-    double x = bfp_val(hm[i], he[i >> 4]);
-    hx[i] = x * x;
-  }
-  __syncthreads();
-  const double s = pairwise_sum_block(hx, a.D, leaf);
-  const double rt = sqrt(s / (double)a.D + 1e-5);
-  for (int i = tid; i < a.D; i += blockDim.x)
-    a.hn[(long long)b * a.D + i] = (bfp_val(hm[i], he[i >> 4]) / rt) * a.norm_w[i];
+  const int b = blockIdx.x;
+  final_norm(a.h_m + b * a.D, a.h_e + b * (a.D / 16), a.norm_w, a.D, dsm, dsm + 3 * a.D,
+             a.hn + (long long)b * a.D);
 }
 
 constexpr int HEAD_SEQ_GROUP = 16;   // most sequences staged in LDS at once
@@ -853,10 +913,10 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         double v = acc[r];
-        v += __shfl_xor(v, 8, 64);
-        v += __shfl_xor(v, 4, 64);
-        v += __shfl_xor(v, 2, 64);
-        v += __shfl_xor(v, 1, 64);
+        v = psum<8>(v);
+        v = psum<4>(v);
+        v = psum<2>(v);
+        v = psum<1>(v);
         const int row = row0 + slot + 16 * r;
         if (row < a.VOCAB) {
           if (a.logits && l16 == 0) a.logits[(long long)(b0 + bb) * a.VOCAB + row] = v;
@@ -866,14 +926,8 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
           }
         }
       }
-      for (int o = 16; o < 64; o <<= 1) {   // the wave's 4 row slots
-        double ov = __shfl_xor(best, o, 64);
-        int oi = __shfl_xor(besti, o, 64);
-        if (ov > best || (ov == best && oi < besti)) {
-          best = ov;
-          besti = oi;
-        }
-      }
+      argmax_step<16>(best, besti);   // the wave's 4 row slots
+      argmax_step<32>(best, besti);
       if (l == 0) {
         bv[w][bb] = best;
         bi[w][bb] = besti;
@@ -914,14 +968,12 @@ __global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
         besti = i;
       }
     }
-    for (int o = 1; o < 64; o <<= 1) {
-      double ov = __shfl_xor(best, o, 64);
-      int oi = __shfl_xor(besti, o, 64);
-      if (ov > best || (ov == best && oi < besti)) {
-        best = ov;
-        besti = oi;
-      }
-    }
+    argmax_step<1>(best, besti);
+    argmax_step<2>(best, besti);
+    argmax_step<4>(best, besti);
+    argmax_step<8>(best, besti);
+    argmax_step<16>(best, besti);
+    argmax_step<32>(best, besti);
     nid = besti;
   }
   if (l == 0) {
@@ -1035,7 +1087,7 @@ static int launch_layer_multi(const LayerArgs &a, hipStream_t s) {
   lkm_fn fd = pick_dres_m(nwf, tptf);
   if (!fq || !fo || !fg || !fd) return set_err(BFP_EINVAL, "no layer kernel for D=%d FFN=%d", a.D, a.FFN);
   const int nq = a.D + 2 * a.KV;
-  const size_t sh_norm = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
+  const size_t sh_norm = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
   const int G = (a.batch + MSEQ - 1) / MSEQ;
   const size_t shD = (size_t)MSEQ * nTD * 17 * 4, shF = (size_t)MSEQ * nTF * 17 * 4;
   hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 1);
@@ -1054,7 +1106,7 @@ int launch_layer(const LayerArgs &a, hipStream_t s) {
   int nw, tpt;
   shape_for(nTD, nw, tpt);
   const int nq = a.D + 2 * a.KV;
-  const size_t sh_norm = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
+  const size_t sh_norm = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
   lk_fn f = pick_qkv(nw, tpt);
   lk_fn fo = pick_ores(nw, tpt), fg = pick_gu(nw, tpt);
   if (!f || !fo || !fg) return set_err(BFP_EINVAL, "no layer kernel for D=%d", a.D);
@@ -1092,7 +1144,7 @@ int prepare_head_kernels(int D) {
 }
 
 int launch_head(const HeadArgs &a, hipStream_t s) {
-  size_t sh = (size_t)(a.D + PW_MAX_LEAVES) * 8;
+  size_t sh = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8;
   if (a.batch == 1) {
     hipLaunchKernelGGL(k_head_logits, dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
     return launch_status("head");

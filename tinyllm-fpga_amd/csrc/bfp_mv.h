@@ -124,8 +124,8 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
     }
   }
 #undef BFP_DOT2
-  M = xor_max(M, 16);
-  M = xor_max(M, 32);
+  M = pmax<16>(M);
+  M = pmax<32>(M);
   if (NW > 1) {
     if (tq == 0) redM[w * 16 + r] = M;
     __syncthreads();
@@ -139,8 +139,8 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
     int sh = M - E[j];
     if (sh <= ALIGN_MAX) A += S[j] >> sh;
   }
-  A = xor_sum(A, 16);
-  A = xor_sum(A, 32);
+  A = psum<16>(A);
+  A = psum<32>(A);
   if (NW > 1) {
     if (tq == 0) redA[w * 16 + r] = A;
     __syncthreads();
@@ -215,8 +215,8 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
 #undef BFP_DOT2
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    M[s] = xor_max(M[s], 16);
-    M[s] = xor_max(M[s], 32);
+    M[s] = pmax<16>(M[s]);
+    M[s] = pmax<32>(M[s]);
   }
   if (NW > 1) {
     if (tq == 0)
@@ -240,8 +240,8 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
       const int sh = M[s] - E[j][s];
       if (sh <= ALIGN_MAX) acc += Sv[j][s] >> sh;
     }
-    acc = xor_sum(acc, 16);
-    acc = xor_sum(acc, 32);
+    acc = psum<16>(acc);
+    acc = psum<32>(acc);
     A[s] = acc;
   }
   if (NW > 1) {
@@ -272,10 +272,10 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
 // raw tile_quantize of the exact outputs, as fp_quantize_vec forms it.
 __device__ __forceinline__ void chunk_quant(long long A, int M, int &m, int &e) {
   int L = row_log2(A, M);
-  L = xor_max(L, 1);
-  L = xor_max(L, 2);
-  L = xor_max(L, 4);
-  L = xor_max(L, 8);
+  L = pmax<1>(L);
+  L = pmax<2>(L);
+  L = pmax<4>(L);
+  L = pmax<8>(L);
   e = chunk_exp_from_lmax(L);
   m = rne_shr_clip(A, e + 15 - M);
 }
