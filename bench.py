@@ -151,6 +151,22 @@ def kernel_config(n_in):
     return nw, tpt
 
 
+def kernel_name(n_out, n_in, reps):
+    """The matvec kernel the library launches for this batch: the streaming
+    kernel when each workgroup of its fixed grid gets enough items (the
+    rule of launch_matvec in csrc/bfp_core.hip), else one chunk per
+    workgroup."""
+    import torch
+    nw, tpt = kernel_config(n_in)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    grid = cus * int(os.environ.get("BFP_STREAM_WG_PER_CU", "4") or 4)
+    items = (n_out // 16) * reps
+    per = -(-items // grid)
+    lds = (-(-per // (n_out // 16)) + 1) * (n_in // 16) * 17 * 4
+    stream = per >= int(os.environ.get("BFP_STREAM_MIN_ITEMS", "256") or 256) and lds <= 48 * 1024
+    return ("matvec_stream_kernel<%d,%d>" if stream else "matvec_kernel<%d,%d>") % (nw, tpt)
+
+
 def cpu_baseline(seconds):
     """The oracle's numpy matvec_hw_golden (restating full.py:217-233),
     single-threaded, on a bounded sample of the same sweep."""
@@ -291,15 +307,23 @@ def cpu_decode_baseline(max_steps=3):
 
 def stream_probe():
     """Practical HBM ceilings: a 1 GiB device-to-device copy (read + write
-    bytes) and a streaming read (float32 sum over 2 GiB)."""
+    bytes) and a plain 16-byte-load streaming read of 2 GiB (the library's
+    bfp_probe_read_d, contiguous range per workgroup, 4 workgroups per CU)."""
     import torch
+    from bfp import _dev
+    from bfp._lib import call
     a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
     a.fill_(1)
     f = torch.ones(1 << 29, dtype=torch.float32, device="cuda")
+    n_wg = torch.cuda.get_device_properties(0).multi_processor_count * 4
+    fold = torch.empty(n_wg, dtype=torch.int32, device="cuda")
+
+    def read():
+        call("bfp_probe_read_d", f.data_ptr(), 2 << 30, fold.data_ptr(), n_wg, _dev.stream())
     res = {}
     for name, fn, nbytes in (("copy_1GiB", lambda: b.copy_(a), 2 << 30),
-                             ("read_sum_2GiB", lambda: f.sum(), 2 << 30)):
+                             ("read_2GiB", read, 2 << 30)):
         fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -361,7 +385,7 @@ def main():
         gbs = c.bytes_per_launch() / (ms * 1e-3) / 1e9
         per_shape.append({"shape": f"{c.n_out}x{c.n_in}", "ms_per_launch": round(ms, 4),
                           "GB_s": round(gbs, 1), "ring": c.ring,
-                          "kernel": "matvec_kernel<%d,%d>" % kernel_config(c.n_in)})
+                          "kernel": kernel_name(c.n_out, c.n_in, c.reps)})
     total_bytes = sum(c.bytes_per_launch() for c in cases) * args.steps
     value = total_bytes / wall / 1e9
     # dominant kernel instantiation: the one with the most time

@@ -104,6 +104,12 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
                       const int16_t *x_m, const int8_t *x_e, long long x_stride, int16_t *y_m,
                       int8_t *y_e, long long y_stride, int waves, void *stream);
 
+/* Measurement probe, no reference counterpart: reads [p, p + bytes) once
+ * with 16-byte loads, each of n_wg workgroups of 256 threads streaming one
+ * contiguous range, writing one fold word per workgroup to out (n_wg words).  Its bytes / time is the
+ * practical HBM read ceiling the matvec is compared with.  bytes % 16 == 0. */
+int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, void *stream);
+
 /* Host-buffer convenience form of matvec_hw_golden: W in the reference
  * layout, x and y in host memory.  Allocates and frees device memory. */
 int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,

@@ -76,6 +76,51 @@ def test_matvec_integer_edges(gpu, n_out, n_in, espread):
     assert (ye == want_e).all() and (ym == want_m.reshape(-1)).all()
 
 
+def _ring_case(n_out, n_in, ring, n_mats, seed):
+    """n_mats problems over a ring of `ring` weight copies in one launch;
+    returns (W ring, X, ym, ye) with device results on the host."""
+    import torch
+    from bfp import _dev
+    from bfp._lib import call
+    rng = np.random.default_rng(seed)
+    W = rng.standard_normal((ring, n_out, n_in)).astype(np.float32) * np.float32(0.02)
+    X = rng.standard_normal((n_mats, n_in))
+    bm = n_out * n_in * 2
+    be = n_out * n_in // 16
+    Pm = torch.empty(ring * bm, dtype=torch.uint8, device="cuda")
+    Pe = torch.empty(ring * be, dtype=torch.uint8, device="cuda")
+    dW = _dev.to_dev(W)
+    for r in range(ring):
+        call("bfp_quantize_pack_f32_d", dW.data_ptr() + r * W[0].nbytes, n_out, n_in,
+             Pm.data_ptr() + r * bm, Pe.data_ptr() + r * be, _dev.stream())
+    xm, xe = sim.tile_quantize(X.reshape(-1))
+    dxm = _dev.to_dev(xm.reshape(n_mats, -1))
+    dxe = _dev.to_dev(xe.reshape(n_mats, -1))
+    ym = torch.empty(n_mats * n_out, dtype=torch.int16, device="cuda")
+    ye = torch.empty(n_mats * n_out // 16, dtype=torch.int8, device="cuda")
+    call("bfp_matvec_ring_d", Pm.data_ptr(), Pe.data_ptr(), n_out, n_in, n_mats, ring, bm, be,
+         dxm.data_ptr(), dxe.data_ptr(), n_in, ym.data_ptr(), ye.data_ptr(), n_out, 0,
+         _dev.stream())
+    return (W, xm.reshape(n_mats, -1, 16), xe.reshape(n_mats, -1),
+            ym.cpu().numpy().reshape(n_mats, -1), ye.cpu().numpy().reshape(n_mats, -1))
+
+
+@pytest.mark.parametrize("n_out,n_in,ring,n_mats", [(192, 576, 5, 401), (576, 1536, 3, 121),
+                                                    (16, 576, 7, 5003)],
+                         ids=["12chunk", "ffn-in", "1chunk"])
+def test_matvec_streaming_path(gpu, n_out, n_in, ring, n_mats):
+    """Long batches run the streaming kernel (fixed grid, contiguous item
+    ranges, double-buffered weight registers, inputs staged per range):
+    every problem bit-exact against the oracle, including ranges that span
+    several problems and an odd item count."""
+    print(f"[matvec] streaming {n_out}x{n_in} ring {ring} x {n_mats}", flush=True)
+    W, xm, xe, ym, ye = _ring_case(n_out, n_in, ring, n_mats, seed=n_mats)
+    Wq = [_oracle_quantize_W(W[r]) for r in range(ring)]
+    for i in range(n_mats):
+        want_m, want_e = sim.matvec_bfp(xm[i], xe[i], *Wq[i % ring])
+        assert (ye[i] == want_e).all() and (ym[i] == want_m.reshape(-1)).all(), f"problem {i}"
+
+
 def test_matvec_batched_ring(gpu):
     """n_mats problems in one launch over a ring of distinct weight copies."""
     import torch

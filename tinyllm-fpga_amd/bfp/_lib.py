@@ -55,6 +55,7 @@ SIGNATURES = {
     "bfp_matvec_ring_d": (i32, [vp, vp, i32, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64,
                                 i32, vp]),
     "bfp_matvec_h": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+    "bfp_probe_read_d": (i32, [vp, sz, vp, i32, vp]),
     "bfp_rtl_tables": (i32, [vp, vp, vp, i32, C.c_double]),
     "bfp_rtl_matvec_d": (i32, [vp, vp, vp, vp, i32, i32, vp, vp, vp]),
     "bfp_rtl_requant_d": (i32, [vp, vp, i32, vp, vp, vp]),

@@ -12,6 +12,7 @@
 // so a wave whose lanes are (row r = lane%16, tile t0 + lane/16) reads four
 // fully used 256-byte runs per 16-byte-per-lane load.
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -204,6 +205,133 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
   }
 }
 
+// Streaming form for long batches: a fixed grid in which workgroup w walks
+// the contiguous item range [w*per_wg, (w+1)*per_wg) (item = problem *
+// n_chunks + chunk, so a workgroup streams contiguous weight memory), with
+// two register sets: the next chunk's weights are in flight while the
+// current chunk is reduced and written.  The input vectors of the range's
+// problems (usually one or two) are staged once up front, so the loop has no
+// branch that issues loads.  Same engine, same results as matvec_kernel.
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void matvec_stream_kernel(
+    const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
+    long long smat_e, int nT, int n_chunks, int ring, const int16_t *__restrict__ xm,
+    const int8_t *__restrict__ xe, long long x_stride, int16_t *__restrict__ ym,
+    int8_t *__restrict__ ye, long long y_stride, long long n_items, long long per_wg) {
+  extern __shared__ int smem[];   // per staged problem: nT*16 (x) then nT (exponents)
+  __shared__ int redM[NW * 16];
+  __shared__ long long redA[NW * 16];
+  const long long i0 = blockIdx.x * per_wg;
+  const long long i1 = i0 + per_wg < n_items ? i0 + per_wg : n_items;
+  if (i0 >= i1) return;
+  const long long m0 = i0 / n_chunks, m1 = (i1 - 1) / n_chunks;
+  for (long long q = m0; q <= m1; ++q) {
+    int *xs = smem + (q - m0) * nT * 17;
+    stage_x_bfp(xs, xs + nT * 16, xm + q * x_stride, xe + q * (x_stride / 16), nT);
+  }
+
+  auto load = [&](long long it, ChunkRegs<TPT> &R) {
+    it = it < i1 ? it : i1 - 1;
+    const long long mat = it / n_chunks;
+    const int c = (int)(it - mat * n_chunks);
+    const long long wmat = ring > 0 ? mat % ring : mat;
+    load_chunk_nb<NW, TPT>(R, Pm + wmat * smat_m + (long long)c * nT * 32,
+                           Pe + wmat * smat_e + (long long)c * nT * 16, nT);
+  };
+  auto process = [&](long long it, const ChunkRegs<TPT> &R) {
+    const bool store = it < i1;
+    it = store ? it : i1 - 1;
+    const long long mat = it / n_chunks;
+    const int c = (int)(it - mat * n_chunks);
+    const int *xs = smem + (mat - m0) * nT * 17;
+    long long A;
+    int M;
+    chunk_AM<NW, TPT>(R, xs, xs + nT * 16, nT, redM, redA, A, M);
+    if (threadIdx.x < 64) {
+      int m, e;
+      chunk_quant(A, M, m, e);
+      const int lane = threadIdx.x;
+      if (store && lane < 16) ym[mat * y_stride + c * 16 + lane] = (int16_t)m;
+      if (store && lane == 0) ye[mat * (y_stride / 16) + c] = (int8_t)e;
+    }
+  };
+
+  ChunkRegs<TPT> RA, RB;
+  load(i0, RA);
+  __syncthreads();   // staged inputs visible
+  for (long long k = i0; k < i1; k += 2) {
+    load(k + 1, RB);
+    process(k, RA);
+    load(k + 2, RA);
+    process(k + 1, RB);
+  }
+}
+
+// Read-only streaming probe: workgroup w reads the contiguous range
+// [w*per, (w+1)*per) of 16-byte words, eight loads in flight per thread
+// (addresses clamped, so there is no branch around a load), folded into one
+// word per workgroup so the loads cannot be dropped.  Measures the
+// practical HBM read ceiling with the access pattern of the streaming matvec.
+__global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *__restrict__ p,
+                                                         long long n16, long long per,
+                                                         unsigned *__restrict__ out) {
+  const long long i0 = blockIdx.x * per;
+  const long long i1 = i0 + per < n16 ? i0 + per : n16;
+  unsigned acc = 0;
+  for (long long b = i0; b < i1; b += 8 * 256) {
+    uint4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      long long i = b + k * 256 + threadIdx.x;
+      v[k] = p[i < i1 ? i : i1 - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+  }
+  acc = acc ^ (unsigned)peer<1>((int)acc);
+  if (threadIdx.x == 0) out[blockIdx.x] = acc;
+}
+
+typedef void (*matvec_stream_fn)(const uint4 *, const int8_t *, long long, long long, int, int,
+                                 int, const int16_t *, const int8_t *, long long, int16_t *,
+                                 int8_t *, long long, long long, long long);
+
+template <int NW>
+static matvec_stream_fn pick_stream_tpt(int tpt) {
+  if (tpt <= 1) return matvec_stream_kernel<NW, 1>;
+  if (tpt <= 2) return matvec_stream_kernel<NW, 2>;
+  if (tpt <= 3) return matvec_stream_kernel<NW, 3>;
+  if (tpt <= 4) return matvec_stream_kernel<NW, 4>;
+  if (tpt <= 6) return matvec_stream_kernel<NW, 6>;
+  if (tpt <= 8) return matvec_stream_kernel<NW, 8>;
+  return nullptr;
+}
+
+static matvec_stream_fn pick_matvec_stream(int nw, int tpt) {
+  switch (nw) {
+    case 1: return pick_stream_tpt<1>(tpt);
+    case 2: return pick_stream_tpt<2>(tpt);
+    case 3: return pick_stream_tpt<3>(tpt);
+    case 4: return pick_stream_tpt<4>(tpt);
+    case 6: return pick_stream_tpt<6>(tpt);
+    case 8: return pick_stream_tpt<8>(tpt);
+    case 9: return pick_stream_tpt<9>(tpt);
+    default: return nullptr;
+  }
+}
+
+static int device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
 typedef void (*matvec_fn)(const uint4 *, const int8_t *, long long, long long, int, int, int,
                           const int16_t *, const int8_t *, long long, int16_t *, int8_t *,
                           long long);
@@ -244,6 +372,24 @@ int default_waves(int nT) {
   return 9;
 }
 
+// Streaming matvec grid: workgroups per CU, and the fewest items per
+// workgroup for which the streaming kernel is used (tuning knobs
+// BFP_STREAM_WG_PER_CU, BFP_STREAM_MIN_ITEMS).
+static int env_int(const char *name, int dflt) {
+  const char *v = getenv(name);
+  if (!v || !*v) return dflt;
+  const int x = atoi(v);
+  return x > 0 ? x : dflt;
+}
+static int stream_wg_per_cu() {
+  static const int v = env_int("BFP_STREAM_WG_PER_CU", 4);
+  return v;
+}
+static int stream_min_items() {
+  static const int v = env_int("BFP_STREAM_MIN_ITEMS", 256);
+  return v;
+}
+
 int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats, int ring,
                   long long smat_m, long long smat_e, const int16_t *x_m, const int8_t *x_e,
                   long long x_stride, int16_t *y_m, int8_t *y_e, long long y_stride, int waves,
@@ -267,6 +413,19 @@ int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_m
   if (blocks > INT_MAX) return set_err(BFP_EINVAL, "matvec: grid too large");
   size_t shm = (size_t)nT * 17 * sizeof(int);
   if (shm > 60 * 1024) return set_err(BFP_EINVAL, "matvec: n_in=%d too large", n_in);
+  // long batches: the streaming kernel, STREAM_WG_PER_CU workgroups per CU
+  matvec_stream_fn sfn = pick_matvec_stream(nw, tpt);
+  const long long grid = (long long)device_cus() * stream_wg_per_cu();
+  const long long per = (blocks + grid - 1) / grid;
+  const size_t shs = (size_t)((per + n_chunks - 1) / n_chunks + 1) * nT * 17 * sizeof(int);
+  if (sfn && per >= stream_min_items() && shs <= 48 * 1024) {
+    const long long nwg = (blocks + per - 1) / per;
+    hipLaunchKernelGGL(sfn, dim3((unsigned)nwg), dim3(64 * nw), shs, stream,
+                       reinterpret_cast<const uint4 *>(P_m), reinterpret_cast<const int8_t *>(P_e),
+                       smat_m / 16, smat_e, nT, n_chunks, ring, x_m, x_e, x_stride, y_m, y_e,
+                       y_stride, blocks, per);
+    return launch_status("matvec");
+  }
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * nw), shm, stream,
                      reinterpret_cast<const uint4 *>(P_m), reinterpret_cast<const int8_t *>(P_e),
                      smat_m / 16, smat_e, nT, n_chunks, ring, x_m, x_e, x_stride, y_m, y_e,
@@ -395,6 +554,17 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
                       int8_t *y_e, long long y_stride, int waves, void *stream) {
   return bfp::launch_matvec(P_m, P_e, n_out, n_in, n_mats, ring, mat_stride_m, mat_stride_e, x_m,
                             x_e, x_stride, y_m, y_e, y_stride, waves, (hipStream_t)stream);
+}
+
+int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, void *stream) {
+  if (!p || !out || n_wg <= 0 || bytes % 16)
+    return set_err(BFP_EINVAL, "probe_read: bad arguments (bytes=%zu n_wg=%d)", bytes, n_wg);
+  const long long n16 = (long long)(bytes / 16);
+  const long long per = (n16 + n_wg - 1) / n_wg;
+  hipLaunchKernelGGL(probe_read_kernel, dim3(n_wg), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const uint4 *>(p), n16, per,
+                     reinterpret_cast<unsigned *>(out));
+  return launch_status("probe_read");
 }
 
 int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,

@@ -44,6 +44,24 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<TPT> &R, const uint4 *__res
   }
 }
 
+// Same, with every load unconditional (tiles past nT re-read tile nT-1; the
+// engine ignores those lanes), so the loads of several chunks can be kept in
+// flight without the compiler draining them at a branch.
+template <int NW, int TPT>
+__device__ __forceinline__ void load_chunk_nb(ChunkRegs<TPT> &R, const uint4 *__restrict__ pm,
+                                              const int8_t *__restrict__ pe, int nT) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    int t = tq + 4 * (w + NW * j);
+    t = t < nT ? t : nT - 1;
+    R.a[j] = pm[t * 32 + r];
+    R.b[j] = pm[t * 32 + 16 + r];
+    R.e[j] = pe[t * 16 + r];
+  }
+}
+
 // LDS form of the input vector: per tile 8 dwords of packed (xh, xh) int16
 // pairs then 8 dwords of (xl, xl) pairs, with x = 256*xh + xl.
 __device__ __forceinline__ void put_x_pair(int *xs, int t, int k, int lo, int hi) {
