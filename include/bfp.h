@@ -65,6 +65,17 @@ size_t bfp_packed_bytes_e(int n_out, int n_in);
 int bfp_pack_d(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
                void *P_m, void *P_e, void *stream);
 
+/* The reference's wide layout -> device layout.  wide_m: (n_out/16, n_in, 16)
+ * int16, one 32-byte entry per (16-row chunk, input column) with row
+ * chunk*16 + lane at lane; wide_e: (n_out/16, n_in/16, 16) int8, one
+ * 16-byte entry per (chunk, tile).  This is the format of the FPGA's DDR3
+ * weight image (gen_smollm_blockfp_ddr.py:88-119, read by
+ * weight_streamer_bfp_mt.sv at the lbfp_ddr3.svh offsets) and of the
+ * per-matrix hex sets (gen_smollm_blockfp_full.py:131-161), one layer of one
+ * matrix at a time. */
+int bfp_pack_wide_d(const void *wide_m, const void *wide_e, int n_out, int n_in, void *P_m,
+                    void *P_e, void *stream);
+
 /* Device layout -> reference layout (inverse of bfp_pack_d). */
 int bfp_unpack_d(const void *P_m, const void *P_e, int n_out, int n_in,
                  int16_t *W_m, int8_t *W_e, void *stream);
@@ -178,6 +189,14 @@ int bfp_get_dims(const bfp_ctx *ctx, bfp_dims *out);
 int bfp_load_weights(bfp_ctx *ctx, int which, int layer, const float *fp32, const int16_t *m,
                      const int8_t *e);
 
+/* Load one matrix of one layer (which = BFP_WQ .. BFP_WD) from host
+ * buffers in the reference's wide layout (see bfp_pack_wide_d): the region
+ * slice of a DDR3 weight image or of a *_m.hex/_e.hex set for that layer.
+ * Replaces the FPGA's weight streamer reading the image
+ * (weight_streamer_bfp_mt.sv, lbfp_ddr3.svh:45-86). */
+int bfp_load_weights_wide(bfp_ctx *ctx, int which, int layer, const void *wide_m,
+                          const void *wide_e);
+
 /* Zero the KV cache (the reference starts every run from zeros, full.py:426-428). */
 int bfp_reset_kv(bfp_ctx *ctx);
 
@@ -218,6 +237,12 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * The KV cache is overwritten from position 0. */
 #define BFP_DECODE_NO_GRAPH 1
 #define BFP_DECODE_STEP_TIMES 2   /* record one HIP event per step */
+/* Loop policy of the FPGA driver (autoregress_bfp_top.sv:357-386, the
+ * tb_full_bfp.cpp auto-feed run) instead of the simulator's: step s feeds
+ * prompt[s] while s < n_prompt, else step s-1's argmax (no repeat of the last
+ * prompt token); every step's argmax is recorded, so tokens_out holds
+ * batch x (n_prompt + n_gen) tokens (the RTL's result_buf / RTL_TOKENS). */
+#define BFP_DECODE_RTL_LOOP 4
 int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int batch,
                int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags);
 

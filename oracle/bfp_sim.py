@@ -301,6 +301,29 @@ def decode(model: Model, prompt, n_gen, max_ctx=None, on_layer=None, on_step=Non
     return generated
 
 
+def decode_rtl_loop(model: Model, prompt, n_gen, max_ctx=None, on_layer=None):
+    """The FPGA driver's token loop (autoregress_bfp_top.sv:357-386; the
+    auto-feed run of sim/tb_full_bfp.cpp:66-74) over sim A's arithmetic:
+    step s feeds prompt[s] while s < len(prompt), else the prediction of step
+    s-1, and every step's prediction is recorded (result_buf[step]).
+    Returns the len(prompt) + n_gen predictions."""
+    dims = model.dims
+    ids = [int(t) for t in prompt]
+    steps = len(ids) + n_gen
+    n_ctx = max_ctx if max_ctx is not None else max(dims.MAX_CTX, steps)
+    kv = [new_kv(dims, n_ctx) for _ in range(dims.NL)]
+    preds = []
+    for step in range(steps):
+        tid = ids[step] if step < len(ids) else preds[-1]
+        h = model.embed_row_q(tid)
+        for li in range(dims.NL):
+            h = fwd_layer(h, model.layers[li], pos=step, kv=kv[li], kv_pos=step, dims=dims)
+            if on_layer is not None:
+                on_layer(step, li, h)
+        preds.append(head_argmax(h, model.norm_w_q, model.embed))
+    return preds
+
+
 # ---------------------------------------------------------------------------
 # Restatements of third-party reduction orders (pinned by tests against the
 # library calls themselves)

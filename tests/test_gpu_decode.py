@@ -87,6 +87,21 @@ def test_decode_single_token_prompt(gpu):
     gm.close()
 
 
+@pytest.mark.parametrize("graph", [True, False], ids=["graph", "direct"])
+def test_decode_rtl_loop(gpu, graph):
+    """The FPGA driver's loop policy (autoregress_bfp_top.sv:357-386): every
+    step's prediction, the step after the prompt fed by the last prediction;
+    batched sequences against the oracle's restatement."""
+    d, om, gm = _setup(TINY, seed=13, max_batch=3)
+    from bfp import synth
+    prompts = np.stack([synth.make_prompt(d, 4, seed=40 + b) for b in range(3)])
+    toks, _ = gm.decode(prompts, 7, graph=graph, rtl_loop=True)
+    assert toks.shape == (3, 11)
+    for b in range(3):
+        assert list(toks[b]) == sim.decode_rtl_loop(om, prompts[b], 7), f"sequence {b}"
+    gm.close()
+
+
 def test_decode_errors(gpu):
     from bfp._lib import BfpError
     d, om, gm = _setup(TINY, seed=8)

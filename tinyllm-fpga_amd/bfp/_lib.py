@@ -56,6 +56,8 @@ SIGNATURES = {
                                 i32, vp]),
     "bfp_matvec_h": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
     "bfp_probe_read_d": (i32, [vp, sz, vp, i32, vp]),
+    "bfp_pack_wide_d": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "bfp_load_weights_wide": (i32, [vp, i32, i32, vp, vp]),
     "bfp_rtl_tables": (i32, [vp, vp, vp, i32, C.c_double]),
     "bfp_rtl_matvec_d": (i32, [vp, vp, vp, vp, i32, i32, vp, vp, vp]),
     "bfp_rtl_requant_d": (i32, [vp, vp, i32, vp, vp, vp]),

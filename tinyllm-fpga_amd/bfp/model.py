@@ -84,6 +84,18 @@ class BfpModel:
         self.load_tensor("embed", fp32=fm.embed)
         self.load_tensor("norm_w", fp32=fm.norm_w)
 
+    def load_ddr_image(self, path):
+        """Load the reference's DDR3 weight image (<PREFIX>DDR3.bin,
+        gen_smollm_blockfp_ddr.py) -- see bfp.image."""
+        from .image import WeightImage, load_image
+        load_image(self, WeightImage.from_ddr(path, self.dims))
+
+    def load_hex_dir(self, directory, prefix="lbfp_full_"):
+        """Load the reference's per-tensor hex set (<PREFIX><TAG>_{m,e}.hex,
+        gen_smollm_blockfp_full.py) -- see bfp.image."""
+        from .image import WeightImage, load_image
+        load_image(self, WeightImage.from_hex_dir(directory, self.dims, prefix))
+
     def reset_kv(self):
         call("bfp_reset_kv", self._h)
 
@@ -153,23 +165,29 @@ class BfpModel:
         return am, lg
 
     # --------------------------------------------------------------- decode
-    def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False):
+    def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False, rtl_loop=False):
         """Greedy decode (full.py:426-443) of a batch of prompts
         (batch, n_prompt).  Returns (tokens (batch, n_gen), hist) where hist
-        is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16))."""
+        is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16)).
+
+        rtl_loop=True runs the FPGA driver's loop policy instead
+        (autoregress_bfp_top.sv:357-386): the step after the prompt feeds
+        the last prediction, and the tokens returned are every step's
+        prediction, (batch, n_prompt + n_gen)."""
         P = np.ascontiguousarray(np.atleast_2d(np.asarray(prompts, dtype=np.int32)))
         batch, n_prompt = P.shape
-        toks = np.zeros((batch, max(n_gen, 1)), np.int32)
+        steps = n_prompt + n_gen
+        n_out = steps if rtl_loop else n_gen
+        toks = np.zeros((batch, max(n_out, 1)), np.int32)
         hm = he = None
         d = self.dims
         if hist:
-            steps = n_prompt + n_gen
             hm = np.zeros((batch, steps, d.NL, d.D), np.int16)
             he = np.zeros((batch, steps, d.NL, d.D // 16), np.int8)
-        flags = (0 if graph else 1) | (2 if step_times else 0)
+        flags = (0 if graph else 1) | (2 if step_times else 0) | (4 if rtl_loop else 0)
         call("bfp_decode", self._h, _p(P), n_prompt, n_gen, batch, _p(toks),
              _p(hm) if hist else None, _p(he) if hist else None, flags)
-        return toks[:, :n_gen], ((hm, he) if hist else None)
+        return toks[:, :n_out], ((hm, he) if hist else None)
 
     def step_times_ms(self):
         """Per-step device times of the last decode(step_times=True)."""

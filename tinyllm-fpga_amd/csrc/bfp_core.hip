@@ -161,6 +161,40 @@ __global__ void quantize_pack_f32_kernel(const float *__restrict__ W, long long 
   Pe[(c * nT + t) * 16 + r] = (int8_t)ex;
 }
 
+// The reference's wide layout (gen_smollm_blockfp_ddr.py:88-119, the DDR3
+// image and the *_m.hex/_e.hex sets of gen_smollm_blockfp_full.py:131-161):
+// mantissa entry (chunk, col) = 16 lanes (rows chunk*16 .. +15) x int16 LE,
+// exponent entry (chunk, tile) = 16 lanes x int8.  Repacked into this
+// build's device layout; source chunk c goes to destination chunk c*cstride.
+// The exponent entries are already in the device order (per chunk and tile,
+// one byte per row).
+__global__ void pack_wide_m_kernel(const int16_t *__restrict__ Wm, long long total, int nT,
+                                   int cstride, uint4 *__restrict__ Pm) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int r = (int)(i & 15), h = (int)((i >> 4) & 1);
+  const long long ct = i >> 5;
+  const long long c = ct / nT;
+  const int t = (int)(ct % nT);
+  const int16_t *src = Wm + (c * nT * 16 + t * 16 + 8 * h) * 16 + r;   // col t*16 + 8h, lane r
+  unsigned v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    v[k] = ((unsigned)(unsigned short)src[(2 * k) * 16]) |
+           ((unsigned)(unsigned short)src[(2 * k + 1) * 16] << 16);
+  Pm[((c * cstride) * nT + t) * 32 + h * 16 + r] = make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__global__ void pack_wide_e_kernel(const int8_t *__restrict__ We, long long total, int nT,
+                                   int cstride, int8_t *__restrict__ Pe) {
+  long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const long long ct = i >> 4;
+  const long long c = ct / nT;
+  const int t = (int)(ct % nT);
+  Pe[((c * cstride) * nT + t) * 16 + (i & 15)] = We[i];
+}
+
 __global__ void tile_decode_kernel(const int16_t *__restrict__ m, const int8_t *__restrict__ e,
                                    long long n, double *__restrict__ v) {
   long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
@@ -456,6 +490,21 @@ int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, 
   return launch_status("pack");
 }
 
+int pack_wide(const void *wide_m, const void *wide_e, int n_out, int n_in, void *P_m, void *P_e,
+              hipStream_t s, int cstride) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !wide_m || !wide_e || !P_m || !P_e)
+    return set_err(BFP_EINVAL, "pack_wide: bad arguments (n_out=%d n_in=%d)", n_out, n_in);
+  int nT = n_in / 16;
+  long long tm = (long long)(n_out / 16) * nT * 32, te = (long long)(n_out / 16) * nT * 16;
+  hipLaunchKernelGGL(pack_wide_m_kernel, dim3(nblk(tm, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const int16_t *>(wide_m), tm, nT, cstride,
+                     reinterpret_cast<uint4 *>(P_m));
+  hipLaunchKernelGGL(pack_wide_e_kernel, dim3(nblk(te, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const int8_t *>(wide_e), te, nT, cstride,
+                     reinterpret_cast<int8_t *>(P_e));
+  return launch_status("pack_wide");
+}
+
 int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s,
                       int cstride) {
   if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || !W || !P_m || !P_e)
@@ -554,6 +603,11 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
                       int8_t *y_e, long long y_stride, int waves, void *stream) {
   return bfp::launch_matvec(P_m, P_e, n_out, n_in, n_mats, ring, mat_stride_m, mat_stride_e, x_m,
                             x_e, x_stride, y_m, y_e, y_stride, waves, (hipStream_t)stream);
+}
+
+int bfp_pack_wide_d(const void *wide_m, const void *wide_e, int n_out, int n_in, void *P_m,
+                    void *P_e, void *stream) {
+  return bfp::pack_wide(wide_m, wide_e, n_out, n_in, P_m, P_e, (hipStream_t)stream);
 }
 
 int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, void *stream) {

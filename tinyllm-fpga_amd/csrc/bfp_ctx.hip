@@ -274,6 +274,57 @@ int bfp_get_dims(const bfp_ctx *c, bfp_dims *out) {
 // weight: float32 (quantised to BFP-exact float64 as fp_quantize_vec does,
 // full.py:322-323,413) or (m, e).  The embedding must be float32: the head
 // uses the raw table (full.py:439).
+int bfp_load_weights_wide(bfp_ctx *c, int which, int layer, const void *wide_m,
+                          const void *wide_e) {
+  if (!c || !wide_m || !wide_e) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  const int KV = d.H_KV * d.HD;
+  if (which < BFP_WQ || which > BFP_WD)
+    return set_err(BFP_EINVAL, "wide layout is for matrices BFP_WQ..BFP_WD, not slot %d", which);
+  if (layer < 0 || layer >= d.NL) return set_err(BFP_EINVAL, "layer %d out of range [0, %d)", layer, d.NL);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  int n_out = d.D, n_in = d.D, cstride = 1;
+  uint8_t *Pm = nullptr;
+  int8_t *Pe = nullptr;
+  switch (which) {
+    case BFP_WQ: case BFP_WK: case BFP_WV: {
+      const int row0 = which == BFP_WQ ? 0 : (which == BFP_WK ? d.D : d.D + KV);
+      n_out = which == BFP_WQ ? d.D : KV;
+      Pm = c->qkv_m + layer * c->s_qkv_m + (size_t)row0 * d.D * 2;
+      Pe = c->qkv_e + layer * c->s_qkv_e + (size_t)row0 * d.D / 16;
+      break;
+    }
+    case BFP_WO:
+      Pm = c->o_m + layer * c->s_o_m;
+      Pe = c->o_e + layer * c->s_o_e;
+      break;
+    case BFP_WG: case BFP_WU: {
+      n_out = d.FFN;
+      cstride = 2;
+      const size_t off = which == BFP_WG ? 0 : 1;   // chunks interleaved G0 U0 G1 U1 ...
+      Pm = c->gu_m + layer * c->s_gu_m + off * (size_t)16 * d.D * 2;
+      Pe = c->gu_e + layer * c->s_gu_e + off * (size_t)16 * d.D / 16;
+      break;
+    }
+    default:   // BFP_WD
+      n_in = d.FFN;
+      Pm = c->d_m + layer * c->s_d_m;
+      Pe = c->d_e + layer * c->s_d_e;
+      break;
+  }
+  const size_t bm = (size_t)n_out * n_in * 2, be = (size_t)n_out * n_in / 16;
+  DevBuf tmp;
+  void *dm, *de;
+  BFP_TRY(tmp.alloc(&dm, bm));
+  BFP_TRY(tmp.alloc(&de, be));
+  HIP_TRY(hipMemcpyAsync(dm, wide_m, bm, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(de, wide_e, be, hipMemcpyHostToDevice, s));
+  BFP_TRY(pack_wide(dm, de, n_out, n_in, Pm, Pe, s, cstride));
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
 int bfp_load_weights(bfp_ctx *c, int which, int layer, const float *fp32, const int16_t *m,
                      const int8_t *e) {
   if (!c) return set_err(BFP_EINVAL, "null context");
@@ -494,7 +545,8 @@ int bfp_head(bfp_ctx *c, int batch, const int16_t *h_m, const int8_t *h_e, doubl
 // (batch, n_prompt + n_gen, NL, D) and (..., D/16).
 int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int batch,
                int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags) {
-  if (!c || !prompt || (!tokens_out && n_gen > 0)) return set_err(BFP_EINVAL, "null argument");
+  if (!c || !prompt || (!tokens_out && (n_gen > 0 || (flags & BFP_DECODE_RTL_LOOP))))
+    return set_err(BFP_EINVAL, "null argument");
   const bfp_dims &d = c->d;
   if (n_prompt < 1 || n_gen < 0) return set_err(BFP_EINVAL, "n_prompt=%d n_gen=%d", n_prompt, n_gen);
   if (batch <= 0 || batch > c->max_batch) return set_err(BFP_EINVAL, "batch %d out of range", batch);
@@ -510,7 +562,9 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   DevBuf tmp;
   int *dprompt, *dout;
   BFP_TRY(tmp.alloc((void **)&dprompt, sizeof(int) * batch * n_prompt));
-  BFP_TRY(tmp.alloc((void **)&dout, sizeof(int) * batch * (n_gen > 0 ? n_gen : 1)));
+  const bool rtl_loop = (flags & BFP_DECODE_RTL_LOOP) != 0;
+  const int n_out = rtl_loop ? steps : n_gen;   // tokens recorded per sequence
+  BFP_TRY(tmp.alloc((void **)&dout, sizeof(int) * batch * (n_out > 0 ? n_out : 1)));
   int16_t *dhm = nullptr;
   int8_t *dhe = nullptr;
   if (hist_m && hist_e) {
@@ -526,7 +580,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
   HeadArgs ha = head_args(c, batch, nullptr);
   CtlArgs ca{batch, n_prompt, n_gen, ha.n_wg, 0, c->state, dprompt, dout, c->part_v,
-             c->part_i, c->last};
+             c->part_i, c->last, rtl_loop ? 1 : 0};
   auto enqueue_step = [&](bool head) -> int {
     BFP_TRY(launch_embed(ea, s));
     for (int l = 0; l < d.NL; ++l) {
@@ -572,7 +626,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     (void)hipEventCreate(&evg);
     (void)hipEventRecord(ev0, s);
     for (int step = 0; step < steps && !rc; ++step) {
-      const bool head = step >= n_prompt - 1;
+      const bool head = rtl_loop || step >= n_prompt - 1;
       if (step == n_prompt) (void)hipEventRecord(evg, s);
       if (per_step) (void)hipEventRecord(sev[step], s);
       if (use_graph) {
@@ -612,8 +666,8 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   if (ev1) (void)hipEventDestroy(ev1);
   if (evg) (void)hipEventDestroy(evg);
   if (rc) return rc;
-  if (n_gen > 0)
-    HIP_TRY(hipMemcpy(tokens_out, dout, sizeof(int) * batch * n_gen, hipMemcpyDeviceToHost));
+  if (n_out > 0)
+    HIP_TRY(hipMemcpy(tokens_out, dout, sizeof(int) * batch * n_out, hipMemcpyDeviceToHost));
   if (dhm) {
     HIP_TRY(hipMemcpy(hist_m, dhm, (size_t)batch * steps * d.NL * d.D * 2, hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(hist_e, dhe, (size_t)batch * steps * d.NL * d.D / 16, hipMemcpyDeviceToHost));

@@ -56,6 +56,8 @@ int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, 
          hipStream_t s, int cstride = 1);
 int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s,
                       int cstride = 1);
+int pack_wide(const void *wide_m, const void *wide_e, int n_out, int n_in, void *P_m, void *P_e,
+              hipStream_t s, int cstride = 1);
 int tile_quantize_f64(const double *v, size_t n, int16_t *m, int8_t *e, hipStream_t s);
 
 }  // namespace bfp

@@ -68,9 +68,10 @@ struct CtlArgs {
   int batch, n_prompt, n_gen, n_wg, head;
   int *state;                 // [0] = step; [1 + b] = next input token of sequence b
   const int *prompt;          // (batch, n_prompt)
-  int *out;                   // (batch, n_gen)
+  int *out;                   // (batch, n_gen); (batch, n_prompt + n_gen) with rtl_loop
   const double *part_v; const int *part_i;
   int *last;                  // (batch,) argmax of the last head evaluation
+  int rtl_loop;               // loop policy of the FPGA driver instead of the simulator's
 };
 
 struct EmbedArgs {

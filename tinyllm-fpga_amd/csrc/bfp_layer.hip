@@ -953,6 +953,9 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
 // prompt[s+1] while s+1 < n_prompt, prompt[n_prompt-1] again at
 // s+1 == n_prompt (the reference feeds generated[-1], still the last prompt
 // token), else the argmax.
+// With rtl_loop, the policy of the FPGA driver (autoregress_bfp_top.sv
+// :357-386): every step's argmax is recorded (result_buf[step]) and the
+// next input is prompt[s+1] while s+1 < n_prompt, else this step's argmax.
 __global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
   const int b = blockIdx.x, l = threadIdx.x;
   const int s = a.state[0];
@@ -978,14 +981,21 @@ __global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
   }
   if (l == 0) {
     if (a.head) a.last[b] = nid;
-    if (a.head && s >= a.n_prompt && s - a.n_prompt < a.n_gen) a.out[b * a.n_gen + (s - a.n_prompt)] = nid;
     int next;
-    if (s + 1 < a.n_prompt)
-      next = a.prompt[b * a.n_prompt + s + 1];
-    else if (s + 1 == a.n_prompt)
-      next = a.prompt[b * a.n_prompt + a.n_prompt - 1];
-    else
-      next = nid;
+    if (a.rtl_loop) {
+      const int steps = a.n_prompt + a.n_gen;
+      if (a.head && s < steps) a.out[b * steps + s] = nid;
+      next = s + 1 < a.n_prompt ? a.prompt[b * a.n_prompt + s + 1] : nid;
+    } else {
+      if (a.head && s >= a.n_prompt && s - a.n_prompt < a.n_gen)
+        a.out[b * a.n_gen + (s - a.n_prompt)] = nid;
+      if (s + 1 < a.n_prompt)
+        next = a.prompt[b * a.n_prompt + s + 1];
+      else if (s + 1 == a.n_prompt)
+        next = a.prompt[b * a.n_prompt + a.n_prompt - 1];
+      else
+        next = nid;
+    }
     a.state[1 + b] = next;
   }
 }
