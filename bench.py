@@ -51,11 +51,17 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-3 decode leg")
     ap.add_argument("--decode-reps", type=int, default=3)
-    ap.add_argument("--long", action="store_true", help="also run config 4 (long context)")
-    ap.add_argument("--batch64", action="store_true", help="also run config 5 (batch 64)")
-    ap.add_argument("--probe", action="store_true",
-                    help="also time a 1 GiB device copy and a 2 GiB streaming read "
-                         "(practical HBM ceiling; the copy calibrates rocprof counters)")
+    ap.add_argument("--long", dest="long", action="store_true", default=True,
+                    help="run config 4 (long context; on by default)")
+    ap.add_argument("--no-long", dest="long", action="store_false", help="skip config 4")
+    ap.add_argument("--batch64", dest="batch64", action="store_true", default=True,
+                    help="run config 5 (batch 64; on by default)")
+    ap.add_argument("--no-batch64", dest="batch64", action="store_false", help="skip config 5")
+    ap.add_argument("--no-layer", action="store_true", help="skip the config-1 layer-step leg")
+    ap.add_argument("--probe", dest="probe", action="store_true", default=True,
+                    help="time a 1 GiB device copy and a 2 GiB streaming read (practical HBM "
+                         "ceiling; the copy calibrates rocprof counters; on by default)")
+    ap.add_argument("--no-probe", dest="probe", action="store_false")
     return ap.parse_args()
 
 
@@ -289,6 +295,35 @@ def batch_leg():
             "ms_per_step": round(g / n_gen, 4), "seq0_matches_reference": exact}
 
 
+def layer_leg():
+    """the cost of one SmolLM2-135M-shaped decoder layer
+    step at batch 1 inside the graph-replayed decode (positions 0..6 of an
+    8-token prompt), as the marginal per-step time of a 10-layer over a
+    2-layer model (HIP events per step; embedding and controller cancel).
+    Parity of this layer against the reference's own fwd_layer is the GPU
+    test test_config1_on_gpu."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    t = {}
+    for nl in (2, 10):
+        d = Dims(NL=nl, MAX_CTX=8)
+        gm = BfpModel(d)
+        gm.load_fp32(synth.make_model(d, seed=1))
+        prompt = synth.make_prompt(d, 8, seed=1)
+        gm.decode(prompt[None, :], 0)                       # warm-up + graph build
+        best = None
+        for _ in range(5):
+            gm.decode(prompt[None, :], 0, step_times=True)
+            st = gm.step_times_ms()[:7]                    # steps without the head
+            best = st if best is None else np.minimum(best, st)
+        t[nl] = float(best.mean())
+        gm.close()
+    us = (t[10] - t[2]) / 8 * 1e3
+    return {"workload": "config 1: one SmolLM2-135M-shaped layer, batch 1, positions 0-6",
+            "layer_step_us": round(us, 2), "steps_per_s": round(1e6 / us, 1)}
+
+
 def cpu_decode_baseline(max_steps=3):
     """The oracle's faithful decode loop (full.py:432-443 restated), timed
     on the first max_steps steps of config 3 on this host (1 thread)."""
@@ -351,6 +386,8 @@ def main():
     _lib.lib()
     if args.decode_only:
         res = {"decode": decode_leg(args.decode_reps)}
+        if not args.no_layer:
+            res["layer"] = layer_leg()
         if args.long:
             res["long_context"] = long_context_leg()
         if args.batch64:
@@ -425,9 +462,14 @@ def main():
     if not args.no_decode:
         print("[bench] config 3 decode", file=sys.stderr, flush=True)
         out["decode"] = decode_leg(args.decode_reps)
+        if not args.no_layer:
+            print("[bench] config 1 layer step", file=sys.stderr, flush=True)
+            out["layer"] = layer_leg()
         if args.long:
+            print("[bench] config 4 long context", file=sys.stderr, flush=True)
             out["long_context"] = long_context_leg()
         if args.batch64:
+            print("[bench] config 5 batch 64", file=sys.stderr, flush=True)
             out["batch64"] = batch_leg()
     if args.probe:
         out["stream_ceiling"] = stream_probe()
