@@ -307,8 +307,10 @@ __device__ __forceinline__ void load_krow(KRow &r, const int16_t *Km, const int8
   r.e4 = *reinterpret_cast<const int *>(Ke + (o >> 4));
 }
 
-template <int PPW>
-__global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
+// SHORT: max_ctx <= 64 * ATT_WAVES, one score per thread; fewer registers,
+// two workgroups per CU (many sequences at short context).
+template <int PPW, bool SHORT>
+__global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerArgs a) {
   constexpr int TB = (ATT_WAVES - 1) * PPW;   // positions per AV block (even)
   constexpr int ATT_DEPTH = PPW;               // V blocks in flight
   constexpr int NT = 64 * ATT_WAVES;
@@ -404,7 +406,12 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void k_attn(LayerArgs a) {
   // position per thread, two rows in flight.  Row pos is read from global
   // memory like the others (the writer may not have stored it yet) and its
   // score is recomputed from LDS afterwards by the same thread.
-  {
+  if constexpr (SHORT) {
+    // contexts of at most NT positions: one row per thread, the one in
+    // flight since the RoPE phase
+    if (tid < n) sc[tid] = ddot64_skx_bfp(q, ra.m, ra.e4) / a.inv_sqrt_hd_div;
+    if (tid == pos) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
+  } else {
     const int last = n - 1;
     for (int t = tid; t < n; t += 2 * NT) {
       const int t1 = t + NT, t2 = t + 2 * NT;
@@ -1058,7 +1065,10 @@ static void shape_for(int nT, int &nw, int &tpt) {
 }
 
 static int attn_ppw(int max_ctx) { return max_ctx <= 128 ? 2 : (max_ctx <= 512 ? 4 : 8); }
-static lk_fn attn_kernel(int ppw) { return ppw == 2 ? k_attn<2> : (ppw == 4 ? k_attn<4> : k_attn<8>); }
+static lk_fn attn_kernel(int ppw) {
+  // max_ctx <= 512 = 64 * ATT_WAVES for ppw 2 and 4: the one-score-per-thread form
+  return ppw == 2 ? k_attn<2, true> : (ppw == 4 ? k_attn<4, true> : k_attn<8, false>);
+}
 
 // Per device, before the first launch (outside any stream capture): allow
 // the dynamic LDS the attention and multi-sequence kernels take.
