@@ -253,6 +253,43 @@ int bfp_decode_time(const bfp_ctx *ctx, float *total_ms, float *gen_ms);
  * copies up to n values, returns the number of steps recorded. */
 int bfp_decode_step_times(const bfp_ctx *ctx, float *ms, int n);
 
+/* ------------------------------------------------------------ vocabulary */
+/* Token-id -> text for human-readable output.  The table is the "BFPV" v1
+ * file written by rtl/vc707/host/gen_bfp_vocab_bin.py:10-17,69-74 (magic,
+ * u32 version, u32 n_tokens, u32 blob_size, n_tokens x {u32 offset, u32
+ * length}, blob; little-endian), as read by the reference's native client
+ * (rtl/vc707/host/bfp_client.cpp:876-903, struct Vocab::load).  Host code:
+ * no device is needed. */
+typedef struct bfp_vocab bfp_vocab;
+/* Vocab::load (bfp_client.cpp:879-903): bad magic, a version other than 1 or
+ * a short file -> BFP_EINVAL; *out = NULL on error. */
+int bfp_vocab_open(const char *path, bfp_vocab **out);
+/* The same from a buffer of n bytes (copied). */
+int bfp_vocab_parse(const void *buf, size_t n, bfp_vocab **out);
+void bfp_vocab_close(bfp_vocab *v);
+/* n_tokens of the table (0 for NULL). */
+int bfp_vocab_size(const bfp_vocab *v);
+/* Vocab::bytes_for (bfp_client.cpp:906-911): a token's raw bytes (not
+ * NUL-terminated, owned by v); an id outside [0, n_tokens) or an entry
+ * reaching past the blob gives len 0. */
+int bfp_vocab_token(const bfp_vocab *v, int id, const char **bytes, size_t *len);
+/* decode_tokens (bfp_client.cpp:1020-1027): the ids' bytes concatenated,
+ * read as lenient UTF-8 and repaired for Windows-1252 mojibake
+ * (fix_mojibake, :973-1018).  Writes at most cap-1 bytes and a NUL to out
+ * (out may be NULL with cap 0) and returns the full text length, or a
+ * negative error code. */
+long long bfp_vocab_decode(const bfp_vocab *v, const int32_t *ids, int n, char *out, size_t cap);
+
+/* Narrow embedding rows (m, e) of n token ids from the reference's
+ * EMBED_LU table (gen_smollm_blockfp_ddr.py:203-216: mantissa row d int16
+ * per token, exponent rows of e_row_bytes >= D/16 int8), as the FPGA's
+ * embedding lookup reads them, gathered on the device: out_m (n, D) int16,
+ * out_e (n, D/16) int8.  All pointers are device pointers; an id outside
+ * [0, vocab) yields the zero tile (m 0, e -127), as tile_quantize maps a
+ * zero vector. */
+int bfp_embed_gather_d(const void *lu_m, const void *lu_e, int vocab, int D, int e_row_bytes,
+                       const int32_t *ids, int n, int16_t *out_m, int8_t *out_e, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,3 +93,39 @@ def test_decode_with_release_gammas(gpu, tmp_path):
     gm.load_ddr_image(path)
     _decode_pair(om, d, gm, [11, 400, 2, 99], 6)
     gm.close()
+
+
+def test_embed_lookup_from_image(gpu, tmp_path):
+    """Narrow rows gathered from a DDR3 image's EMBED_LU table equal the
+    oracle's tile_quantize of the embedding rows; ids outside the
+    vocabulary give the zero tile."""
+    from bfp import Dims, image, synth
+    d = Dims(**TINY)
+    om = sim.build_model(synth.make_model(d, seed=23))
+    path = tmp_path / "e_DDR3.bin"
+    path.write_bytes(oimg.ddr_image_bytes(om))
+    img = image.WeightImage.from_ddr(path, d)
+    ids = [0, 5, d.VOCAB - 1, 3, 3, -1, d.VOCAB, 10 ** 6]
+    m, e = img.embed_lookup(ids)
+    assert m.shape == (len(ids), d.D) and e.shape == (len(ids), d.D // 16)
+    for r, t in enumerate(ids):
+        if 0 <= t < d.VOCAB:
+            wm, we = sim.tile_quantize(om.embed[t])
+            assert (m[r] == wm.reshape(-1)).all() and (e[r] == we).all(), t
+        else:
+            assert (m[r] == 0).all() and (e[r] == -127).all(), t
+
+
+def test_embed_lookup_full_table(gpu):
+    """SmolLM2 size (49152 x 576, exponent rows of 64 bytes): 4096 random
+    ids and the table's first and last rows against numpy indexing."""
+    from bfp.api import embed_lookup
+    rng = np.random.default_rng(5)
+    V, D = 49152, 576
+    lu_m = rng.integers(-32768, 32768, size=(V, D), dtype=np.int16)
+    lu_e = rng.integers(-128, 128, size=(V, 64), dtype=np.int8)
+    ids = np.concatenate([[0, V - 1], rng.integers(0, V, 4096)]).astype(np.int32)
+    m, e = embed_lookup(lu_m, lu_e, ids)
+    assert (m == lu_m[ids]).all() and (e == lu_e[ids, :D // 16]).all()
+    m0, e0 = embed_lookup(lu_m, lu_e, [])
+    assert m0.shape == (0, D) and e0.shape == (0, D // 16)

@@ -78,6 +78,13 @@ SIGNATURES = {
     "bfp_decode": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, i32]),
     "bfp_decode_time": (i32, [vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     "bfp_decode_step_times": (i32, [vp, vp, i32]),
+    "bfp_vocab_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "bfp_vocab_parse": (i32, [vp, sz, C.POINTER(vp)]),
+    "bfp_vocab_close": (None, [vp]),
+    "bfp_vocab_size": (i32, [vp]),
+    "bfp_vocab_token": (i32, [vp, i32, C.POINTER(C.c_char_p), C.POINTER(sz)]),
+    "bfp_vocab_decode": (i64, [vp, vp, i32, vp, sz]),
+    "bfp_embed_gather_d": (i32, [vp, vp, i32, i32, i32, vp, i32, vp, vp, vp]),
 }
 
 _LIB = None

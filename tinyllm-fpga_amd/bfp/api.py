@@ -128,3 +128,30 @@ def matvec_hw_golden(x_m, x_e, W_m, W_e):
     """full.py:217-233: float64 output (the decoded BFP result)."""
     ym, ye = matvec_bfp(x_m, x_e, W_m, W_e)
     return tile_decode(ym, ye)
+
+
+def embed_lookup(lu_m, lu_e, ids, vocab=None):
+    """The FPGA's embedding lookup: narrow BFP rows of token `ids` from an
+    EMBED_LU table (gen_smollm_blockfp_ddr.py:203-216), gathered on the
+    device.  lu_m (V, D) int16, lu_e (V, R) int8 with R >= D/16 (the image
+    pads exponent rows to 64 bytes); `vocab` (default V) bounds the valid
+    ids, and an id outside [0, vocab) gives the zero tile (m 0, e -127).
+    Returns (m (n, D) int16, e (n, D/16) int8)."""
+    def host(a, t):   # contiguous and writable (torch.from_numpy wants both)
+        a = np.ascontiguousarray(np.asarray(a, dtype=t))
+        return a if a.flags.writeable else a.copy()
+    lu_m, lu_e, ids = host(lu_m, np.int16), host(lu_e, np.int8), host(ids, np.int32).reshape(-1)
+    if lu_m.ndim != 2 or lu_e.ndim != 2 or lu_e.shape[0] != lu_m.shape[0]:
+        raise ValueError(f"bad table shapes {lu_m.shape} / {lu_e.shape}")
+    V, D = lu_m.shape
+    vocab = V if vocab is None else int(vocab)
+    if not 0 < vocab <= V or D % TILE or lu_e.shape[1] < D // TILE:
+        raise ValueError(f"bad table: vocab {vocab}, shapes {lu_m.shape} / {lu_e.shape}")
+    n = ids.size
+    om, oe = _dev.empty(max(n, 1) * D, "int16"), _dev.empty(max(n, 1) * (D // TILE), "int8")
+    if n:
+        dm, de, di = _dev.to_dev(lu_m), _dev.to_dev(lu_e), _dev.to_dev(ids)
+        call("bfp_embed_gather_d", _dev.ptr(dm), _dev.ptr(de), vocab, D, lu_e.shape[1],
+             _dev.ptr(di), n, _dev.ptr(om), _dev.ptr(oe), _dev.stream())
+    return (_dev.to_host(om)[:n * D].reshape(n, D),
+            _dev.to_host(oe)[:n * (D // TILE)].reshape(n, D // TILE))

@@ -190,6 +190,15 @@ class WeightImage:
         e = self.regions["EMBED_LU_e"].view(np.int8).reshape(-1, EMBED_LU_E_ROW)[:d.VOCAB, :d.D // 16]
         return np.ascontiguousarray(m), np.ascontiguousarray(e)
 
+    def embed_lookup(self, ids) -> tuple[np.ndarray, np.ndarray]:
+        """Rows (m (n, D), e (n, D/16)) of token ids from the narrow table,
+        gathered on the device as the FPGA's embedding lookup reads them."""
+        from .api import embed_lookup
+        d = self.dims
+        lu_m = self.regions["EMBED_LU_m"].view(np.int16).reshape(-1, d.D)
+        lu_e = self.regions["EMBED_LU_e"].view(np.int8).reshape(-1, EMBED_LU_E_ROW)
+        return embed_lookup(lu_m, lu_e, ids, vocab=d.VOCAB)
+
     def embed_f32(self) -> np.ndarray:
         """The embedding's BFP values, m * 2^(e-15), exact in float32."""
         m, e = self.embed_rows()

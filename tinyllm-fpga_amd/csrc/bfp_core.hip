@@ -326,6 +326,24 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *__restrict
   if (threadIdx.x == 0) out[blockIdx.x] = acc;
 }
 
+// Narrow embedding rows of n token ids, one workgroup per id: the mantissa
+// row as 16-byte words, the exponent bytes from a row of e_row bytes.
+__global__ __launch_bounds__(128) void embed_gather_kernel(const uint4 *__restrict__ lu_m,
+                                                           const int8_t *__restrict__ lu_e,
+                                                           int vocab, int D, int e_row,
+                                                           const int32_t *__restrict__ ids,
+                                                           uint4 *__restrict__ out_m,
+                                                           int8_t *__restrict__ out_e) {
+  const int r = blockIdx.x;
+  const int id = ids[r];
+  const bool ok = id >= 0 && id < vocab;
+  const int w = D / 8;  // 16-byte words per mantissa row
+  for (int i = threadIdx.x; i < w; i += blockDim.x)
+    out_m[(long long)r * w + i] = ok ? lu_m[(long long)id * w + i] : make_uint4(0, 0, 0, 0);
+  for (int t = threadIdx.x; t < D / 16; t += blockDim.x)
+    out_e[(long long)r * (D / 16) + t] = ok ? lu_e[(long long)id * e_row + t] : (int8_t)-127;
+}
+
 typedef void (*matvec_stream_fn)(const uint4 *, const int8_t *, long long, long long, int, int,
                                  int, const int16_t *, const int8_t *, long long, int16_t *,
                                  int8_t *, long long, long long, long long);
@@ -619,6 +637,22 @@ int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, void 
                      reinterpret_cast<const uint4 *>(p), n16, per,
                      reinterpret_cast<unsigned *>(out));
   return launch_status("probe_read");
+}
+
+int bfp_embed_gather_d(const void *lu_m, const void *lu_e, int vocab, int D, int e_row_bytes,
+                       const int32_t *ids, int n, int16_t *out_m, int8_t *out_e, void *stream) {
+  if (vocab <= 0 || D <= 0 || D % 16 || e_row_bytes < D / 16 || n < 0)
+    return set_err(BFP_EINVAL, "embed_gather: bad arguments (vocab=%d D=%d e_row=%d n=%d)", vocab,
+                   D, e_row_bytes, n);
+  if (n == 0) return BFP_OK;
+  if (!lu_m || !lu_e || !ids || !out_m || !out_e)
+    return set_err(BFP_EINVAL, "embed_gather: null pointer");
+  if ((reinterpret_cast<uintptr_t>(lu_m) | reinterpret_cast<uintptr_t>(out_m)) & 15)
+    return set_err(BFP_EINVAL, "embed_gather: mantissa tables must be 16-byte aligned");
+  hipLaunchKernelGGL(embed_gather_kernel, dim3(n), dim3(128), 0, (hipStream_t)stream,
+                     reinterpret_cast<const uint4 *>(lu_m), reinterpret_cast<const int8_t *>(lu_e),
+                     vocab, D, e_row_bytes, ids, reinterpret_cast<uint4 *>(out_m), out_e);
+  return launch_status("embed_gather");
 }
 
 int bfp_matvec_h(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in,
