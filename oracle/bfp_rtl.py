@@ -70,15 +70,31 @@ def rtl_matvec(x_m, x_e, W_m, W_e):
     return out_m, out_e
 
 
+def _wrap8(v):
+    """An integer reduced to the 8-bit two's-complement range."""
+    return ((int(v) + 128) & 0xFF) - 128
+
+
+def shr8(m: int, e_to: int, e_from: int) -> int:
+    """requant_mant (smollm_layer_bfp.sv:1387-1396): the shift e_to - e_from
+    is held in `logic signed [7:0]`, so it wraps; >= 16 gives 0, a negative
+    (wrapped) shift leaves m unchanged.  The AV pre-shift of V
+    (:2149-2166) has the same form."""
+    sh = _wrap8(e_to - e_from)
+    if sh >= 16:
+        return 0
+    return int(m) >> sh if sh >= 0 else int(m)
+
+
 def rtl_requant(m, e):
     """Per-lane exponents of a 16-lane chunk -> one tile exponent
     (smollm_layer_bfp.sv:1387-1396 requant_mant, :1672-1693 emax):
-    emax = max(e); m >>> (emax - e), 0 when the shift is >= 16."""
+    emax = max(e); each m through shr8(m, emax, e)."""
     m = np.asarray(m, np.int64).reshape(-1, TILE)
     e = np.asarray(e, np.int64).reshape(-1, TILE)
     emax = e.max(axis=1)
-    sh = emax[:, None] - e
-    out = np.where(sh >= 16, 0, m >> np.clip(sh, 0, 15))
+    out = np.array([[shr8(m[c, k], emax[c], e[c, k]) for k in range(TILE)]
+                    for c in range(m.shape[0])], np.int64)
     return out.astype(np.int16).reshape(-1), emax.astype(np.int8)
 
 
@@ -352,3 +368,127 @@ def rtl_argmax(m, e):
         if bfp_gt(lm, le, best_m, best_e):
             best_m, best_e, best_i = lm, le, c * TILE + li
     return best_i
+
+
+# ------------------------------------------------------- composed RTL layer
+class RtlTables:
+    """The engines' lookup tables: EXP_LUT, SILU_LUT, FREQ_TURNS_Q31."""
+
+    def __init__(self, head_dim=64, base=10000.0):
+        self.exp = exp_lut()
+        self.silu = silu_lut()
+        self.freq = rope_freq_turns(base, head_dim)
+
+
+def rtl_kv_cache(max_ctx, kv):
+    """One layer's RTL KV cache: per position the post-RoPE K and the V as
+    BFP (m per element, e per 16-element tile)."""
+    return {"k_m": np.zeros((max_ctx, kv), np.int16), "k_e": np.zeros((max_ctx, kv // TILE), np.int8),
+            "v_m": np.zeros((max_ctx, kv), np.int16), "v_e": np.zeros((max_ctx, kv // TILE), np.int8)}
+
+
+def _mv_tile(x_m, x_e, W):
+    """A matvec on the engine, then the chunk re-tile (S_xMV_DRAIN/REQ):
+    per-lane (m, e) -> requant per 16 output rows."""
+    Wm, We = W
+    nt = We.shape[1]
+    m, e = rtl_matvec(np.asarray(x_m).reshape(nt, TILE), np.asarray(x_e).reshape(-1), Wm, We)
+    return rtl_requant(m, e)
+
+
+def rtl_fwd_layer(h_m, h_e, lw, pos, kv_pos, kv, tabs, dims, stages=None):
+    """One decoder layer as smollm_layer_bfp.sv:1603-2600 wires its engines.
+
+    h (D BFP) -> out (D BFP); kv (rtl_kv_cache) gets slot kv_pos.  lw holds
+    the layer's (m, e) matrices and float gammas (BFP-exact; the ROM holds
+    their tile_quantize).  Order of the FSM:
+      NORM1 -> Q/K/V matvec + re-tile (:1616-1829) -> RoPE per head and
+      re-tile (:1831-1954) -> KV write (:1956-1974) -> per head: QK on the
+      engine's lane 0 for t = 0..kv_pos (:1976-2036), pre-align to the
+      shared max exponent and softmax with exponent - 3 (:2038-2072), AV per
+      16-dim chunk with V pre-shifted to its max exponent over t <= kv_pos
+      and one 16-input tile of probabilities (t <= 15 only, :2074-2226) ->
+      O matvec (:2228-2294) -> residual 1 (:2296-2327) -> NORM2
+      (:2329-2349) -> G, U matvecs -> SwiGLU (:2470-2494) -> D matvec ->
+      residual 2 (:2496-2580).
+    ``stages`` (optional dict) receives each stage's (m, e) under the
+    names N1 Q K V ATTN O H1 N2 G U MLP D HOUT (Q, K after RoPE)."""
+    from . import bfp_sim as sim
+    D, H_Q, H_KV, HD = dims.D, dims.H_Q, dims.H_KV, dims.HD
+    KV = H_KV * HD
+    st = stages if stages is not None else {}
+
+    def gamma(g):
+        m, e = sim.tile_quantize(np.asarray(g, np.float64))
+        return m.reshape(-1), e
+
+    n1 = rtl_rmsnorm(h_m, h_e, *gamma(lw["g1"]))
+    st["N1"] = n1
+    q = _mv_tile(*n1, lw["Wq"])
+    k = _mv_tile(*n1, lw["Wk"])
+    v = _mv_tile(*n1, lw["Wv"])
+    st["V"] = v
+
+    def rope_all(x, n_heads):
+        xm, xe = x
+        om, oe = np.zeros(n_heads * HD, np.int16), np.zeros(n_heads * HD // TILE, np.int8)
+        for hh in range(n_heads):
+            rm, re = rtl_rope(xm[hh * HD:(hh + 1) * HD], xe[hh * HD // TILE:(hh + 1) * HD // TILE],
+                              pos, tabs.freq)
+            tm, te = rtl_requant(rm, re)
+            om[hh * HD:(hh + 1) * HD], oe[hh * HD // TILE:(hh + 1) * HD // TILE] = tm, te
+        return om, oe
+
+    q = rope_all(q, H_Q)
+    k = rope_all(k, H_KV)
+    st["Q"], st["K"] = q, k
+    kv["k_m"][kv_pos], kv["k_e"][kv_pos] = k
+    kv["v_m"][kv_pos], kv["v_e"][kv_pos] = v
+
+    att_m, att_e = np.zeros(D, np.int16), np.zeros(D // TILE, np.int8)
+    ntq = HD // TILE
+    n = kv_pos + 1
+    for hh in range(H_Q):
+        g = (hh * H_KV) // H_Q
+        qm = q[0][hh * HD:(hh + 1) * HD].reshape(ntq, TILE)
+        qe = q[1][hh * ntq:(hh + 1) * ntq]
+        sm, se = np.zeros(n, np.int64), np.zeros(n, np.int64)
+        for t in range(n):
+            km = kv["k_m"][t, g * HD:(g + 1) * HD].reshape(1, ntq, TILE)
+            ke = kv["k_e"][t, g * ntq:(g + 1) * ntq].reshape(1, ntq)
+            m1, e1 = rtl_matvec(qm, qe, km, ke)
+            sm[t], se[t] = int(m1[0]), int(e1[0])
+        es = max(-128, int(se.max()))
+        xm = [0 if es - int(se[t]) >= 16 else int(sm[t]) >> (es - int(se[t])) for t in range(n)]
+        pm, pe = rtl_softmax(xm, _wrap8(es - 3), n, tabs.exp)
+        x_av = np.zeros((1, TILE), np.int64)
+        x_av[0, :min(n, TILE)] = pm[:min(n, TILE)]
+        for c in range(ntq):
+            tile = g * ntq + c
+            emax = int(kv["v_e"][:n, tile].max())
+            W = np.zeros((TILE, 1, TILE), np.int64)
+            for t in range(min(n, TILE)):
+                for lane in range(TILE):
+                    W[lane, 0, t] = shr8(kv["v_m"][t, tile * TILE + lane], emax,
+                                         kv["v_e"][t, tile])
+            m16, e16 = rtl_matvec(x_av, np.array([int(pe)]), W, np.full((TILE, 1), emax))
+            tm, te = rtl_requant(m16, e16)
+            att_m[(hh * ntq + c) * TILE:(hh * ntq + c + 1) * TILE] = tm
+            att_e[hh * ntq + c] = te[0]
+    st["ATTN"] = (att_m, att_e)
+    o = _mv_tile(att_m, att_e, lw["Wo"])
+    st["O"] = o
+    h1 = rtl_residual(h_m, h_e, *o)
+    st["H1"] = h1
+    n2 = rtl_rmsnorm(*h1, *gamma(lw["g2"]))
+    st["N2"] = n2
+    gg = _mv_tile(*n2, lw["Wg"])
+    uu = _mv_tile(*n2, lw["Wu"])
+    st["G"], st["U"] = gg, uu
+    mlp = rtl_swiglu(*gg, *uu, tabs.silu)
+    st["MLP"] = mlp
+    dd = _mv_tile(*mlp, lw["Wd"])
+    st["D"] = dd
+    out = rtl_residual(*h1, *dd)
+    st["HOUT"] = out
+    return out

@@ -141,6 +141,25 @@ class BfpModel:
              C.byref(sd) if sd is not None else None)
         return out_m, out_e, stages
 
+    def rtl_layer_step(self, layer, pos, h_m, h_e, kv_pos=None, dump=False):
+        """The FPGA's decoder layer (smollm_layer_bfp.sv, the RTL engines in
+        its FSM order) on one BFP input (D,) / (D/16,) at RoPE position pos
+        and KV slot kv_pos (default pos); returns (out_m, out_e, stages)."""
+        d = self.dims
+        h_m = _c16(h_m).reshape(d.D)
+        h_e = _c8(h_e).reshape(d.D // 16)
+        out_m, out_e = np.empty_like(h_m), np.empty_like(h_e)
+        stages, sd = {}, None
+        if dump:
+            sd = StageDumpC()
+            for i, name in enumerate(STAGES):
+                n = self._stage_len(name)
+                stages[name] = (np.empty(n, np.int16), np.empty(n // 16, np.int8))
+                sd.m[i], sd.e[i] = _p(stages[name][0]), _p(stages[name][1])
+        call("bfp_rtl_layer_step", self._h, layer, pos, pos if kv_pos is None else kv_pos,
+             _p(h_m), _p(h_e), _p(out_m), _p(out_e), C.byref(sd) if sd is not None else None)
+        return out_m, out_e, stages
+
     def fwd_layer(self, h, layer, pos, kv_pos=None):
         """The reference's fwd_layer(h, lw, pos, kv, kv_pos) (full.py:261-293)
         with the layer's weights and KV cache resident in the context:

@@ -74,4 +74,7 @@ int head_workgroups(int vocab, int D, int rows_single, int batch);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);
 int launch_ctl(const CtlArgs &a, hipStream_t s);
+struct RtlArgs;
+// The composed RTL-exact layer step (bfp_rtl.hip).
+int launch_rtl_layer(const RtlArgs &a, hipStream_t s);
 }  // namespace bfp

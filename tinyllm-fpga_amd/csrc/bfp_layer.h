@@ -50,6 +50,17 @@ struct LayerArgs {
   int hist_steps, layer, NL;
 };
 
+// The composed RTL-exact layer (smollm_layer_bfp.sv) on one sequence: the
+// layer's buffers (L.batch == 1; xn holds NORM1 and NORM2 outputs, qkv the
+// Q/K/V tiles, att the attention output) plus the engines' tables.
+struct RtlArgs {
+  LayerArgs L;
+  const uint16_t *exp_lut;    // EXP_LUT[1024]
+  const int16_t *silu_lut;    // SILU_LUT[65536], indexed by code & 0xFFFF
+  const unsigned *freq;       // FREQ_TURNS_Q31[HD/2]
+  int pos, kv_pos;            // RoPE position, KV slot (attention over 0..kv_pos)
+};
+
 struct HeadArgs {
   int D, VOCAB, batch, rows_per_wg, n_wg;
   const int16_t *h_m; const int8_t *h_e;   // final hidden (BFP)
