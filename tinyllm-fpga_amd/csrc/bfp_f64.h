@@ -75,7 +75,7 @@ constexpr int PW_MAX_LEAVES = 64;  // n <= 8192 has at most 64 leaves of >= 128 
 // Sum of a[0..n) (a in LDS) in numpy order, plus numpy's initial 0.0.
 // Called by all threads of a workgroup (uses __syncthreads); leafbuf holds
 // PW_MAX_LEAVES doubles of LDS.  Returns the sum in every thread.
-__device__ inline double pairwise_sum_block(const double *a, int n, double *leafbuf) {
+__device__ __forceinline__ double pairwise_sum_block(const double *a, int n, double *leafbuf) {
   int k = 0, flo = 0, fn = 0;
   const int t = threadIdx.x;
   if (t < PW_MAX_LEAVES) {

@@ -18,6 +18,7 @@
 #include "bfp_internal.h"
 #include "bfp_layer.h"
 #include "bfp_mv.h"
+#include "bfp_mx.h"
 
 namespace bfp {
 
@@ -37,7 +38,7 @@ __device__ __forceinline__ int cur_pos(const LayerArgs &a) {
 // dbuf: 3*D doubles of LDS (x*x, x, g), leaf: PW_MAX_LEAVES doubles.  Every
 // thread issues all of its global loads (h, its exponents, g) before using
 // any, so the prologue costs one memory round trip.  All threads call.
-__device__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
+__device__ __forceinline__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
                              const double *__restrict__ g, int D, int *xs, int *xes, double *dbuf,
                              double *leaf, int16_t *dm, int8_t *de) {
   const int bs = blockDim.x, tid = threadIdx.x;
@@ -240,7 +241,6 @@ __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
   __shared__ int redM[NW * 16];
   __shared__ long long redA[NW * 16];
   const int c = blockIdx.x, b = blockIdx.y;
-  const int nq = a.D + 2 * a.KV;
 
   ChunkRegs<TPT> R;
   load_chunk<NW, TPT>(R, a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT);
@@ -715,6 +715,91 @@ __global__ __launch_bounds__(64 * NW) void k_d_res_m(LayerArgs a) {
                          a.h1_m[b * a.D + c * 16 + r_], a.h1_e[b * (a.D / 16) + c]))
 }
 
+// ------------------------------------------ matrix-core multi-sequence path
+// The four matvecs of a layer for 16 sequences per workgroup on the int8
+// MFMA (bfp_mx.h); the epilogues are the multi-sequence path's.  blockIdx.x
+// is a block of NC chunks, blockIdx.y a group of 16 sequences.  Each
+// 16-lane group runs the epilogue of one (chunk, sequence) pair per pass.
+#define BFP_MX_EPI(NPAIR, ...)                                                    \
+  {                                                                              \
+    const int r_ = threadIdx.x & 15, grp_ = threadIdx.x >> 4;                     \
+    const int ngrp_ = blockDim.x >> 4;                                            \
+    for (int p0_ = 0; p0_ < (NPAIR); p0_ += ngrp_) {                              \
+      if (p0_ + 4 * (threadIdx.x >> 6) >= (NPAIR)) break; /* wave has no pair */ \
+      const int p_ = p0_ + grp_;                                                  \
+      const int pc_ = p_ < (NPAIR) ? p_ : 0;                                      \
+      const int cc_ = pc_ / MX_SEQ, j_ = pc_ % MX_SEQ;                            \
+      const bool wr_ = p_ < (NPAIR) && j_ < ns;                                   \
+      const int b = b0 + (wr_ ? j_ : 0);                                          \
+      __VA_ARGS__;                                                                \
+    }                                                                             \
+  }
+
+// Q|K|V: two chunks per block.
+__global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_qkv_mx(LayerArgs a) {
+  __shared__ long long Ao[2 * 16 * MX_SEQ];
+  __shared__ int Mo[2 * 16 * MX_SEQ];
+  extern __shared__ int8_t mx_ex[];
+  const int nT = a.D / 16, c0 = 2 * blockIdx.x, b0 = blockIdx.y * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  mx_block<2>(a.w_qkv_m + (long long)c0 * nT * 32, a.w_qkv_e + (long long)c0 * nT * 16, nT,
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(2 * MX_SEQ, {
+    const int q_ = (cc_ * 16 + r_) * MX_SEQ + j_;
+    epi_qkv(a, b, c0 + cc_, mx_A(Ao, q_), Mo[q_], wr_);
+  })
+}
+
+// O and residual 1: one chunk per block.
+__global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_mx(LayerArgs a) {
+  __shared__ long long Ao[16 * MX_SEQ];
+  __shared__ int Mo[16 * MX_SEQ];
+  extern __shared__ int8_t mx_ex[];
+  const int nT = a.D / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  mx_block<1>(a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT,
+              a.att_m + (long long)b0 * a.D, a.att_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(MX_SEQ, {
+    const int q_ = r_ * MX_SEQ + j_;
+    (void)cc_;
+    epi_ores(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h_m[b * a.D + c * 16 + r_],
+             a.h_e[b * (a.D / 16) + c]);
+  })
+}
+
+// G and U: the G chunk (2x) and U chunk (2x+1) of FFN chunk x per block.
+__global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_gu_mx(LayerArgs a) {
+  __shared__ long long Ao[2 * 16 * MX_SEQ];
+  __shared__ int Mo[2 * 16 * MX_SEQ];
+  extern __shared__ int8_t mx_ex[];
+  const int nT = a.D / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  mx_block<2>(a.w_gu_m + (long long)(2 * c) * nT * 32, a.w_gu_e + (long long)(2 * c) * nT * 16, nT,
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(MX_SEQ, {
+    const int qg_ = r_ * MX_SEQ + j_, qu_ = (16 + r_) * MX_SEQ + j_;
+    (void)cc_;
+    epi_gu(a, b, c, mx_A(Ao, qg_), Mo[qg_], mx_A(Ao, qu_), Mo[qu_], wr_);
+  })
+}
+
+// D and residual 2: one chunk per block.
+__global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_d_res_mx(LayerArgs a) {
+  __shared__ long long Ao[16 * MX_SEQ];
+  __shared__ int Mo[16 * MX_SEQ];
+  extern __shared__ int8_t mx_ex[];
+  const int nT = a.FFN / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  mx_block<1>(a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT,
+              a.mlp_m + (long long)b0 * a.FFN, a.mlp_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(MX_SEQ, {
+    const int q_ = r_ * MX_SEQ + j_;
+    (void)cc_;
+    epi_dres(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h1_m[b * a.D + c * 16 + r_],
+             a.h1_e[b * (a.D / 16) + c]);
+  })
+}
+
 // ------------------------------------------------------------------ head
 // One step of a (value, index) argmax over lanes: larger value wins, the
 // lower index on ties (a total order, so any combining order gives the
@@ -733,7 +818,7 @@ __device__ __forceinline__ void argmax_step(double &best, int &besti) {
 // 1e-5)) * w, float64, not re-quantised.  work: 3*D doubles of LDS, leaf:
 // PW_MAX_LEAVES; hn may alias work (LDS) or be global.  Loads are issued in
 // one batch per thread.  All threads call.
-__device__ void final_norm(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
+__device__ __forceinline__ void final_norm(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
                            const double *__restrict__ w, int D, double *work, double *leaf,
                            double *hn) {
   const int bs = blockDim.x, tid = threadIdx.x;
@@ -1034,8 +1119,13 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
 // --------------------------------------------------------------- launchers
 typedef void (*lk_fn)(LayerArgs);
 
-// Batches from this size on use the multi-sequence kernels.
+// Batches from this size on use the multi-sequence kernels, and from
+// MX_MIN_BATCH on their matrix-core form.
 constexpr int MULTI_MIN_BATCH = 4;
+static int MX_MIN_BATCH = [] {
+  const char *v = getenv("BFP_MX_MIN_BATCH");
+  return v ? atoi(v) : 32;
+}();
 
 // The (waves, tiles per lane) pairs default_waves() produces for
 // 4 <= in/16 <= 108, i.e. every supported D and FFN.
@@ -1098,7 +1188,37 @@ static int launch_attn(const LayerArgs &a, hipStream_t s) {
   return BFP_OK;
 }
 
+// Waves per workgroup of an MFMA matvec over nT tiles with n_blocks blocks:
+// at most one resident round on the chip (two waves per SIMD), at least two
+// tiles per wave.
+static int mx_waves(int nT, int n_blocks) {
+  int w = 2048 / n_blocks;
+  w = w < (nT + 1) / 2 ? w : (nT + 1) / 2;
+  w = w < MX_WAVES_MAX ? w : MX_WAVES_MAX;
+  return w < 1 ? 1 : w;
+}
+
+static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
+  const int nTD = a.D / 16, nTF = a.FFN / 16;
+  const size_t sh_norm = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
+  const int G = (a.batch + MX_SEQ - 1) / MX_SEQ;
+  const int bq = (a.D + 2 * a.KV) / 32, bo = a.D / 16, bg = a.FFN / 16;
+  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 1);
+  hipLaunchKernelGGL(k_qkv_mx, dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
+                     mx_lds_bytes(2, nTD), s, a);
+  BFP_TRY(launch_attn(a, s));
+  hipLaunchKernelGGL(k_o_res_mx, dim3(bo, G), dim3(64 * mx_waves(nTD, bo * G)),
+                     mx_lds_bytes(1, nTD), s, a);
+  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 2);
+  hipLaunchKernelGGL(k_gu_mx, dim3(bg, G), dim3(64 * mx_waves(nTD, bg * G)),
+                     mx_lds_bytes(2, nTD), s, a);
+  hipLaunchKernelGGL(k_d_res_mx, dim3(bo, G), dim3(64 * mx_waves(nTF, bo * G)),
+                     mx_lds_bytes(1, nTF), s, a);
+  return launch_status("layer");
+}
+
 static int launch_layer_multi(const LayerArgs &a, hipStream_t s) {
+  if (a.batch >= MX_MIN_BATCH) return launch_layer_mx(a, s);
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   int nw, tpt, nwf, tptf;
   shape_for(nTD, nw, tpt);

@@ -1,0 +1,217 @@
+// Exact BFP tile sums of many sequences on the matrix cores (int8 MFMA).
+//
+// Semantics are the engine's (rtl/vc707/host/gen_smollm_blockfp_full.py
+// :217-233): per row o, sequence s and input tile t the exact
+// S = sum_k W_m[o,t,k] x_m[s,t,k], E = W_e[o,t] + x_e[s,t], M = max_t E,
+// A = sum_t floor(S / 2^(M-E)) for M-E <= 47.
+//
+// Both int16 operands are split into a signed high byte and an offset low
+// byte: v = 256*vh + vl' + 128 with vh = v >> 8 and vl' = (v & 255) - 128,
+// both in [-128, 127].  Over one 16-element tile
+//   S = 65536*Phh + 256*(Phl + Plh + 128*sum Wh) + (Pll + 128*sum Wl')
+//       + 128*sum x
+// where Pab = sum_k Wa*xb.  Every product sum is one v_mfma_i32_16x16x32_i8
+// whose 32-deep k axis holds the tile twice (k-groups 0-1 and 2-3 of the
+// operand layout): Phh and Pll with the second copy of A zeroed, the cross
+// term as Wh.xl' over the first copy plus Wl'.xh over the second, and the
+// weight sums against a constant 64 operand over both copies (= 128 sum).
+// sum x (one value per sequence) comes from the vector unit.  |Phh| < 2^18
+// and the rest fits in 29 bits, so S is formed exactly in 64 bits.  One
+// more MFMA places E = W_e + x_e straight into the accumulator layout (A
+// holds [W_e, 1], B holds [1, x_e]), so every per-output quantity is in the
+// lane that owns the output: no lane exchange is needed.
+//
+// A block is NC adjacent 16-row chunks of the device layout by 16
+// sequences.  Lane l supplies row / sequence l % 16 and k-group l / 16
+// (the tile's 8-element half (l/16) & 1), and owns outputs
+// (row 4*(l/16) + v, sequence l % 16), v < 4, of every chunk.  The waves of
+// a workgroup split the input tiles; M is reduced with LDS max and A with
+// LDS 64-bit adds.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bfp_device.h"
+
+namespace bfp {
+
+typedef int mx_v4 __attribute__((ext_vector_type(4)));
+
+constexpr int MX_SEQ = 16;    // sequences per block
+constexpr int MX_WAVES_MAX = 8;
+
+// High bytes and offset low bytes of the 8 int16 in w (little-endian pairs).
+__device__ __forceinline__ void mx_split(const uint4 w, long &hi, long &lo) {
+  const unsigned h0 = __builtin_amdgcn_perm(w.y, w.x, 0x07050301u);
+  const unsigned h1 = __builtin_amdgcn_perm(w.w, w.z, 0x07050301u);
+  const unsigned l0 = __builtin_amdgcn_perm(w.y, w.x, 0x06040200u) ^ 0x80808080u;
+  const unsigned l1 = __builtin_amdgcn_perm(w.w, w.z, 0x06040200u) ^ 0x80808080u;
+  hi = (long)(((unsigned long)h1 << 32) | h0);
+  lo = (long)(((unsigned long)l1 << 32) | l0);
+}
+
+__device__ __forceinline__ int mx_sum8(const uint4 w) {
+  return (int)(short)(w.x & 0xffffu) + ((int)w.x >> 16) + (int)(short)(w.y & 0xffffu) +
+         ((int)w.y >> 16) + (int)(short)(w.z & 0xffffu) + ((int)w.z >> 16) +
+         (int)(short)(w.w & 0xffffu) + ((int)w.w >> 16);
+}
+
+__device__ __forceinline__ mx_v4 mx_mfma(long a, long b, mx_v4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// LDS bytes mx_block<NC> needs beyond its caller's Ao / Mo: the block's
+// weight and input exponents, tile-major.
+__host__ __device__ constexpr int mx_lds_bytes(int nc, int nT) { return (nc + 1) * 16 * nT; }
+
+// (A, M) of the (row, sequence) pairs of a block: the NC adjacent 16-row
+// chunks at pm / pe (device layout, nT tiles each; chunk c is rows
+// 16c..16c+15) against sequences s < ns at x_m + s*nT*16, x_e + s*nT.
+// Every thread of the workgroup calls it; on return (after a barrier)
+// Ao[row*16 + s] and Mo[row*16 + s] (LDS) hold the pair of (row, s).
+// ex: mx_lds_bytes(NC, nT) bytes of LDS.
+template <int NC>
+__device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int8_t *__restrict__ pe, int nT,
+                         const int16_t *__restrict__ xm, const int8_t *__restrict__ xe, int ns,
+                         long long *Ao, int *Mo, int8_t *ex) {
+  constexpr int G = 4;           // tiles whose loads are in flight together
+  constexpr int RW = NC * 16;    // rows of the block
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int i = lane & 15, kg = lane >> 4, h = kg & 1;
+  const bool first = kg < 2;     // first copy of the tile on the k axis
+  const int sc = i < ns ? i : ns - 1;
+  const uint4 *xr = reinterpret_cast<const uint4 *>(xm);
+  const int wo = h * 16 + i, xo = sc * nT * 2 + h;   // + t*32 (+ c*nT*32), + t*2
+  int8_t *wex = ex, *xex = ex + RW * nT;             // [t*RW + row], [t*16 + sequence]
+  // exponents of the whole block into LDS: the weights' as 4-row words, the
+  // inputs' as bytes, every load of a thread issued before its stores
+  {
+    const int nw4 = NC * nT * 4, nx = MX_SEQ * nT, bs = blockDim.x;
+    const int *pe4 = reinterpret_cast<const int *>(pe);
+    for (int q0 = threadIdx.x; q0 < nw4 + nx; q0 += 4 * bs) {
+      int v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int q = q0 + k * bs;
+        if (q < nw4) {
+          v[k] = pe4[q];
+        } else {
+          int qx = q - nw4;
+          qx = qx < nx ? qx : nx - 1;
+          const int t = qx >> 4, ss = qx & 15;
+          v[k] = xe[(ss < ns ? ss : ns - 1) * nT + t];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int q = q0 + k * bs;
+        if (q < nw4) {
+          // word q: chunk q / (4nT), tile (q / 4) % nT, rows 4*(q%4) .. +3
+          const int c = q / (4 * nT), t = (q >> 2) - c * nT;
+          *reinterpret_cast<int *>(wex + t * RW + c * 16 + 4 * (q & 3)) = v[k];
+        } else if (q < nw4 + nx) {
+          xex[q - nw4] = (int8_t)v[k];
+        }
+      }
+    }
+  }
+  for (int q = threadIdx.x; q < RW * MX_SEQ; q += blockDim.x) {
+    Ao[q] = 0;
+    Mo[q] = -(1 << 29);
+  }
+  __syncthreads();
+  const mx_v4 zero = {0, 0, 0, 0};
+  // E = W_e + x_e of chunk c, tile t in the accumulator layout (k-group 0)
+  auto tile_E = [&](int c, int t) {
+    const int we = wex[t * RW + c * 16 + i], xv = xex[t * 16 + i];
+    const long a = kg == 0 ? (long)((we & 0xff) | (1 << 8)) : 0;
+    const long b = kg == 0 ? (long)(1 | ((xv & 0xff) << 8)) : 0;
+    return mx_mfma(a, b, zero);
+  };
+  const int tpw = (nT + nw - 1) / nw;
+  const int t0 = w * tpw, t1 = t0 + tpw < nT ? t0 + tpw : nT;
+  // pass 1: M over all tiles, split across the waves, reduced in LDS
+  int M[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) M[c][v] = -(1 << 29);
+    for (int t = t0; t < t1; ++t) {
+      const mx_v4 E = tile_E(c, t);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) M[c][v] = E[v] > M[c][v] ? E[v] : M[c][v];
+    }
+    if (t0 < t1) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) atomicMax(&Mo[(c * 16 + 4 * kg + v) * MX_SEQ + i], M[c][v]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) M[c][v] = Mo[(c * 16 + 4 * kg + v) * MX_SEQ + i];
+  // pass 2: aligned tile sums
+  long long A[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) A[c][v] = 0;
+  const long k64 = 0x4040404040404040L;
+  for (int tb = t0; tb < t1; tb += G) {
+    uint4 xv[G], wv[G][NC];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int t = tb + k < t1 ? tb + k : t1 - 1;
+      xv[k] = xr[xo + t * 2];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) wv[k][c] = pm[wo + c * nT * 32 + t * 32];
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      if (tb + k >= t1) break;
+      long xh, xl;
+      mx_split(xv[k], xh, xl);
+      int sx = mx_sum8(xv[k]);
+      sx += peer<16>(sx);   // the tile's other half (k-group l/16 ^ 1)
+      const int cx = 128 * sx;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        long wh, wl;
+        mx_split(wv[k][c], wh, wl);
+        const mx_v4 hh = mx_mfma(first ? wh : 0, xh, zero);
+        mx_v4 ll = mx_mfma(first ? wl : 0, xl, zero);
+        mx_v4 cr = mx_mfma(first ? wh : wl, first ? xl : xh, zero);
+        cr = mx_mfma(wh, k64, cr);
+        ll = mx_mfma(wl, k64, ll);
+        const mx_v4 E = tile_E(c, tb + k);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int d = M[c][v] - E[v];
+          if (d <= ALIGN_MAX) {
+            const int lo = (cr[v] << 8) + ll[v] + cx;
+            const long long S = (long long)hh[v] * 65536 + lo;
+            A[c][v] += S >> d;
+          }
+        }
+      }
+    }
+  }
+  if (t0 < t1) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        atomicAdd(reinterpret_cast<unsigned long long *>(&Ao[(c * 16 + 4 * kg + v) * MX_SEQ + i]),
+                  (unsigned long long)A[c][v]);
+  }
+  __syncthreads();
+}
+
+// A read back for an epilogue, clipped as the engine clips.
+__device__ __forceinline__ long long mx_A(const long long *Ao, int q) {
+  const long long A = Ao[q];
+  return A < SAT_LO ? SAT_LO : (A > SAT_HI ? SAT_HI : A);
+}
+
+}  // namespace bfp
