@@ -71,14 +71,14 @@ def test_layer_batched_sequences(gpu):
     gm.close()
 
 
-@pytest.mark.parametrize("cfg,batch", [(MID, 5), (FULL, 6), (MID, 33), (FULL, 40)],
-                         ids=["mid-b5", "full-b6", "mfma-mid-b33", "mfma-full-b40"])
+@pytest.mark.parametrize("cfg,batch", [(MID, 5), (FULL, 6), (MID, 9), (MID, 33), (FULL, 40)],
+                         ids=["mid-b5", "full-b6", "mfma-mid-b9", "mfma-mid-b33", "mfma-full-b40"])
 def test_layer_multi_sequence_path(gpu, cfg, batch):
     """Batches of 4 or more run the multi-sequence kernels (separate norm,
-    weight chunks reused across a group of sequences), from 32 on with the
-    tile sums on the int8 matrix cores (33: a second block of one
-    sequence): every stage of every sequence still equals its own oracle
-    run."""
+    weight chunks reused across a group of sequences), from 8 on with the
+    tile sums on the int8 matrix cores in blocks of 16 sequences (9: one
+    partial block; 33: a last block of one sequence): every stage of every
+    sequence still equals its own oracle run."""
     d, om, gm = _setup(cfg, seed=7, max_batch=batch)
     rng = np.random.default_rng(9)
     kvs = [sim.new_kv(om.dims, d.MAX_CTX) for _ in range(batch)]

@@ -1120,11 +1120,12 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
 typedef void (*lk_fn)(LayerArgs);
 
 // Batches from this size on use the multi-sequence kernels, and from
-// MX_MIN_BATCH on their matrix-core form.
+// MX_MIN_BATCH on their matrix-core form (measured crossover: the MFMA form
+// is ahead from 8 sequences; env BFP_MX_MIN_BATCH overrides).
 constexpr int MULTI_MIN_BATCH = 4;
 static int MX_MIN_BATCH = [] {
   const char *v = getenv("BFP_MX_MIN_BATCH");
-  return v ? atoi(v) : 32;
+  return v ? atoi(v) : 8;
 }();
 
 // The (waves, tiles per lane) pairs default_waves() produces for

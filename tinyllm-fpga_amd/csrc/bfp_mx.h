@@ -15,7 +15,7 @@
 // operand layout): Phh and Pll with the second copy of A zeroed, the cross
 // term as Wh.xl' over the first copy plus Wl'.xh over the second, and the
 // weight sums against a constant 64 operand over both copies (= 128 sum).
-// sum x (one value per sequence) comes from the vector unit.  |Phh| < 2^18
+// sum x (one value per sequence) comes from the vector unit.  |Phh| <= 2^18
 // and the rest fits in 29 bits, so S is formed exactly in 64 bits.  One
 // more MFMA places E = W_e + x_e straight into the accumulator layout (A
 // holds [W_e, 1], B holds [1, x_e]), so every per-output quantity is in the
