@@ -283,16 +283,24 @@ __device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
 //     thread, in OpenBLAS's SkylakeX ddot order;
 //  3. softmax: exp(s - max) / pairwise_sum (numpy's order);
 //  4. attn = sum_t p[t] * V[t] in ascending t from 0.0 (numpy's
-//     `attn[h] += p[t] * V[t]` loop, full.py:280-281).  The products are
-//     independent and are formed by waves 1.. into an LDS double buffer of
-//     TB positions while wave 0 runs the (inherently sequential) add chain
-//     over the previous block, one dimension per lane.  V is prefetched into
-//     registers ATT_DEPTH blocks ahead.
+//     `attn[h] += p[t] * V[t]` loop, full.py:280-281).  V rows are staged
+//     through LDS in chunks of AVC rows by every thread (16-byte loads, the
+//     next chunk's loads in flight while the current one is used); wave 0
+//     forms each product and runs the (inherently sequential) add chain, one
+//     dimension per lane, straight from LDS.
 constexpr int ATT_WAVES = 8;
 
+// V rows per staged chunk of the AV phase (short contexts).
+constexpr int ATT_AVC = 128;
+
+// The AV phase at long context (PPW 8) instead has waves 1.. form the
+// products of blocks of TB = 7*PPW positions into an LDS double buffer
+// while wave 0 adds the previous block; V is prefetched PPW blocks ahead.
 size_t attn_lds_bytes(int max_ctx, int ppw) {
   const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
-  return (256 + sc_len) * 8 + (size_t)(ATT_WAVES - 1) * ppw * 64 * 8 * 2;
+  const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4)
+                             : (size_t)(ATT_WAVES - 1) * ppw * 64 * 8 * 2;
+  return (256 + sc_len) * 8 + av;
 }
 
 // One K row of the cache (64 mantissas, 4 tile exponents) in registers.
@@ -311,16 +319,22 @@ __device__ __forceinline__ void load_krow(KRow &r, const int16_t *Km, const int8
 // two workgroups per CU (many sequences at short context).
 template <int PPW, bool SHORT>
 __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerArgs a) {
-  constexpr int TB = (ATT_WAVES - 1) * PPW;   // positions per AV block (even)
-  constexpr int ATT_DEPTH = PPW;               // V blocks in flight
   constexpr int NT = 64 * ATT_WAVES;
+  constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
+  constexpr int VL = AVC * 8 / NT;             // 16-byte V loads per thread and chunk
+  constexpr int TB = (ATT_WAVES - 1) * PPW;    // positions per AV block (long)
+  constexpr int ATT_DEPTH = PPW;               // V blocks in flight (long)
   extern __shared__ double dsm[];
   double *q = dsm;                  // 64
   double *kc = dsm + 64;            // 64 (current position, post-rope)
   double *vc = dsm + 128;           // 64
   double *leaf = dsm + 192;         // PW_MAX_LEAVES (= 64)
   double *sc = dsm + 256;           // max_ctx, rounded up to even
-  double2 *buf = reinterpret_cast<double2 *>(sc + ((a.max_ctx + 1) & ~1));   // 2 x TB/2 x 64
+  // short: staged V, 2 x AVC x 64 mantissas and 2 x AVC x 4 exponents;
+  // long: product double buffer, 2 x TB/2 x 64 double2
+  int16_t *vsm = reinterpret_cast<int16_t *>(sc + ((a.max_ctx + 1) & ~1));
+  int8_t *vse = reinterpret_cast<int8_t *>(vsm + 2 * AVC * 64);
+  double2 *buf = reinterpret_cast<double2 *>(sc + ((a.max_ctx + 1) & ~1));
   __shared__ double red[ATT_WAVES];
   const int hq = blockIdx.x, b = blockIdx.y;
   const int grp = a.H_Q / a.H_KV, g = hq / grp;
@@ -339,7 +353,35 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   int8_t *Ve = a.v_e + (long long)b * a.max_ctx * (kv_tok / 16);
   const bool writer = (hq % grp) == 0;
 
-  // V prefetch ring of the AV phase (filled after the scores).  Producer
+  // AV staging: chunk c holds rows c*AVC .. c*AVC+AVC-1 (clamped to n-1, so
+  // no load sits in a branch); thread tid loads 16-byte part tid%8 of rows
+  // tid/8 + 64j and, for tid < AVC, the 4 exponent bytes of row tid.
+  uint4 vr[VL];
+  int ver = 0;
+  const int16_t *Vg = Vm + (long long)g * HD + 8 * (tid & 7);
+  const int8_t *Veg = Ve + (long long)g * (HD / 16);
+  const long long vstride = (long long)a.H_KV * HD;    // elements per position
+#define BFP_ATT_LOAD_V(c)                                                        \
+  {                                                                              \
+    _Pragma("unroll") for (int j = 0; j < VL; ++j) {                             \
+      int t_ = (c) * AVC + (tid >> 3) + j * (NT / 8);                            \
+      t_ = t_ < n ? t_ : n - 1;                                                  \
+      vr[j] = *reinterpret_cast<const uint4 *>(Vg + t_ * vstride);               \
+    }                                                                            \
+    int t_ = (c) * AVC + (tid < AVC ? tid : 0);                                  \
+    t_ = t_ < n ? t_ : n - 1;                                                    \
+    ver = *reinterpret_cast<const int *>(Veg + t_ * (vstride / 16));             \
+  }
+#define BFP_ATT_STORE_V(c)                                                       \
+  {                                                                              \
+    int16_t *dst_ = vsm + ((c) & 1) * AVC * 64;                                  \
+    _Pragma("unroll") for (int j = 0; j < VL; ++j)                               \
+        *reinterpret_cast<uint4 *>(dst_ + ((tid >> 3) + j * (NT / 8)) * 64 +     \
+                                   8 * (tid & 7)) = vr[j];                       \
+    if (tid < AVC) *reinterpret_cast<int *>(vse + ((c) & 1) * AVC * 4 + tid * 4) = ver; \
+  }
+
+  // Long contexts: V prefetch ring of the AV phase (filled after the scores).  Producer
   // wave pw (waves 1..) owns positions k*TB + pw*PPW + pp, pp < PPW, of
   // block k; lane (pp = l/8, c = l%8) holds dimensions 8c..8c+7 of its
   // position: one 16-byte mantissa load and one exponent byte per block.
@@ -348,8 +390,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   // copy it does not use), so the compiler can count ATT_DEPTH blocks of
   // loads in flight instead of draining them.
   const int pw = w >= 1 ? w - 1 : 0, pp = l >> 3, pc = l & 7;
-  uint4 rm[ATT_DEPTH];
-  int re[ATT_DEPTH];
+  uint4 rm[SHORT ? 1 : ATT_DEPTH];
+  int re[SHORT ? 1 : ATT_DEPTH];
   auto load_blk = [&](int k, uint4 &m, int &e) {
     int t = k * TB + pw * PPW + (pp < PPW ? pp : 0);
     t = t < n ? t : n - 1;
@@ -402,6 +444,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   }
   __syncthreads();
 
+  if constexpr (SHORT) BFP_ATT_LOAD_V(0)   // in flight during the scores
   // scores[t] = float(np.dot(q, K[t])) / sqrt(HD)   (full.py:277-278), one
   // position per thread, two rows in flight.  Row pos is read from global
   // memory like the others (the writer may not have stored it yet) and its
@@ -423,8 +466,12 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     }
     if (tid == pos % NT) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
   }
+  if constexpr (SHORT) {
+    BFP_ATT_STORE_V(0)
+  } else {
 #pragma unroll
-  for (int d = 0; d < ATT_DEPTH; ++d) load_blk(d, rm[d], re[d]);   // overlaps the softmax
+    for (int d = 0; d < ATT_DEPTH; ++d) load_blk(d, rm[d], re[d]);   // overlaps the softmax
+  }
   __syncthreads();
   // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
   double mx = -INFINITY;
@@ -446,52 +493,91 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
   __syncthreads();
 
-  // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281).
-  // Iteration k: waves 1.. write the products of block k into buf[k & 1]
-  // (element (tt, dim) at double tt*64 + dim) and refill their ring slot
-  // with block k + ATT_DEPTH; wave 0 adds block k-1 from buf[(k-1) & 1],
-  // one dimension per lane.
-  const int nb = (n + TB - 1) / TB;
   double acc = 0.0;
-  for (int k0 = 0; k0 <= nb; k0 += ATT_DEPTH) {
+  if constexpr (SHORT) {
+    // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281):
+    // every product rounded, then added, in t order.  Chunk c+1 is loaded
+    // while wave 0 adds chunk c.  Row pos is this launch's V (vc): its writer
+    // workgroup may not have stored it yet.
+    const int nch = (n + AVC - 1) / AVC;
+    for (int c = 0; c < nch; ++c) {
+      BFP_ATT_LOAD_V(c + 1 < nch ? c + 1 : c)
+      if (w == 0) {
+        // 16 positions at a time: their LDS reads and products are independent
+        // and issued together; only the adds form the chain
+        // pos = n - 1 is the last position: it is added after the loop
+        const int t0 = c * AVC, t1 = min(pos, t0 + AVC);
+        const int16_t *vm = vsm + (c & 1) * AVC * 64 + l;
+        const int8_t *ve = vse + (c & 1) * AVC * 4 + (l >> 4);
+        int t = t0;
+        for (; t + 16 <= t1; t += 16) {
+          double pv[16];
 #pragma unroll
-    for (int d = 0; d < ATT_DEPTH; ++d) {
-      const int k = k0 + d;               // iterations past nb do unused work
-      if (w >= 1) {
-        const int tt = pw * PPW + pp;
-        const int t = k * TB + tt;
-        const int tc = t < n ? t : n - 1;
-        const double pt = sc[tc];
-        const double s = ldexp(1.0, re[d] - 15);
-        const unsigned wv[4] = {rm[d].x, rm[d].y, rm[d].z, rm[d].w};
-        double pr[8];
+          for (int i = 0; i < 16; ++i) {
+            const int r = t + i - t0;
+            pv[i] = sc[t + i] * ldexp((double)vm[r * 64], (int)ve[r * 4] - 15);
+          }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int mi = (int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
-          const double vcur = vc[8 * pc + i];
-          const double v = (t == pos) ? vcur : (double)mi * s;
-          pr[i] = t < n ? pt * v : 0.0;
+          for (int i = 0; i < 16; ++i) acc = acc + pv[i];
         }
-        if (pp < PPW) {
-          double2 *bp = buf + (k & 1) * (TB / 2) * 64 + tt * 32 + 4 * pc;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) bp[i] = make_double2(pr[2 * i], pr[2 * i + 1]);
+        for (; t < t1; ++t) {
+          const int r = t - t0;
+          acc = acc + sc[t] * ldexp((double)vm[r * 64], (int)ve[r * 4] - 15);
         }
+        if (c == nch - 1) acc = acc + sc[pos] * vc[l];
       }
-      load_blk(k + ATT_DEPTH, rm[d], re[d]);
-      if (w == 0 && k >= 1 && k <= nb) {
-        const double *bb = reinterpret_cast<const double *>(buf + ((k - 1) & 1) * (TB / 2) * 64) + l;
-        const int cnt = min(TB, n - (k - 1) * TB);
-        if (cnt == TB) {
-#pragma unroll
-          for (int i = 0; i < TB; ++i) acc = acc + bb[i * 64];
-        } else {
-          for (int i = 0; i < cnt; ++i) acc = acc + bb[i * 64];
-        }
-      }
+      if (c + 1 < nch) BFP_ATT_STORE_V(c + 1)
       __syncthreads();
     }
+  } else {
+    // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281).
+    // Iteration k: waves 1.. write the products of block k into buf[k & 1]
+    // (element (tt, dim) at double tt*64 + dim) and refill their ring slot
+    // with block k + ATT_DEPTH; wave 0 adds block k-1 from buf[(k-1) & 1],
+    // one dimension per lane.
+    const int nb = (n + TB - 1) / TB;
+    for (int k0 = 0; k0 <= nb; k0 += ATT_DEPTH) {
+#pragma unroll
+      for (int d = 0; d < ATT_DEPTH; ++d) {
+        const int k = k0 + d;               // iterations past nb do unused work
+        if (w >= 1) {
+          const int tt = pw * PPW + pp;
+          const int t = k * TB + tt;
+          const int tc = t < n ? t : n - 1;
+          const double pt = sc[tc];
+          const double s = ldexp(1.0, re[d] - 15);
+          const unsigned wv[4] = {rm[d].x, rm[d].y, rm[d].z, rm[d].w};
+          double pr[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int mi = (int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
+            const double vcur = vc[8 * pc + i];
+            const double v = (t == pos) ? vcur : (double)mi * s;
+            pr[i] = t < n ? pt * v : 0.0;
+          }
+          if (pp < PPW) {
+            double2 *bp = buf + (k & 1) * (TB / 2) * 64 + tt * 32 + 4 * pc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bp[i] = make_double2(pr[2 * i], pr[2 * i + 1]);
+          }
+        }
+        load_blk(k + ATT_DEPTH, rm[d], re[d]);
+        if (w == 0 && k >= 1 && k <= nb) {
+          const double *bb = reinterpret_cast<const double *>(buf + ((k - 1) & 1) * (TB / 2) * 64) + l;
+          const int cnt = min(TB, n - (k - 1) * TB);
+          if (cnt == TB) {
+#pragma unroll
+            for (int i = 0; i < TB; ++i) acc = acc + bb[i * 64];
+          } else {
+            for (int i = 0; i < cnt; ++i) acc = acc + bb[i * 64];
+          }
+        }
+        __syncthreads();
+      }
+    }
   }
+#undef BFP_ATT_LOAD_V
+#undef BFP_ATT_STORE_V
   if (w == 0) {
     int e;
     int m = quantize16_lanes(acc, e, true);   // tile_quantize(fp_quantize_vec(attn))
