@@ -37,54 +37,85 @@ __device__ inline double pw_leaf_sum(const double *a, int n) {
   return res;
 }
 
-template <int DEPTH>
-__device__ inline void pw_find_leaf(int lo, int n, int want, int &k, int &flo, int &fn) {
-  if constexpr (DEPTH > 0) {
-    if (n > 128) {
-      int n2 = n / 2;
-      n2 -= n2 % 8;
-      pw_find_leaf<DEPTH - 1>(lo, n2, want, k, flo, fn);
-      pw_find_leaf<DEPTH - 1>(lo + n2, n - n2, want, k, flo, fn);
-      return;
-    }
-  }
-  if (k == want) {
-    flo = lo;
-    fn = n;
-  }
-  ++k;
-}
-
-template <int DEPTH>
-__device__ inline double pw_combine(int n, const double *leaf, int &k) {
-  if constexpr (DEPTH > 0) {
-    if (n > 128) {
-      int n2 = n / 2;
-      n2 -= n2 % 8;
-      double l = pw_combine<DEPTH - 1>(n2, leaf, k);
-      double r = pw_combine<DEPTH - 1>(n - n2, leaf, k);
-      return l + r;
-    }
-  }
-  return leaf[k++];
-}
-
 constexpr int PW_DEPTH = 6;        // n <= 128 * 2^6 = 8192
-constexpr int PW_MAX_LEAVES = 64;  // n <= 8192 has at most 64 leaves of >= 128 ... (>= 64 elements)
+constexpr int PW_MAX_LEAVES = 64;  // leaf slots: one per 64-element block, n <= 4096
 
-// Sum of a[0..n) (a in LDS) in numpy order, plus numpy's initial 0.0.
-// Called by all threads of a workgroup (uses __syncthreads); leafbuf holds
-// PW_MAX_LEAVES doubles of LDS.  Returns the sum in every thread.
+// numpy's leaves combined in its order; the leaf starting at element lo is
+// leaf[lo / 64] (see pairwise_sum_block).
+template <int DEPTH>
+__device__ __forceinline__ double pw_combine_blocks(int lo, int n, const double *leaf) {
+  if constexpr (DEPTH > 0) {
+    if (n > 128) {
+      int n2 = n / 2;
+      n2 -= n2 % 8;
+      return pw_combine_blocks<DEPTH - 1>(lo, n2, leaf) +
+             pw_combine_blocks<DEPTH - 1>(lo + n2, n - n2, leaf);
+    }
+  }
+  return leaf[lo >> 6];
+}
+
+// Sum of a[0..n) (a in LDS, 1 <= n <= 4096) in numpy order, plus numpy's
+// initial 0.0.  Called by all threads of a workgroup (uses __syncthreads);
+// leafbuf holds PW_MAX_LEAVES doubles of LDS.  Returns the sum in every
+// thread.
+//
+// numpy splits a range longer than 128 at n/2 rounded down to a multiple of
+// 8, so every leaf of a range longer than 128 has at least 64 elements and
+// each 64-element block [64g, 64g+64) holds at most one leaf start.  Group
+// g of 8 lanes descends to the leaf holding element min(64g+63, n-1) and
+// owns it if the leaf starts in its block.  Lane j of the group runs
+// numpy's accumulator r_j (elements j, j+8, ... of the leaf, in order); the
+// tree ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) is formed with row rotates (lane
+// 7 of the group ends with it; float addition is commutative, so the
+// rotate partners give the same sums); then the leaf's last n%8 elements
+// are added in order.  A leaf of fewer than 8 elements is summed from 0.0
+// by one lane, as numpy does.
 __device__ __forceinline__ double pairwise_sum_block(const double *a, int n, double *leafbuf) {
-  int k = 0, flo = 0, fn = 0;
-  const int t = threadIdx.x;
-  if (t < PW_MAX_LEAVES) {
-    pw_find_leaf<PW_DEPTH>(0, n, t, k, flo, fn);
-    if (t < k) leafbuf[t] = pw_leaf_sum(a + flo, fn);
+  const int t = threadIdx.x, bs = blockDim.x;
+  const int ng = (n + 63) >> 6;
+  for (int base = 0; base < 8 * ng; base += bs) {   // uniform loop
+    const int q = base + t, gq = q >> 3, j = q & 7;
+    const int e = min(gq * 64 + 63, n - 1);
+    int flo = 0, fn = n;
+    while (fn > 128) {
+      int n2 = fn / 2;
+      n2 -= n2 % 8;
+      if (e < flo + n2) {
+        fn = n2;
+      } else {
+        flo += n2;
+        fn -= n2;
+      }
+    }
+    const bool own = gq < ng && flo >= gq * 64;
+    const int top = fn - fn % 8, end = flo + top;
+    double x[16];   // a leaf has at most 128 elements: 16 per accumulator
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int idx = flo + j + 8 * i;
+      x[i] = a[own && idx < end ? idx : 0];
+    }
+    double r = x[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = flo + j + 8 * i < end ? r + x[i] : r;
+    r = r + peer<1>(r);
+    r = r + peer<2>(r);
+    r = r + peer<4>(r);
+    if (own && j == 7) {
+      double res;
+      if (fn < 8) {
+        res = 0.0;
+        for (int i = 0; i < fn; ++i) res += a[flo + i];
+      } else {
+        res = r;
+        for (int i = top; i < fn; ++i) res += a[flo + i];
+      }
+      leafbuf[gq] = res;
+    }
   }
   __syncthreads();
-  int kk = 0;
-  double s = 0.0 + pw_combine<PW_DEPTH>(n, leafbuf, kk);
+  double s = 0.0 + pw_combine_blocks<PW_DEPTH>(0, n, leafbuf);
   __syncthreads();
   return s;
 }
