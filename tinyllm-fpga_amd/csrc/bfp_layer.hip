@@ -295,7 +295,18 @@ constexpr int ATT_AVC = 128;
 
 // The AV phase at long context (PPW 8) instead has waves 1.. form the
 // products of blocks of TB = 7*PPW positions into an LDS double buffer
-// while wave 0 adds the previous block; V is prefetched PPW blocks ahead.
+// while wave 0 adds the previous block; V is prefetched 2*PPW blocks ahead.
+// A position's 64 products sit in a row of 64 doubles as 32 16-byte
+// chunks; the pair of dimensions 8c + 2i, +1 is chunk
+// (4c + (i ^ (c >> 1))) ^ ((tt >> 1) & 1) of row tt.  With producer lane l
+// holding dimensions 8c..8c+7 (c = l % 8) of row att_lane_row(l / 8), the
+// 16 lanes of each write instruction (pair i of every lane) hit 16
+// distinct 16-byte bank groups, and the 32 lanes of each of wave 0's reads
+// (one dimension per lane) a contiguous 256 bytes.  Rows t and t+1 (t even)
+// share the swizzle, so one ds_read2st64 serves both.  (Dimension order
+// would put a write's lanes 64 bytes apart: a 4-way bank conflict.)
+__device__ __forceinline__ int att_lane_row(int g) { return ((g & 1) << 1) | ((g >> 1) & 1) | (g & 4); }
+__device__ __forceinline__ int att_chunk(int c, int i, int x) { return (4 * c + (i ^ (c >> 1))) ^ x; }
 size_t attn_lds_bytes(int max_ctx, int ppw) {
   const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
   const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4)
@@ -323,7 +334,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
   constexpr int VL = AVC * 8 / NT;             // 16-byte V loads per thread and chunk
   constexpr int TB = (ATT_WAVES - 1) * PPW;    // positions per AV block (long)
-  constexpr int ATT_DEPTH = PPW;               // V blocks in flight (long)
+  constexpr int ATT_DEPTH = 2 * PPW;           // V blocks in flight (long)
+  static_assert(SHORT || PPW == 8, "the long AV path maps 8 positions x 8 dimension groups to a wave");
   extern __shared__ double dsm[];
   double *q = dsm;                  // 64
   double *kc = dsm + 64;            // 64 (current position, post-rope)
@@ -331,10 +343,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   double *leaf = dsm + 192;         // PW_MAX_LEAVES (= 64)
   double *sc = dsm + 256;           // max_ctx, rounded up to even
   // short: staged V, 2 x AVC x 64 mantissas and 2 x AVC x 4 exponents;
-  // long: product double buffer, 2 x TB/2 x 64 double2
+  // long: product double buffer, 2 x TB rows of 64 doubles
   int16_t *vsm = reinterpret_cast<int16_t *>(sc + ((a.max_ctx + 1) & ~1));
   int8_t *vse = reinterpret_cast<int8_t *>(vsm + 2 * AVC * 64);
-  double2 *buf = reinterpret_cast<double2 *>(sc + ((a.max_ctx + 1) & ~1));
+  double *buf = sc + ((a.max_ctx + 1) & ~1);
   __shared__ double red[ATT_WAVES];
   const int hq = blockIdx.x, b = blockIdx.y;
   const int grp = a.H_Q / a.H_KV, g = hq / grp;
@@ -383,13 +395,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
 
   // Long contexts: V prefetch ring of the AV phase (filled after the scores).  Producer
   // wave pw (waves 1..) owns positions k*TB + pw*PPW + pp, pp < PPW, of
-  // block k; lane (pp = l/8, c = l%8) holds dimensions 8c..8c+7 of its
+  // block k; lane (pp = att_lane_row(l/8), c = l%8) holds dimensions 8c..8c+7 of its
   // position: one 16-byte mantissa load and one exponent byte per block.
   // Every wave issues the same loads on every path (positions past the end
   // are clamped to a valid row and their products zeroed; wave 0 loads a
   // copy it does not use), so the compiler can count ATT_DEPTH blocks of
   // loads in flight instead of draining them.
-  const int pw = w >= 1 ? w - 1 : 0, pp = l >> 3, pc = l & 7;
+  const int pw = w >= 1 ? w - 1 : 0, pp = att_lane_row(l >> 3), pc = l & 7;
   uint4 rm[SHORT ? 1 : ATT_DEPTH];
   int re[SHORT ? 1 : ATT_DEPTH];
   auto load_blk = [&](int k, uint4 &m, int &e) {
@@ -532,49 +544,91 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   } else {
     // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281).
     // Iteration k: waves 1.. write the products of block k into buf[k & 1]
-    // (element (tt, dim) at double tt*64 + dim) and refill their ring slot
+    // (row tt, chunks swizzled by att_chunk) and refill their ring slot
     // with block k + ATT_DEPTH; wave 0 adds block k-1 from buf[(k-1) & 1],
-    // one dimension per lane.
-    const int nb = (n + TB - 1) / TB;
+    // one dimension per lane.  The blocks cover positions 0 .. pos-1; row
+    // pos is this launch's V (vc, its writer workgroup may not have stored
+    // it yet) and is added last.
+    //
+    // Product: p * (m * 2^(e-15)) is one rounding of the exact real
+    // p*m*2^(e-15); so is ps * m with ps = p * 2^(e-15) whenever ps is exact,
+    // i.e. a normal number (or p = 0).  A wave with any lane whose ps falls
+    // below the normal range forms p * (m * 2^(e-15)) instead.  Positions
+    // >= pos get ps = 0: adding +-0 leaves acc (never -0) unchanged.
+    const int nb = (pos + TB - 1) / TB;
+    const int tt = pw * PPW + pp;          // this producer lane's position in a block
+    double pt_nx = sc[tt < pos ? tt : 0];  // p of the next block, read a block ahead
     for (int k0 = 0; k0 <= nb; k0 += ATT_DEPTH) {
 #pragma unroll
       for (int d = 0; d < ATT_DEPTH; ++d) {
-        const int k = k0 + d;               // iterations past nb do unused work
-        if (w >= 1) {
-          const int tt = pw * PPW + pp;
-          const int t = k * TB + tt;
-          const int tc = t < n ? t : n - 1;
-          const double pt = sc[tc];
-          const double s = ldexp(1.0, re[d] - 15);
-          const unsigned wv[4] = {rm[d].x, rm[d].y, rm[d].z, rm[d].w};
-          double pr[8];
+        const int k = k0 + d;
+        if (k <= nb) {                      // uniform: k0, d and nb are
+          if (w >= 1) {
+            const int t = k * TB + tt;
+            const bool live = t < pos;
+            const double pt = pt_nx;
+            pt_nx = sc[t + TB < pos ? t + TB : 0];
+            const double s = ldexp(1.0, re[d] - 15);
+            const double ps = live ? pt * s : 0.0;
+            const unsigned wv[4] = {rm[d].x, rm[d].y, rm[d].z, rm[d].w};
+            double pr[8];
+            if (!__any(live && pt != 0.0 && ps < 0x1p-1022)) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int mi = (int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
-            const double vcur = vc[8 * pc + i];
-            const double v = (t == pos) ? vcur : (double)mi * s;
-            pr[i] = t < n ? pt * v : 0.0;
+              for (int i = 0; i < 8; ++i)
+                pr[i] = ps * (double)(int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const double v = (double)(int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff) * s;
+                pr[i] = live ? pt * v : 0.0;
+              }
+            }
+            double2 *bp = reinterpret_cast<double2 *>(buf + (k & 1) * TB * 64 + tt * 64);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bp[att_chunk(pc, i, (tt >> 1) & 1)] = make_double2(pr[2 * i], pr[2 * i + 1]);
           }
-          if (pp < PPW) {
-            double2 *bp = buf + (k & 1) * (TB / 2) * 64 + tt * 32 + 4 * pc;
+          if (w == 0 && k >= 1) {
+            // dimension l of row i at bb[(i >> 1) & 1][i * 64]
+            const double *bb0 = buf + ((k - 1) & 1) * TB * 64;
+            const double *bb[2] = {bb0 + 2 * att_chunk(l >> 3, (l >> 1) & 3, 0) + (l & 1),
+                                   bb0 + 2 * att_chunk(l >> 3, (l >> 1) & 3, 1) + (l & 1)};
+            const int cnt = min(TB, pos - (k - 1) * TB);
+            if (cnt == TB) {
+              // groups of AV_G products; the reads of the next two groups
+              // are in flight while a group is added (LDS latency is about
+              // 8 dependent adds).  The scheduling barriers keep that
+              // shape: left alone the compiler sinks the reads toward
+              // their adds and the chain waits on each one.
+              constexpr int AV_G = 8, NG = TB / AV_G;
+              static_assert(TB % AV_G == 0, "AV groups");
+              double v[3][AV_G];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bp[i] = make_double2(pr[2 * i], pr[2 * i + 1]);
+              for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int i = 0; i < AV_G; ++i) v[q][i] = bb[(i >> 1) & 1][(q * AV_G + i) * 64];
+#pragma unroll
+              for (int gq = 0; gq < NG; ++gq) {
+                if (gq + 2 < NG) {
+#pragma unroll
+                  for (int i = 0; i < AV_G; ++i) v[(gq + 2) % 3][i] = bb[(i >> 1) & 1][((gq + 2) * AV_G + i) * 64];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < AV_G; ++i) acc = acc + v[gq % 3][i];
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            } else {
+              for (int i = 0; i < cnt; ++i) acc = acc + bb[(i >> 1) & 1][i * 64];
+            }
           }
         }
+        // outside the branch: a load in a branch makes the compiler drain
+        // every outstanding load there
         load_blk(k + ATT_DEPTH, rm[d], re[d]);
-        if (w == 0 && k >= 1 && k <= nb) {
-          const double *bb = reinterpret_cast<const double *>(buf + ((k - 1) & 1) * (TB / 2) * 64) + l;
-          const int cnt = min(TB, n - (k - 1) * TB);
-          if (cnt == TB) {
-#pragma unroll
-            for (int i = 0; i < TB; ++i) acc = acc + bb[i * 64];
-          } else {
-            for (int i = 0; i < cnt; ++i) acc = acc + bb[i * 64];
-          }
-        }
-        __syncthreads();
+        if (k <= nb) __syncthreads();
       }
     }
+    if (w == 0) acc = acc + sc[pos] * vc[l];
   }
 #undef BFP_ATT_LOAD_V
 #undef BFP_ATT_STORE_V
