@@ -294,12 +294,13 @@ constexpr int ATT_WAVES = 8;
 constexpr int ATT_AVC = 128;
 
 // The AV phase at long context (PPW 8) instead has waves 1.. form the
-// products of blocks of TB = 7*PPW positions into an LDS double buffer
-// while wave 0 adds the previous block; V is prefetched 2*PPW blocks ahead.
+// products of blocks of TB = 14*PPW positions into an LDS double buffer
+// while wave 0 adds the previous block; V is prefetched PPW blocks ahead.
 // A position's 64 products sit in a row of 64 doubles as 32 16-byte
 // chunks; the pair of dimensions 8c + 2i, +1 is chunk
 // (4c + (i ^ (c >> 1))) ^ ((tt >> 1) & 1) of row tt.  With producer lane l
-// holding dimensions 8c..8c+7 (c = l % 8) of row att_lane_row(l / 8), the
+// holding dimensions 8c..8c+7 (c = l % 8) of rows att_lane_row(l / 8) + 8r
+// (plus the wave's base, a multiple of 16), the
 // 16 lanes of each write instruction (pair i of every lane) hit 16
 // distinct 16-byte bank groups, and the 32 lanes of each of wave 0's reads
 // (one dimension per lane) a contiguous 256 bytes.  Rows t and t+1 (t even)
@@ -310,7 +311,7 @@ __device__ __forceinline__ int att_chunk(int c, int i, int x) { return (4 * c + 
 size_t attn_lds_bytes(int max_ctx, int ppw) {
   const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
   const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4)
-                             : (size_t)(ATT_WAVES - 1) * ppw * 64 * 8 * 2;
+                             : (size_t)(ATT_WAVES - 1) * 2 * ppw * 64 * 8 * 2;
   return (256 + sc_len) * 8 + av;
 }
 
@@ -333,8 +334,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   constexpr int NT = 64 * ATT_WAVES;
   constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
   constexpr int VL = AVC * 8 / NT;             // 16-byte V loads per thread and chunk
-  constexpr int TB = (ATT_WAVES - 1) * PPW;    // positions per AV block (long)
-  constexpr int ATT_DEPTH = 2 * PPW;           // V blocks in flight (long)
+  constexpr int TB = (ATT_WAVES - 1) * 2 * PPW;  // positions per AV block (long)
+  constexpr int ATT_DEPTH = PPW;                 // V blocks in flight (long)
   static_assert(SHORT || PPW == 8, "the long AV path maps 8 positions x 8 dimension groups to a wave");
   extern __shared__ double dsm[];
   double *q = dsm;                  // 64
@@ -394,22 +395,28 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   }
 
   // Long contexts: V prefetch ring of the AV phase (filled after the scores).  Producer
-  // wave pw (waves 1..) owns positions k*TB + pw*PPW + pp, pp < PPW, of
-  // block k; lane (pp = att_lane_row(l/8), c = l%8) holds dimensions 8c..8c+7 of its
-  // position: one 16-byte mantissa load and one exponent byte per block.
+  // wave pw + 1 owns rows pw*2*PPW + 8r + pp (r = 0, 1) of block k,
+  // positions k*TB + row; lane (pp = att_lane_row(l/8), c = l%8) holds
+  // dimensions 8c..8c+7 of both its positions: one 16-byte mantissa load
+  // and one exponent byte per row and block.  Two independent rows per lane
+  // halve the barriers per position and give the product arithmetic ILP.
   // Every wave issues the same loads on every path (positions past the end
   // are clamped to a valid row and their products zeroed; wave 0 loads a
   // copy it does not use), so the compiler can count ATT_DEPTH blocks of
   // loads in flight instead of draining them.
-  const int pw = w >= 1 ? w - 1 : 0, pp = att_lane_row(l >> 3), pc = l & 7;
-  uint4 rm[SHORT ? 1 : ATT_DEPTH];
-  int re[SHORT ? 1 : ATT_DEPTH];
-  auto load_blk = [&](int k, uint4 &m, int &e) {
-    int t = k * TB + pw * PPW + (pp < PPW ? pp : 0);
-    t = t < n ? t : n - 1;
-    const long long o = ((long long)t * a.H_KV + g) * HD + 8 * pc;
-    m = *reinterpret_cast<const uint4 *>(Vm + o);
-    e = Ve[o >> 4];
+  const bool producer = w >= 1;
+  const int pw = producer ? w - 1 : 0, pp = att_lane_row(l >> 3), pc = l & 7;
+  uint4 rm[SHORT ? 1 : ATT_DEPTH][2];
+  int re[SHORT ? 1 : ATT_DEPTH][2];
+  auto load_blk = [&](int k, uint4 (&m)[2], int (&e)[2]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      int t = k * TB + pw * 2 * PPW + 8 * r + pp;
+      t = t < n ? t : n - 1;
+      const long long o = ((long long)t * a.H_KV + g) * HD + 8 * pc;
+      m[r] = *reinterpret_cast<const uint4 *>(Vm + o);
+      e[r] = Ve[o >> 4];
+    }
   };
 
   // the first K row of this thread's scores, in flight during the RoPE phase
@@ -543,7 +550,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     }
   } else {
     // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281).
-    // Iteration k: waves 1.. write the products of block k into buf[k & 1]
+    // Iteration k: the producers write the products of block k into buf[k & 1]
     // (row tt, chunks swizzled by att_chunk) and refill their ring slot
     // with block k + ATT_DEPTH; wave 0 adds block k-1 from buf[(k-1) & 1],
     // one dimension per lane.  The blocks cover positions 0 .. pos-1; row
@@ -556,69 +563,84 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     // below the normal range forms p * (m * 2^(e-15)) instead.  Positions
     // >= pos get ps = 0: adding +-0 leaves acc (never -0) unchanged.
     const int nb = (pos + TB - 1) / TB;
-    const int tt = pw * PPW + pp;          // this producer lane's position in a block
-    double pt_nx = sc[tt < pos ? tt : 0];  // p of the next block, read a block ahead
+    const int tt0 = pw * 2 * PPW + pp;     // this producer lane's rows in a block: tt0, tt0 + 8
+    const int xs = (pp >> 1) & 1;          // their chunk swizzle ((row >> 1) & 1)
+    double pt_nx[2];                       // p of the next block's rows, read a block ahead
+#pragma unroll
+    for (int r = 0; r < 2; ++r) pt_nx[r] = sc[tt0 + 8 * r < pos ? tt0 + 8 * r : 0];
     for (int k0 = 0; k0 <= nb; k0 += ATT_DEPTH) {
 #pragma unroll
       for (int d = 0; d < ATT_DEPTH; ++d) {
         const int k = k0 + d;
         if (k <= nb) {                      // uniform: k0, d and nb are
-          if (w >= 1) {
-            const int t = k * TB + tt;
-            const bool live = t < pos;
-            const double pt = pt_nx;
-            pt_nx = sc[t + TB < pos ? t + TB : 0];
-            const double s = ldexp(1.0, re[d] - 15);
-            const double ps = live ? pt * s : 0.0;
-            const unsigned wv[4] = {rm[d].x, rm[d].y, rm[d].z, rm[d].w};
-            double pr[8];
-            if (!__any(live && pt != 0.0 && ps < 0x1p-1022)) {
+          if (producer) {
+            bool live[2], slow = false;
+            double pt[2], s[2], ps[2];
 #pragma unroll
-              for (int i = 0; i < 8; ++i)
-                pr[i] = ps * (double)(int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
+            for (int r = 0; r < 2; ++r) {
+              const int t = k * TB + tt0 + 8 * r;
+              live[r] = t < pos;
+              pt[r] = pt_nx[r];
+              pt_nx[r] = sc[t + TB < pos ? t + TB : 0];
+              s[r] = ldexp(1.0, re[d][r] - 15);
+              ps[r] = live[r] ? pt[r] * s[r] : 0.0;
+              slow = slow || (live[r] && pt[r] != 0.0 && ps[r] < 0x1p-1022);
+            }
+            double pr[2][8];
+            if (!__any(slow)) {
+#pragma unroll
+              for (int r = 0; r < 2; ++r) {
+                const unsigned wv[4] = {rm[d][r].x, rm[d][r].y, rm[d][r].z, rm[d][r].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                  pr[r][i] = ps[r] * (double)(int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff);
+              }
             } else {
 #pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                const double v = (double)(int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff) * s;
-                pr[i] = live ? pt * v : 0.0;
+              for (int r = 0; r < 2; ++r) {
+                const unsigned wv[4] = {rm[d][r].x, rm[d][r].y, rm[d][r].z, rm[d][r].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                  const double v = (double)(int)(short)((wv[i >> 1] >> (16 * (i & 1))) & 0xffff) * s[r];
+                  pr[r][i] = live[r] ? pt[r] * v : 0.0;
+                }
               }
             }
-            double2 *bp = reinterpret_cast<double2 *>(buf + (k & 1) * TB * 64 + tt * 64);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bp[att_chunk(pc, i, (tt >> 1) & 1)] = make_double2(pr[2 * i], pr[2 * i + 1]);
+            for (int r = 0; r < 2; ++r) {
+              double2 *bp = reinterpret_cast<double2 *>(buf + (k & 1) * TB * 64 + (tt0 + 8 * r) * 64);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) bp[att_chunk(pc, i, xs)] = make_double2(pr[r][2 * i], pr[r][2 * i + 1]);
+            }
           }
           if (w == 0 && k >= 1) {
-            // dimension l of row i at bb[(i >> 1) & 1][i * 64]
-            const double *bb0 = buf + ((k - 1) & 1) * TB * 64;
-            const double *bb[2] = {bb0 + 2 * att_chunk(l >> 3, (l >> 1) & 3, 0) + (l & 1),
-                                   bb0 + 2 * att_chunk(l >> 3, (l >> 1) & 3, 1) + (l & 1)};
-            const int cnt = min(TB, pos - (k - 1) * TB);
-            if (cnt == TB) {
-              // groups of AV_G products; the reads of the next two groups
-              // are in flight while a group is added (LDS latency is about
-              // 8 dependent adds).  The scheduling barriers keep that
-              // shape: left alone the compiler sinks the reads toward
-              // their adds and the chain waits on each one.
-              constexpr int AV_G = 8, NG = TB / AV_G;
-              static_assert(TB % AV_G == 0, "AV groups");
-              double v[3][AV_G];
+            // block k-1 in full: its rows past pos - 1 hold products of +-0.
+            // Dimension l of row i is at lb[o[(i >> 1) & 1] + 64 i].
+            const double *lb = buf + ((k - 1) & 1) * TB * 64 + (l & 1);
+            const int o0 = 2 * att_chunk(l >> 3, (l >> 1) & 3, 0), o1 = 2 * att_chunk(l >> 3, (l >> 1) & 3, 1);
+            // groups of AV_G products; the reads of the next two groups are
+            // in flight while a group is added (LDS latency is about 8
+            // dependent adds).  The scheduling barriers keep that shape:
+            // left alone the compiler sinks the reads toward their adds and
+            // the chain waits on each one.
+            constexpr int AV_G = 8, NG = TB / AV_G;
+            static_assert(TB % AV_G == 0 && AV_G % 4 == 0, "AV groups");
+            double v[3][AV_G];
 #pragma unroll
-              for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < 2; ++q)
 #pragma unroll
-                for (int i = 0; i < AV_G; ++i) v[q][i] = bb[(i >> 1) & 1][(q * AV_G + i) * 64];
+              for (int i = 0; i < AV_G; ++i) v[q][i] = lb[((i >> 1) & 1 ? o1 : o0) + (q * AV_G + i) * 64];
 #pragma unroll
-              for (int gq = 0; gq < NG; ++gq) {
-                if (gq + 2 < NG) {
+            for (int gq = 0; gq < NG; ++gq) {
+              if (gq + 2 < NG) {
 #pragma unroll
-                  for (int i = 0; i < AV_G; ++i) v[(gq + 2) % 3][i] = bb[(i >> 1) & 1][((gq + 2) * AV_G + i) * 64];
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int i = 0; i < AV_G; ++i) acc = acc + v[gq % 3][i];
-                __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < AV_G; ++i)
+                  v[(gq + 2) % 3][i] = lb[((i >> 1) & 1 ? o1 : o0) + ((gq + 2) * AV_G + i) * 64];
               }
-            } else {
-              for (int i = 0; i < cnt; ++i) acc = acc + bb[(i >> 1) & 1][i * 64];
+              __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+              for (int i = 0; i < AV_G; ++i) acc = acc + v[gq % 3][i];
+              __builtin_amdgcn_sched_barrier(0);
             }
           }
         }
