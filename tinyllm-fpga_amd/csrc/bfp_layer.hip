@@ -421,7 +421,26 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
 
   // the first K row of this thread's scores, in flight during the RoPE phase
   KRow ra, rb;
-  load_krow(ra, Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
+  // contexts of at most 128 positions (PPW 2): each 32-lane half-wave scores
+  // one position, lane j (of 32) holding elements j and 32 + j of its K row;
+  // all LS_PASS passes' elements are in flight during the RoPE phase
+  constexpr bool LANE_SPLIT = SHORT && PPW == 2;
+  constexpr int LS_PASS = LANE_SPLIT ? 128 / (2 * ATT_WAVES) : 1;
+  int lsm[LS_PASS][2], lse[LS_PASS][2];
+  if constexpr (LANE_SPLIT) {
+#pragma unroll
+    for (int ps_ = 0; ps_ < LS_PASS; ++ps_) {
+      int t = 2 * ATT_WAVES * ps_ + 2 * w + (l >> 5);
+      t = t < n ? t : n - 1;
+      const long long o = ((long long)t * a.H_KV + g) * HD + (l & 31);
+      lsm[ps_][0] = Km[o];
+      lsm[ps_][1] = Km[o + 32];
+      lse[ps_][0] = Ke[o >> 4];
+      lse[ps_][1] = Ke[(o + 32) >> 4];
+    }
+  } else {
+    load_krow(ra, Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
+  }
 
   if (w == 0) {            // q head hq
     int idx = hq * HD + l;
@@ -468,7 +487,31 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   // position per thread, two rows in flight.  Row pos is read from global
   // memory like the others (the writer may not have stored it yet) and its
   // score is recomputed from LDS afterwards by the same thread.
-  if constexpr (SHORT) {
+  if constexpr (LANE_SPLIT) {
+    // ddot64_skx's order spread over 32 lanes: lane j = 8r + c forms
+    // accumulator (r, c) = fma(x[32+j], y[32+j], fma(x[j], y[j], 0)); then
+    // f_r(c) = acc(r, c) + acc(r, c+4) lands in lane 8r + c + 4,
+    // s_c = ((f_0 + f_1) + f_2) + f_3 in lane 28 + c, and
+    // (s_0 + s_2) + (s_1 + s_3) in lane 31 (each single addition commutes).
+    // Row pos comes from LDS (its writer may not have stored it yet).
+    const int j = l & 31;
+    const double q0 = q[j], q1 = q[32 + j];
+    const double k0 = kc[j], k1 = kc[32 + j];
+#pragma unroll
+    for (int ps_ = 0; ps_ < LS_PASS; ++ps_) {
+      if (2 * ATT_WAVES * ps_ >= n) break;   // uniform; every load was issued earlier
+      const int t = 2 * ATT_WAVES * ps_ + 2 * w + (l >> 5);
+      const double y0 = t == pos ? k0 : bfp_val(lsm[ps_][0], lse[ps_][0]);
+      const double y1 = t == pos ? k1 : bfp_val(lsm[ps_][1], lse[ps_][1]);
+      const double acc = fma(q1, y1, fma(q0, y0, 0.0));
+      const double f = acc + peer<4>(acc);
+      const double t01 = peer<16>(f + peer<8>(f));
+      const double sl = (t01 + peer<8>(f)) + f;
+      const double s2 = sl + peer<2>(sl);
+      const double tot = s2 + peer<1>(s2);
+      if (j == 31 && t < n) sc[t] = tot / a.inv_sqrt_hd_div;
+    }
+  } else if constexpr (SHORT) {
     // contexts of at most NT positions: one row per thread, the one in
     // flight since the RoPE phase
     if (tid < n) sc[tid] = ddot64_skx_bfp(q, ra.m, ra.e4) / a.inv_sqrt_hd_div;
