@@ -13,30 +13,6 @@ namespace bfp {
 // <= 128 are summed with 8 accumulators, longer ranges split at
 // n2 = n/2 rounded down to a multiple of 8.  Leaves are numbered in
 // left-to-right order.
-__device__ inline double pw_leaf_sum(const double *a, int n) {
-  if (n < 8) {
-    double r = 0.0;
-    for (int i = 0; i < n; ++i) r += a[i];
-    return r;
-  }
-  double r0 = a[0], r1 = a[1], r2 = a[2], r3 = a[3], r4 = a[4], r5 = a[5], r6 = a[6], r7 = a[7];
-  int i = 8;
-  const int top = n - (n % 8);
-  for (; i < top; i += 8) {
-    r0 += a[i];
-    r1 += a[i + 1];
-    r2 += a[i + 2];
-    r3 += a[i + 3];
-    r4 += a[i + 4];
-    r5 += a[i + 5];
-    r6 += a[i + 6];
-    r7 += a[i + 7];
-  }
-  double res = ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7));
-  for (; i < n; ++i) res += a[i];
-  return res;
-}
-
 constexpr int PW_DEPTH = 6;        // n <= 128 * 2^6 = 8192
 constexpr int PW_MAX_LEAVES = 64;  // leaf slots: one per 64-element block, n <= 4096
 
@@ -55,8 +31,10 @@ __device__ __forceinline__ double pw_combine_blocks(int lo, int n, const double 
   return leaf[lo >> 6];
 }
 
-// Sum of a[0..n) (a in LDS, 1 <= n <= 4096) in numpy order, plus numpy's
-// initial 0.0.  Called by all threads of a workgroup (uses __syncthreads);
+// Sum of get(0) .. get(n-1) (1 <= n <= 4096) in numpy order, plus numpy's
+// initial 0.0; get(i) is called for the elements of this lane's leaf (and
+// for index 0 by lanes that own none), so it may read global memory.
+// Called by all threads of a workgroup (uses __syncthreads);
 // leafbuf holds PW_MAX_LEAVES doubles of LDS.  Returns the sum in every
 // thread.
 //
@@ -71,7 +49,8 @@ __device__ __forceinline__ double pw_combine_blocks(int lo, int n, const double 
 // rotate partners give the same sums); then the leaf's last n%8 elements
 // are added in order.  A leaf of fewer than 8 elements is summed from 0.0
 // by one lane, as numpy does.
-__device__ __forceinline__ double pairwise_sum_block(const double *a, int n, double *leafbuf) {
+template <class Get>
+__device__ __forceinline__ double pairwise_sum_block_g(Get get, int n, double *leafbuf) {
   const int t = threadIdx.x, bs = blockDim.x;
   const int ng = (n + 63) >> 6;
   for (int base = 0; base < 8 * ng; base += bs) {   // uniform loop
@@ -94,7 +73,7 @@ __device__ __forceinline__ double pairwise_sum_block(const double *a, int n, dou
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int idx = flo + j + 8 * i;
-      x[i] = a[own && idx < end ? idx : 0];
+      x[i] = get(own && idx < end ? idx : 0);
     }
     double r = x[0];
 #pragma unroll
@@ -106,10 +85,10 @@ __device__ __forceinline__ double pairwise_sum_block(const double *a, int n, dou
       double res;
       if (fn < 8) {
         res = 0.0;
-        for (int i = 0; i < fn; ++i) res += a[flo + i];
+        for (int i = 0; i < fn; ++i) res += get(flo + i);
       } else {
         res = r;
-        for (int i = top; i < fn; ++i) res += a[flo + i];
+        for (int i = top; i < fn; ++i) res += get(flo + i);
       }
       leafbuf[gq] = res;
     }
@@ -118,6 +97,11 @@ __device__ __forceinline__ double pairwise_sum_block(const double *a, int n, dou
   double s = 0.0 + pw_combine_blocks<PW_DEPTH>(0, n, leafbuf);
   __syncthreads();
   return s;
+}
+
+// The same sum of a[0..n) held in LDS.
+__device__ __forceinline__ double pairwise_sum_block(const double *a, int n, double *leafbuf) {
+  return pairwise_sum_block_g([a](int i) { return a[i]; }, n, leafbuf);
 }
 
 // ------------------------------------------------------------------ ddot

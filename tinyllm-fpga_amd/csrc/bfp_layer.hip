@@ -35,53 +35,57 @@ __device__ __forceinline__ int cur_pos(const LayerArgs &a) {
 
 // rmsnorm_fp (full.py:236-238) of a BFP vector, re-quantised, into the
 // matvec's LDS input form.  v = pairwise_sum(x*x)/D + 1e-5, y = (x*g)/sqrt(v).
-// dbuf: 3*D doubles of LDS (x*x, x, g), leaf: PW_MAX_LEAVES doubles.  Every
-// thread issues all of its global loads (h, its exponents, g) before using
-// any, so the prologue costs one memory round trip.  All threads call.
+// dbuf: D shorts of LDS, leaf: PW_MAX_LEAVES doubles.  Thread tid keeps
+// elements tid + k*bs (k < 4) and their gammas in registers from one batch
+// of loads; the owners of numpy's pairwise leaves load their x elements
+// themselves (pairwise_sum_block_g), so nothing is staged in LDS before the
+// sum, and the up-to-four divisions and tile quantisations of a thread are
+// independent chains.  All threads call.
 __device__ __forceinline__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
                              const double *__restrict__ g, int D, int *xs, int *xes, double *dbuf,
                              double *leaf, int16_t *dm, int8_t *de) {
+  constexpr int KE = 4;
   const int bs = blockDim.x, tid = threadIdx.x;
-  double *sq = dbuf, *xv = dbuf + D, *gv = dbuf + 2 * D;
-  for (int i0 = tid; i0 < D; i0 += 4 * bs) {
-    int m[4], e[4];
-    double gg[4];
+  int m[KE], e[KE];
+  double gg[KE];
+  auto load = [&](int base) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      int i = i0 + k * bs;
+    for (int k = 0; k < KE; ++k) {
+      int i = base + tid + k * bs;
       i = i < D ? i : D - 1;
       m[k] = hm[i];
       e[k] = he[i >> 4];
       gg[k] = g[i];
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = i0 + k * bs;
-      if (i < D) {
-        const double x = bfp_val(m[k], e[k]);
-        sq[i] = x * x;
-        xv[i] = x;
-        gv[i] = gg[k];
-      }
-    }
-  }
-  __syncthreads();
-  const double s = pairwise_sum_block(sq, D, leaf);
+  };
+  load(0);
+  const double s = pairwise_sum_block_g(
+      [&](int i) {
+        const double x = bfp_val(hm[i], he[i >> 4]);
+        return x * x;
+      },
+      D, leaf);
   const double rt = sqrt(s / (double)D + 1e-5);
-  short *mq = reinterpret_cast<short *>(sq);   // sq is free again
-  for (int base = 0; base < D; base += bs) {
-    int i = base + tid;
-    bool ok = i < D;
-    double y = 0.0;
-    if (ok) y = (xv[i] * gv[i]) / rt;
-    int e;
-    int m = quantize16_lanes(y, e, true);   // tile_quantize(rmsnorm_fp(.)): canonical
-    if (ok) {
-      mq[i] = (short)m;
-      if ((i & 15) == 0) xes[i >> 4] = e;
-      if (dm) {
-        dm[i] = (int16_t)m;
-        if ((i & 15) == 0) de[i >> 4] = (int8_t)e;
+  short *mq = reinterpret_cast<short *>(dbuf);
+  for (int base = 0; base < D; base += KE * bs) {   // one pass when D <= 4*bs
+    if (base > 0) load(base);
+    int mm[KE], ee[KE];
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+      const int i = base + tid + k * bs;
+      const double y = i < D ? (bfp_val(m[k], e[k]) * gg[k]) / rt : 0.0;
+      mm[k] = quantize16_lanes(y, ee[k], true);   // tile_quantize(rmsnorm_fp(.)): canonical
+    }
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+      const int i = base + tid + k * bs;
+      if (i < D) {
+        mq[i] = (short)mm[k];
+        if ((i & 15) == 0) xes[i >> 4] = ee[k];
+        if (dm) {
+          dm[i] = (int16_t)mm[k];
+          if ((i & 15) == 0) de[i >> 4] = (int8_t)ee[k];
+        }
       }
     }
   }
