@@ -132,20 +132,21 @@ def test_decode_long_context(gpu):
     gm.close()
 
 
-def test_decode_mid_context(gpu):
-    """Contexts of 129..512 positions (the attention variant with four
-    positions per thread and V staged in chunks of 128 rows): 290 greedy
-    tokens after a 10-token prompt, every layer output at every step
-    against the oracle, for two sequences at once."""
-    cfg = dict(TINY, MAX_CTX=300)
+@pytest.mark.parametrize("max_ctx", [200, 300], ids=["lane-split-256", "per-thread-512"])
+def test_decode_mid_context(gpu, max_ctx):
+    """Context capacities of 129..256 (scores spread over 32-lane half-waves)
+    and 257..512 (one score per thread), V staged in chunks of 128 rows:
+    greedy decode to the capacity after a 10-token prompt, every layer output
+    at every step against the oracle, for two sequences at once."""
+    cfg = dict(TINY, MAX_CTX=max_ctx)
     d, om, gm = _setup(cfg, seed=14, max_batch=2)
     from bfp import synth
     prompts = np.stack([synth.make_prompt(d, 10, seed=14 + b) for b in range(2)])
-    n_gen = 300 - 10
+    n_gen = max_ctx - 10
     toks, (hm, he) = gm.decode(prompts, n_gen, hist=True)
     for b in range(2):
         want, whm, whe = _oracle_decode(om, prompts[b], n_gen)
-        bad = [s for s in range(300) if not ((hm[b, s] == whm[s]).all() and (he[b, s] == whe[s]).all())]
+        bad = [s for s in range(max_ctx) if not ((hm[b, s] == whm[s]).all() and (he[b, s] == whe[s]).all())]
         assert not bad, f"seq {b}: steps with differing layer outputs: {bad[:10]}"
         assert list(toks[b]) == list(want)
     gm.close()

@@ -331,8 +331,9 @@ __device__ __forceinline__ void load_krow(KRow &r, const int16_t *Km, const int8
   r.e4 = *reinterpret_cast<const int *>(Ke + (o >> 4));
 }
 
-// SHORT: max_ctx <= 64 * ATT_WAVES, one score per thread; fewer registers,
-// two workgroups per CU (many sequences at short context).
+// SHORT: max_ctx <= 64 * ATT_WAVES, at most one score per thread (PPW 4) or
+// one per 32-lane half-wave (PPW 2: max_ctx <= 128, PPW 3: <= 256); fewer
+// registers, two workgroups per CU (many sequences at short context).
 template <int PPW, bool SHORT>
 __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerArgs a) {
   constexpr int NT = 64 * ATT_WAVES;
@@ -425,11 +426,12 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
 
   // the first K row of this thread's scores, in flight during the RoPE phase
   KRow ra, rb;
-  // contexts of at most 128 positions (PPW 2): each 32-lane half-wave scores
-  // one position, lane j (of 32) holding elements j and 32 + j of its K row;
-  // all LS_PASS passes' elements are in flight during the RoPE phase
-  constexpr bool LANE_SPLIT = SHORT && PPW == 2;
-  constexpr int LS_PASS = LANE_SPLIT ? 128 / (2 * ATT_WAVES) : 1;
+  // contexts of at most 128 (PPW 2) or 256 (PPW 3) positions: each 32-lane
+  // half-wave scores one position, lane j (of 32) holding elements j and
+  // 32 + j of its K row; all LS_PASS passes' elements are in flight during
+  // the RoPE phase
+  constexpr bool LANE_SPLIT = SHORT && (PPW == 2 || PPW == 3);
+  constexpr int LS_PASS = LANE_SPLIT ? (PPW == 2 ? 128 : 256) / (2 * ATT_WAVES) : 1;
   int lsm[LS_PASS][2], lse[LS_PASS][2];
   if constexpr (LANE_SPLIT) {
 #pragma unroll
@@ -1364,10 +1366,12 @@ static void shape_for(int nT, int &nw, int &tpt) {
   tpt = (nT + 4 * nw - 1) / (4 * nw);
 }
 
-static int attn_ppw(int max_ctx) { return max_ctx <= 128 ? 2 : (max_ctx <= 512 ? 4 : 8); }
+static int attn_ppw(int max_ctx) {
+  return max_ctx <= 128 ? 2 : (max_ctx <= 256 ? 3 : (max_ctx <= 512 ? 4 : 8));
+}
 static lk_fn attn_kernel(int ppw) {
-  // max_ctx <= 512 = 64 * ATT_WAVES for ppw 2 and 4: the one-score-per-thread form
-  return ppw == 2 ? k_attn<2, true> : (ppw == 4 ? k_attn<4, true> : k_attn<8, false>);
+  // max_ctx <= 512 = 64 * ATT_WAVES for ppw 2, 3 and 4: the short forms
+  return ppw == 2 ? k_attn<2, true> : (ppw == 3 ? k_attn<3, true> : (ppw == 4 ? k_attn<4, true> : k_attn<8, false>));
 }
 
 // Per device, before the first launch (outside any stream capture): allow
