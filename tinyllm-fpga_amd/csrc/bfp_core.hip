@@ -223,8 +223,8 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
   const int wmat = ring > 0 ? mat % ring : mat;
 
   ChunkRegs<TPT> R;
-  load_chunk<NW, TPT>(R, Pm + wmat * smat_m + (long long)c * nT * 32,
-                      Pe + wmat * smat_e + (long long)c * nT * 16, nT);
+  load_chunk<NW, TPT, true>(R, Pm + wmat * smat_m + (long long)c * nT * 32,
+                            Pe + wmat * smat_e + (long long)c * nT * 16, nT);
   stage_x_bfp(xs, xes, xm + mat * x_stride, xe + mat * (x_stride / 16), nT);
   __syncthreads();
   long long A;

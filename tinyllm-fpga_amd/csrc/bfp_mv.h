@@ -24,7 +24,11 @@ struct ChunkRegs {
   int e[TPT];
 };
 
-template <int NW, int TPT>
+// NT: mantissas with the non-temporal cache policy.  Measured on the
+// one-chunk-per-workgroup matvec it lifts the weight stream 3-10%; the
+// streaming form and the latency-bound decode kernels read faster with
+// ordinary loads.
+template <int NW, int TPT, bool NT = false>
 __device__ __forceinline__ void load_chunk(ChunkRegs<TPT> &R, const uint4 *__restrict__ pm,
                                            const int8_t *__restrict__ pe, int nT) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -33,8 +37,8 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<TPT> &R, const uint4 *__res
   for (int j = 0; j < TPT; ++j) {
     int t = tq + 4 * (w + NW * j);
     if (t < nT) {
-      R.a[j] = pm[t * 32 + r];
-      R.b[j] = pm[t * 32 + 16 + r];
+      R.a[j] = NT ? ld_nt(pm + t * 32 + r) : pm[t * 32 + r];
+      R.b[j] = NT ? ld_nt(pm + t * 32 + 16 + r) : pm[t * 32 + 16 + r];
       R.e[j] = pe[t * 16 + r];
     } else {
       R.a[j] = make_uint4(0, 0, 0, 0);
