@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--reps", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-workers", type=int, default=0,
+                    help="processes for the all-cores CPU baseline (0: min(cpu count, 16))")
+    ap.add_argument("--cpu-worker", type=float, default=None, help=argparse.SUPPRESS)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-3 decode leg")
     ap.add_argument("--decode-reps", type=int, default=3)
@@ -177,13 +180,13 @@ def kernel_name(n_out, n_in, reps):
     return ("matvec_stream_kernel<%d,%d>" if stream else "matvec_kernel<%d,%d>") % (nw, tpt)
 
 
-def cpu_baseline(seconds):
-    """The oracle's numpy matvec_hw_golden (restating full.py:217-233),
-    single-threaded, on a bounded sample of the same sweep."""
+def _cpu_matvec_sample(seconds):
+    """The oracle's numpy matvec_hw_golden (restating full.py:217-233) on a
+    bounded sample of the sweep: up to 1000 reps per shape, about
+    seconds/5 per shape.  Returns (algorithmic bytes, seconds, reps)."""
     import numpy as np
     from oracle import bfp_sim as sim
     from bfp import synth
-    os.environ.setdefault("OPENBLAS_NUM_THREADS", "1")
     total_b, total_t, done = 0, 0.0, []
     per_shape = seconds / len(SHAPES)
     for n_out, n_in in SHAPES:
@@ -202,10 +205,41 @@ def cpu_baseline(seconds):
         total_b += alg_bytes(n_out, n_in) * n
         total_t += dt
         done.append(f"{n_out}x{n_in}:{n}")
+    return total_b, total_t, done
+
+
+def cpu_baseline(seconds):
+    """The oracle's numpy matvec, single-threaded, on a bounded sample of
+    the same sweep."""
+    os.environ.setdefault("OPENBLAS_NUM_THREADS", "1")
+    total_b, total_t, done = _cpu_matvec_sample(seconds)
     return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "port",
             "sample": "oracle/bfp_sim.matvec_hw_golden (numpy, 1 thread), reps per shape "
                       + ", ".join(done) + f" in {total_t:.1f} s"}
+
+
+def cpu_baseline_all_cores(seconds, workers):
+    """The same sample run concurrently by `workers` single-threaded child
+    processes (this script with --cpu-worker; they import numpy and the
+    oracle only, never the GPU runtime); aggregate bytes over the slowest
+    worker's time."""
+    import subprocess
+    env = dict(os.environ, OPENBLAS_NUM_THREADS="1", OMP_NUM_THREADS="1")
+    procs = [subprocess.Popen([sys.executable, str(Path(__file__).resolve()), "--cpu-worker",
+                               str(seconds)], stdout=subprocess.PIPE, env=env, text=True)
+             for _ in range(workers)]
+    res = []
+    for p in procs:
+        out, _ = p.communicate()
+        if p.returncode != 0:
+            raise RuntimeError(f"cpu worker exited with {p.returncode}")
+        res.append(json.loads(out.strip().splitlines()[-1]))
+    total_b = sum(r["bytes"] for r in res)
+    t = max(r["seconds"] for r in res)
+    return {"value": round(total_b / t / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
+            "sample": f"{workers} concurrent single-threaded processes, each the 1-thread sample "
+                      f"({seconds:.0f} s budget), slowest {t:.1f} s"}
 
 
 def decode_leg(reps):
@@ -379,6 +413,10 @@ def stream_probe():
 
 def main():
     args = parse()
+    if args.cpu_worker is not None:   # child of cpu_baseline_all_cores: CPU only
+        b, t, _ = _cpu_matvec_sample(args.cpu_worker)
+        print(json.dumps({"bytes": b, "seconds": t}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py: only --gpus 1 is supported on this build (asked for {args.gpus}); "
               "the BFP datapath is measured on one GPU", file=sys.stderr)
@@ -480,6 +518,8 @@ def main():
         out["stream_ceiling"] = stream_probe()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        workers = args.cpu_workers or min(os.cpu_count() or 1, 16)
+        out["cpu_baseline_all_cores"] = cpu_baseline_all_cores(8.0, workers)
         if not args.no_decode:
             out["decode"]["cpu_baseline"] = cpu_decode_baseline()
     print(json.dumps(out), flush=True)
