@@ -76,6 +76,8 @@ SIGNATURES = {
     "bfp_layer_step": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, C.POINTER(StageDumpC)]),
     "bfp_rtl_layer_step": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, C.POINTER(StageDumpC)]),
     "bfp_head": (i32, [vp, i32, vp, vp, vp, vp]),
+    "bfp_rtl_head": (i32, [vp, vp, vp, vp, vp, vp]),
+    "bfp_rtl_decode": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "bfp_decode": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, i32]),
     "bfp_decode_time": (i32, [vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     "bfp_decode_step_times": (i32, [vp, vp, i32]),

@@ -160,6 +160,37 @@ class BfpModel:
              _p(h_m), _p(h_e), _p(out_m), _p(out_e), C.byref(sd) if sd is not None else None)
         return out_m, out_e, stages
 
+    def rtl_head(self, h_m, h_e, logits=False):
+        """The FPGA decode head (smollm_decode_head_bfp.sv: RMSNorm engine
+        with the final norm gamma, lm_head on the matvec engine over the
+        tile-quantised tied embedding, bfp_gt running argmax) on one BFP
+        hidden state; returns token or (token, (logit_m, logit_e)) with one
+        exponent per logit."""
+        d = self.dims
+        h_m = _c16(h_m).reshape(d.D)
+        h_e = _c8(h_e).reshape(d.D // 16)
+        tok = np.zeros(1, np.int32)
+        lm = np.empty(d.VOCAB, np.int16) if logits else None
+        le = np.empty(d.VOCAB, np.int8) if logits else None
+        call("bfp_rtl_head", self._h, _p(h_m), _p(h_e), _p(lm) if logits else None,
+             _p(le) if logits else None, _p(tok))
+        return (int(tok[0]), (lm, le)) if logits else int(tok[0])
+
+    def rtl_decode(self, prompt, n_gen, hist=False):
+        """The FPGA's token loop (autoregress_bfp_top.sv:357-386) over the
+        composed RTL layer and head, on sequence 0 of this context: returns
+        the len(prompt) + n_gen per-step predictions, and with hist=True also
+        the last layer's output per step ((steps, D), (steps, D/16))."""
+        d = self.dims
+        ids = np.ascontiguousarray(np.asarray(prompt, np.int32).reshape(-1))
+        steps = ids.size + int(n_gen)
+        preds = np.zeros(steps, np.int32)
+        hm = np.zeros((steps, d.D), np.int16) if hist else None
+        he = np.zeros((steps, d.D // 16), np.int8) if hist else None
+        call("bfp_rtl_decode", self._h, _p(ids), ids.size, int(n_gen), _p(preds),
+             _p(hm) if hist else None, _p(he) if hist else None)
+        return (preds, (hm, he)) if hist else preds
+
     def fwd_layer(self, h, layer, pos, kv_pos=None):
         """The reference's fwd_layer(h, lw, pos, kv, kv_pos) (full.py:261-293)
         with the layer's weights and KV cache resident in the context:

@@ -43,6 +43,11 @@ struct bfp_ctx {
   uint16_t *rtl_exp = nullptr;
   int16_t *rtl_silu = nullptr;
   unsigned *rtl_freq = nullptr;
+  // the RTL decode head's buffers, made on its first use
+  uint4 *rtl_emb_m = nullptr;
+  int8_t *rtl_emb_e = nullptr, *rtl_lg_e = nullptr, *rtl_xn_e = nullptr;
+  int16_t *rtl_lg_m = nullptr, *rtl_xn_m = nullptr;
+  int *rtl_work = nullptr, *rtl_tok = nullptr;
   std::vector<void *> allocs;
   float last_decode_ms = 0.f, last_gen_ms = 0.f;
   std::vector<float> step_ms;   // per-step device time of the last decode (BFP_DECODE_STEP_TIMES)
@@ -508,6 +513,60 @@ int bfp_layer_step(bfp_ctx *c, int layer, int pos, int batch, const int16_t *h_m
   return BFP_OK;
 }
 
+// The engine tables of the composed RTL layer, made on their first use.
+static int rtl_tables_ready(bfp_ctx *c) {
+  if (c->rtl_exp) return BFP_OK;
+  const bfp_dims &d = c->d;
+  std::vector<uint16_t> ex(1024);
+  std::vector<int16_t> si(65536);
+  std::vector<uint32_t> fr(d.HD / 2);
+  BFP_TRY(bfp_rtl_tables(ex.data(), si.data(), fr.data(), d.HD, 10000.0));
+  uint16_t *de;
+  int16_t *ds;
+  unsigned *df;
+  BFP_TRY(c->alloc((void **)&de, ex.size() * 2));
+  BFP_TRY(c->alloc((void **)&ds, si.size() * 2));
+  BFP_TRY(c->alloc((void **)&df, fr.size() * 4));
+  HIP_TRY(hipMemcpy(de, ex.data(), ex.size() * 2, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(ds, si.data(), si.size() * 2, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(df, fr.data(), fr.size() * 4, hipMemcpyHostToDevice));
+  c->rtl_exp = de, c->rtl_silu = ds, c->rtl_freq = df;
+  return BFP_OK;
+}
+
+static RtlArgs rtl_args(bfp_ctx *c, int layer, int pos, int kv_pos) {
+  RtlArgs a;
+  a.L = layer_args(c, layer, 1);
+  a.exp_lut = c->rtl_exp;
+  a.silu_lut = c->rtl_silu;
+  a.freq = c->rtl_freq;
+  a.pos = pos;
+  a.kv_pos = kv_pos;
+  return a;
+}
+
+// The RTL head's buffers (made once) and its tile-quantised embedding in the
+// device layout (re-made on every call, so it follows the loaded weights).
+static int rtl_head_ready(bfp_ctx *c, RtlHeadArgs &ha) {
+  const bfp_dims &d = c->d;
+  if (d.D % 64 || d.VOCAB % 16)
+    return set_err(BFP_EINVAL, "rtl head: D %d must be a multiple of 64, VOCAB %d of 16", d.D, d.VOCAB);
+  if (!c->rtl_emb_m) {
+    BFP_TRY(c->alloc((void **)&c->rtl_emb_m, (size_t)d.VOCAB * d.D * 2));
+    BFP_TRY(c->alloc((void **)&c->rtl_emb_e, (size_t)d.VOCAB * d.D / 16));
+    BFP_TRY(c->alloc((void **)&c->rtl_lg_m, (size_t)d.VOCAB * 2));
+    BFP_TRY(c->alloc((void **)&c->rtl_lg_e, (size_t)d.VOCAB));
+    BFP_TRY(c->alloc((void **)&c->rtl_xn_m, (size_t)d.D * 2));
+    BFP_TRY(c->alloc((void **)&c->rtl_xn_e, (size_t)d.D / 16));
+    BFP_TRY(c->alloc((void **)&c->rtl_work, sizeof(int) * 3 * (size_t)(d.VOCAB / 16)));
+    BFP_TRY(c->alloc((void **)&c->rtl_tok, sizeof(int)));
+  }
+  BFP_TRY(bfp_quantize_pack_f32_d(c->embed, d.VOCAB, d.D, c->rtl_emb_m, c->rtl_emb_e, c->stream));
+  ha = RtlHeadArgs{d.D, d.VOCAB, c->h_m, c->h_e, c->norm_w, c->rtl_xn_m, c->rtl_xn_e,
+                   c->rtl_emb_m, c->rtl_emb_e, c->rtl_lg_m, c->rtl_lg_e, c->rtl_work, c->rtl_tok};
+  return BFP_OK;
+}
+
 // The composed RTL-exact layer (smollm_layer_bfp.sv:1603-2600) on one
 // sequence: RoPE at pos, KV slot kv_pos, attention over slots 0..kv_pos.
 int bfp_rtl_layer_step(bfp_ctx *c, int layer, int pos, int kv_pos, const int16_t *h_m,
@@ -521,31 +580,10 @@ int bfp_rtl_layer_step(bfp_ctx *c, int layer, int pos, int kv_pos, const int16_t
     return set_err(BFP_ERANGE, "kv_pos %d outside the KV capacity %d", kv_pos, c->max_ctx);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t s = c->stream;
-  if (!c->rtl_exp) {
-    std::vector<uint16_t> ex(1024);
-    std::vector<int16_t> si(65536);
-    std::vector<uint32_t> fr(d.HD / 2);
-    BFP_TRY(bfp_rtl_tables(ex.data(), si.data(), fr.data(), d.HD, 10000.0));
-    uint16_t *de;
-    int16_t *ds;
-    unsigned *df;
-    BFP_TRY(c->alloc((void **)&de, ex.size() * 2));
-    BFP_TRY(c->alloc((void **)&ds, si.size() * 2));
-    BFP_TRY(c->alloc((void **)&df, fr.size() * 4));
-    HIP_TRY(hipMemcpy(de, ex.data(), ex.size() * 2, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(ds, si.data(), si.size() * 2, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(df, fr.data(), fr.size() * 4, hipMemcpyHostToDevice));
-    c->rtl_exp = de, c->rtl_silu = ds, c->rtl_freq = df;
-  }
+  BFP_TRY(rtl_tables_ready(c));
   HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)d.D * 2, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)d.D / 16, hipMemcpyHostToDevice, s));
-  RtlArgs a;
-  a.L = layer_args(c, layer, 1);
-  a.exp_lut = c->rtl_exp;
-  a.silu_lut = c->rtl_silu;
-  a.freq = c->rtl_freq;
-  a.pos = pos;
-  a.kv_pos = kv_pos;
+  RtlArgs a = rtl_args(c, layer, pos, kv_pos);
   DevBuf tmp;
   StageDump sd;
   int len[ST_COUNT];
@@ -571,6 +609,63 @@ int bfp_rtl_layer_step(bfp_ctx *c, int layer, int pos, int kv_pos, const int16_t
     }
   }
   HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+// The FPGA decode head (smollm_decode_head_bfp.sv) on one hidden state.
+int bfp_rtl_head(bfp_ctx *c, const int16_t *h_m, const int8_t *h_e, int16_t *logit_m,
+                 int8_t *logit_e, int32_t *token) {
+  if (!c || !h_m || !h_e || !token) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  RtlHeadArgs ha;
+  BFP_TRY(rtl_head_ready(c, ha));
+  HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)d.D * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)d.D / 16, hipMemcpyHostToDevice, s));
+  BFP_TRY(launch_rtl_head(ha, s));
+  if (logit_m) HIP_TRY(hipMemcpyAsync(logit_m, c->rtl_lg_m, (size_t)d.VOCAB * 2, hipMemcpyDeviceToHost, s));
+  if (logit_e) HIP_TRY(hipMemcpyAsync(logit_e, c->rtl_lg_e, (size_t)d.VOCAB, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(token, c->rtl_tok, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+// The FPGA's token loop over the composed RTL layer and head, sequence 0.
+int bfp_rtl_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int32_t *preds,
+                   int16_t *hist_m, int8_t *hist_e) {
+  if (!c || !prompt || !preds) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  if (n_prompt < 1 || n_gen < 0) return set_err(BFP_EINVAL, "n_prompt %d, n_gen %d", n_prompt, n_gen);
+  const int steps = n_prompt + n_gen;
+  if (steps > c->max_ctx || steps > 2048)
+    return set_err(BFP_ERANGE, "%d steps beyond the KV capacity %d or the RTL position range 2048",
+                   steps, c->max_ctx);
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= d.VOCAB)
+      return set_err(BFP_EINVAL, "prompt id %d out of range", prompt[i]);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  BFP_TRY(rtl_tables_ready(c));
+  RtlHeadArgs ha;
+  BFP_TRY(rtl_head_ready(c, ha));
+  const EmbedArgs ea{d.D, 1, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
+  for (int step = 0; step < steps; ++step) {
+    const int st[2] = {step, step < n_prompt ? prompt[step] : preds[step - 1]};
+    HIP_TRY(hipMemcpyAsync(c->state, st, sizeof st, hipMemcpyHostToDevice, s));
+    BFP_TRY(launch_embed(ea, s));
+    for (int l = 0; l < d.NL; ++l) BFP_TRY(launch_rtl_layer(rtl_args(c, l, step, step), s));
+    if (hist_m && hist_e) {
+      HIP_TRY(hipMemcpyAsync(hist_m + (size_t)step * d.D, c->h_m, (size_t)d.D * 2, hipMemcpyDeviceToHost, s));
+      HIP_TRY(hipMemcpyAsync(hist_e + (size_t)step * d.D / 16, c->h_e, (size_t)d.D / 16,
+                             hipMemcpyDeviceToHost, s));
+    }
+    BFP_TRY(launch_rtl_head(ha, s));
+    int tok = 0;
+    HIP_TRY(hipMemcpyAsync(&tok, c->rtl_tok, sizeof tok, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    preds[step] = tok;
+  }
   return BFP_OK;
 }
 

@@ -77,4 +77,6 @@ int launch_ctl(const CtlArgs &a, hipStream_t s);
 struct RtlArgs;
 // The composed RTL-exact layer step (bfp_rtl.hip).
 int launch_rtl_layer(const RtlArgs &a, hipStream_t s);
+struct RtlHeadArgs;
+int launch_rtl_head(const RtlHeadArgs &a, hipStream_t s);
 }  // namespace bfp

@@ -61,6 +61,18 @@ struct RtlArgs {
   int pos, kv_pos;            // RoPE position, KV slot (attention over 0..kv_pos)
 };
 
+// The FPGA decode head (smollm_decode_head_bfp.sv) on one sequence.
+struct RtlHeadArgs {
+  int D, VOCAB;
+  const int16_t *h_m; const int8_t *h_e;     // final hidden state
+  const double *norm_w;                      // final norm gamma (tile_quantize'd on the device)
+  int16_t *xn_m; int8_t *xn_e;               // normed hidden
+  const uint4 *emb_m; const int8_t *emb_e;   // tile-quantised tied embedding, device layout
+  int16_t *lg_m; int8_t *lg_e;               // per-row logits (VOCAB of each)
+  int *work;                                 // 3 * VOCAB / 16 ints
+  int *token;                                // argmax out (device)
+};
+
 struct HeadArgs {
   int D, VOCAB, batch, rows_per_wg, n_wg;
   const int16_t *h_m; const int8_t *h_e;   // final hidden (BFP)
