@@ -52,6 +52,28 @@ def test_head_argmax_and_logits(gpu):
     gm.close()
 
 
+def test_head_batched_equals_single_d576(gpu):
+    """The batched head (k_head_norm + k_head_gemv, D = 576: the exact-width
+    variant) over 20 sequences -- one full LDS group of 16 and a partial
+    one -- equals the single-sequence head bit for bit (same summation
+    order per logit), and the oracle to rounding."""
+    cfg = dict(D=576, H_Q=9, H_KV=3, HD=64, FFN=1536, NL=1, MAX_CTX=8, VOCAB=1024)
+    d, om, gm = _setup(cfg, seed=9, max_batch=20)
+    rng = np.random.default_rng(9)
+    hs = [sim.fp_quantize_vec(rng.standard_normal(d.D) * (0.3 + 0.2 * b)) for b in range(20)]
+    q = [sim.tile_quantize(h) for h in hs]
+    am, lg = gm.head(np.stack([x[0].reshape(-1) for x in q]), np.stack([x[1] for x in q]),
+                     logits=True)
+    for b in (0, 7, 15, 16, 19):
+        a1, l1 = gm.head(q[b][0].reshape(1, -1), q[b][1].reshape(1, -1), logits=True)
+        assert (lg[b].view(np.int64) == l1[0].view(np.int64)).all(), b
+        assert am[b] == a1[0]
+        want = sim.head_logits(hs[b], om.norm_w_q, om.embed)
+        assert np.allclose(lg[b], want, rtol=1e-13, atol=1e-13)
+        assert am[b] == int(np.argmax(want))
+    gm.close()
+
+
 @pytest.mark.parametrize("graph", [True, False], ids=["graph", "direct"])
 def test_decode_tiny(gpu, graph):
     d, om, gm = _setup(TINY, seed=5)

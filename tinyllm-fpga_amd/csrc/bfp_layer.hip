@@ -1068,6 +1068,7 @@ __device__ __forceinline__ void final_norm(const int16_t *__restrict__ hm, const
 // 0..3) with FMA, then a fixed 16-lane butterfly.  (BLAS dgemv's order is
 // host-specific; the argmax differs only if the top two logits are within
 // a few ulps.)
+template <int MAXD64, bool EXACT>
 __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
   extern __shared__ double dsm[];
   double *hn = dsm;                    // 3*D: the final norm's work space, then hn (D)
@@ -1075,25 +1076,41 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
   __shared__ double bv[16];
   __shared__ int bi[16];
   const int b = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
+  const int l16 = tid & 15, sub = tid >> 4;      // 16 row slots per pass
+  const int d64 = a.D / 64, r0 = wg * a.rows_per_wg;
+  // a pass's embedding words, every load unconditional (a load behind a
+  // branch is waited out there); the first pass is in flight during the
+  // final norm, each later one during the previous pass's arithmetic
+  float4 cur[MAXD64], nxt[MAXD64];
+  auto load_rows = [&](int rr, float4 (&f)[MAXD64]) {
+    rr = rr < a.rows_per_wg ? rr : sub;
+    const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)(r0 + rr) * a.D);
+#pragma unroll
+    for (int i = 0; i < MAXD64; ++i) f[i] = e4[(EXACT || i < d64 ? i : d64 - 1) * 16 + l16];
+  };
+  load_rows(sub, cur);
   final_norm(a.h_m + b * a.D, a.h_e + b * (a.D / 16), a.norm_w, a.D, dsm, leaf, hn);
   __syncthreads();
 
-  const int l16 = tid & 15, sub = tid >> 4;      // 16 row slots per pass
   double best = -INFINITY;
   int besti = 0x7fffffff;
-  const int r0 = wg * a.rows_per_wg;
   for (int rr = sub; rr < a.rows_per_wg; rr += 16) {
     const int row = r0 + rr;
-    const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)row * a.D);
+    load_rows(rr + 16, nxt);
     double acc = 0.0;
-    for (int i = 0; i < a.D / 64; ++i) {
-      float4 f = e4[i * 16 + l16];
-      const double *hp = hn + i * 64 + 4 * l16;
-      acc = fma((double)f.x, hp[0], acc);
-      acc = fma((double)f.y, hp[1], acc);
-      acc = fma((double)f.z, hp[2], acc);
-      acc = fma((double)f.w, hp[3], acc);
+#pragma unroll
+    for (int i = 0; i < MAXD64; ++i) {
+      if (EXACT || i < d64) {
+        const float4 f = cur[i];
+        const double *hp = hn + i * 64 + 4 * l16;
+        acc = fma((double)f.x, hp[0], acc);
+        acc = fma((double)f.y, hp[1], acc);
+        acc = fma((double)f.z, hp[2], acc);
+        acc = fma((double)f.w, hp[3], acc);
+      }
     }
+#pragma unroll
+    for (int i = 0; i < MAXD64; ++i) cur[i] = nxt[i];
     acc = psum<8>(acc);
     acc = psum<4>(acc);
     acc = psum<2>(acc);
@@ -1146,7 +1163,10 @@ static int head_seq_group(int D) {
   return g < 1 ? 1 : (g > HEAD_SEQ_GROUP ? HEAD_SEQ_GROUP : g);
 }
 
-template <int MAXD64, int R>
+// EXACT: D == 64 * MAXD64, so every 64-column block is present and no load
+// or LDS read sits behind a per-block branch (the compiler waits out every
+// load at such a branch).
+template <int MAXD64, int R, bool EXACT>
 __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
   extern __shared__ double hs[];       // sg x D
   __shared__ double bv[4][HEAD_SEQ_GROUP];
@@ -1163,7 +1183,8 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
     const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)row * a.D);
 #pragma unroll
     for (int i = 0; i < MAXD64; ++i) {
-      float4 f = i < d64 ? e4[i * 16 + l16] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 f = e4[(EXACT || i < d64 ? i : d64 - 1) * 16 + l16];   // unconditional load
+      if (!EXACT && i >= d64) f = make_float4(0.f, 0.f, 0.f, 0.f);
       eD[r][4 * i] = (double)f.x;
       eD[r][4 * i + 1] = (double)f.y;
       eD[r][4 * i + 2] = (double)f.z;
@@ -1173,19 +1194,20 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
   for (int b0 = 0; b0 < a.batch; b0 += sg) {
     const int nb = min(sg, a.batch - b0);
     __syncthreads();
-    {   // 16-byte loads, eight in flight per thread before the LDS stores
+    {   // 16-byte loads, all of a group's (18 per thread at D 576) in flight before the LDS stores
       const double2 *src = reinterpret_cast<const double2 *>(a.hn + (long long)b0 * a.D);
       double2 *dst = reinterpret_cast<double2 *>(hs);
       const int n2 = nb * a.D / 2;
-      for (int p0 = tid; p0 < n2; p0 += 8 * 256) {
-        double2 v[8];
+      constexpr int U = 18;
+      for (int p0 = tid; p0 < n2; p0 += U * 256) {
+        double2 v[U];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < U; ++k) {
           const int p = p0 + k * 256;
           v[k] = src[p < n2 ? p : n2 - 1];
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < U; ++k) {
           const int p = p0 + k * 256;
           if (p < n2) dst[p] = v[k];
         }
@@ -1199,7 +1221,7 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
       for (int r = 0; r < R; ++r) acc[r] = 0.0;
 #pragma unroll
       for (int i = 0; i < MAXD64; ++i) {
-        if (i < d64) {
+        if (EXACT || i < d64) {
           const double2 h01 = *reinterpret_cast<const double2 *>(hp + 64 * i);
           const double2 h23 = *reinterpret_cast<const double2 *>(hp + 64 * i + 2);
 #pragma unroll
@@ -1490,9 +1512,11 @@ int head_workgroups(int vocab, int D, int rows_single, int batch) {
 
 int prepare_head_kernels(int D) {
   const int sh = head_seq_group(D) * D * 8;
-  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<9, 2>),
+  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<9, 2, true>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, sh));
-  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<27, 1>),
+  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<9, 2, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, sh));
+  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<27, 1, false>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, sh));
   return BFP_OK;
 }
@@ -1500,7 +1524,12 @@ int prepare_head_kernels(int D) {
 int launch_head(const HeadArgs &a, hipStream_t s) {
   size_t sh = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8;
   if (a.batch == 1) {
-    hipLaunchKernelGGL(k_head_logits, dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
+    if (a.D == 576)
+      hipLaunchKernelGGL((k_head_logits<9, true>), dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
+    else if (a.D < 576)
+      hipLaunchKernelGGL((k_head_logits<9, false>), dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
+    else
+      hipLaunchKernelGGL((k_head_logits<27, false>), dim3(a.n_wg, a.batch), dim3(256), sh, s, a);
     return launch_status("head");
   }
   if (!a.hn) return set_err(BFP_EINVAL, "head: no normed-hidden buffer for batch %d", a.batch);
@@ -1509,10 +1538,12 @@ int launch_head(const HeadArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
   const int sg = head_seq_group(a.D);
   const size_t shg = (size_t)sg * a.D * 8;
-  if (a.D <= 576)
-    hipLaunchKernelGGL((k_head_gemv<9, 2>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
+  if (a.D == 576)
+    hipLaunchKernelGGL((k_head_gemv<9, 2, true>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
+  else if (a.D < 576)
+    hipLaunchKernelGGL((k_head_gemv<9, 2, false>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
   else
-    hipLaunchKernelGGL((k_head_gemv<27, 1>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
+    hipLaunchKernelGGL((k_head_gemv<27, 1, false>), dim3(a.n_wg), dim3(256), shg, s, a, sg);
   return launch_status("head");
 }
 
