@@ -154,6 +154,27 @@ def test_decode_long_context(gpu):
     gm.close()
 
 
+def test_decode_long_context_full_width(gpu):
+    """The long-context attention form (capacity above 512: four workgroups
+    per head, one 16-dimension tile each) at SmolLM2's width -- 9 heads in 3
+    KV groups -- for two sequences at once: every layer output at every step
+    to position 519 against the oracle."""
+    cfg = dict(D=576, H_Q=9, H_KV=3, HD=64, FFN=1536, NL=1, MAX_CTX=520, VOCAB=512)
+    d, om, gm = _setup(cfg, seed=15, max_batch=2)
+    from bfp import synth
+    prompts = np.stack([synth.make_prompt(d, 10, seed=15 + b) for b in range(2)])
+    n_gen = d.MAX_CTX - 10
+    print("[decode] long context, full width: gpu", flush=True)
+    toks, (hm, he) = gm.decode(prompts, n_gen, hist=True)
+    for b in range(2):
+        print(f"[decode] long context, full width: oracle seq {b}", flush=True)
+        want, whm, whe = _oracle_decode(om, prompts[b], n_gen)
+        bad = [s for s in range(d.MAX_CTX) if not ((hm[b, s] == whm[s]).all() and (he[b, s] == whe[s]).all())]
+        assert not bad, f"seq {b}: steps with differing layer outputs: {bad[:10]}"
+        assert list(toks[b]) == list(want)
+    gm.close()
+
+
 @pytest.mark.parametrize("max_ctx", [200, 300], ids=["lane-split-256", "per-thread-512"])
 def test_decode_mid_context(gpu, max_ctx):
     """Context capacities of 129..256 (scores spread over 32-lane half-waves)

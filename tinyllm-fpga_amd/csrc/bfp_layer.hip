@@ -279,43 +279,52 @@ __device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
   return quantize16_lanes(out, e);
 }
 
-// Attention of one q head (full.py:268-283) in one workgroup of ATT_WAVES
+// Attention of one q head (full.py:268-283) in workgroups of ATT_WAVES
 // waves:
-//  1. waves 0-2: RoPE of q (head hq) and k (group g), v of group g; the
-//     writer workgroup of the group stores k, v at slot pos of the KV cache;
-//  2. all threads: scores[t] = np.dot(q, K[t]) / sqrt(HD), one position per
-//     thread, in OpenBLAS's SkylakeX ddot order;
+//  1. waves 0-2: RoPE of q (head hq) and k (group g), v of group g; one
+//     workgroup of the group stores k, v at slot pos of the KV cache;
+//  2. all threads: scores[t] = np.dot(q, K[t]) / sqrt(HD), in OpenBLAS's
+//     SkylakeX ddot order;
 //  3. softmax: exp(s - max) / pairwise_sum (numpy's order);
 //  4. attn = sum_t p[t] * V[t] in ascending t from 0.0 (numpy's
-//     `attn[h] += p[t] * V[t]` loop, full.py:280-281).  V rows are staged
-//     through LDS in chunks of AVC rows by every thread (16-byte loads, the
-//     next chunk's loads in flight while the current one is used); wave 0
-//     forms each product and runs the (inherently sequential) add chain, one
-//     dimension per lane, straight from LDS.
+//     `attn[h] += p[t] * V[t]` loop, full.py:280-281), one add chain per
+//     dimension.
+// Short contexts (at most 64 * ATT_WAVES positions): one workgroup per
+// head.  V rows are staged through LDS in chunks of AVC rows by every
+// thread (16-byte loads, the next chunk's loads in flight while the current
+// one is used); wave 0 forms each product and runs the chains, one
+// dimension per lane, straight from LDS.
+// Long contexts: ATT_DSPLIT workgroups per head, workgroup dg owning the
+// 16 dimensions (one output tile) 16dg .. 16dg+15.  Each computes the whole
+// score vector and softmax (the chip has far more CUs than heads) and the
+// AV chains of its own tile only, so the LDS traffic of the products is a
+// quarter of a whole head's.
 constexpr int ATT_WAVES = 8;
 
 // V rows per staged chunk of the AV phase (short contexts).
 constexpr int ATT_AVC = 128;
 
-// The AV phase at long context (PPW 8) instead has waves 1.. form the
-// products of blocks of TB = 14*PPW positions into an LDS double buffer
-// while wave 0 adds the previous block; V is prefetched PPW blocks ahead.
-// A position's 64 products sit in a row of 64 doubles as 32 16-byte
-// chunks; the pair of dimensions 8c + 2i, +1 is chunk
-// (4c + (i ^ (c >> 1))) ^ ((tt >> 1) & 1) of row tt.  With producer lane l
-// holding dimensions 8c..8c+7 (c = l % 8) of rows att_lane_row(l / 8) + 8r
-// (plus the wave's base, a multiple of 16), the
-// 16 lanes of each write instruction (pair i of every lane) hit 16
-// distinct 16-byte bank groups, and the 32 lanes of each of wave 0's reads
-// (one dimension per lane) a contiguous 256 bytes.  Rows t and t+1 (t even)
-// share the swizzle, so one ds_read2st64 serves both.  (Dimension order
-// would put a write's lanes 64 bytes apart: a 4-way bank conflict.)
-__device__ __forceinline__ int att_lane_row(int g) { return ((g & 1) << 1) | ((g >> 1) & 1) | (g & 4); }
-__device__ __forceinline__ int att_chunk(int c, int i, int x) { return (4 * c + (i ^ (c >> 1))) ^ x; }
+// Long contexts: workgroups per head, and the AV phase's geometry.  Waves
+// 1 .. AVL_PW form the products of blocks of AVL_TB positions into an LDS
+// double buffer while lanes 0-15 of wave 0 add the previous block, V
+// prefetched AVL_DEPTH blocks ahead.  Producer lane l holds dimensions
+// 8(l/32) .. +7 of the tile for rows 2(l%32) and 2(l%32)+1 of its wave's
+// 64 (one 16-byte load per row); products are stored dimension-major,
+// AVL_TBP doubles per dimension, so each write is a 16-byte pair of rows
+// and the 32 lanes of a half-wave write 512 contiguous bytes, and the
+// chain lane of dimension d reads two positions per 16-byte load at
+// d*AVL_TBP: the padding of 2 puts the 16 lanes in 16 distinct bank
+// groups.
+constexpr int ATT_DSPLIT = 4;
+constexpr int AVL_PW = 3;
+constexpr int AVL_TB = AVL_PW * 64;
+constexpr int AVL_TBP = AVL_TB + 2;
+constexpr int AVL_DEPTH = 4;
+constexpr int AVL_G = 8;        // chain: positions per group of LDS reads
+constexpr int AVL_AHEAD = 3;    // chain: groups of reads in flight ahead of the adds
 size_t attn_lds_bytes(int max_ctx, int ppw) {
   const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
-  const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4)
-                             : (size_t)(ATT_WAVES - 1) * 2 * ppw * 64 * 8 * 2;
+  const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4) : (size_t)2 * 16 * AVL_TBP * 8;
   return (256 + sc_len) * 8 + av;
 }
 
@@ -339,9 +348,9 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   constexpr int NT = 64 * ATT_WAVES;
   constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
   constexpr int VL = AVC * 8 / NT;             // 16-byte V loads per thread and chunk
-  constexpr int TB = (ATT_WAVES - 1) * 2 * PPW;  // positions per AV block (long)
-  constexpr int ATT_DEPTH = PPW;                 // V blocks in flight (long)
-  static_assert(SHORT || PPW == 8, "the long AV path maps 8 positions x 8 dimension groups to a wave");
+  constexpr int TB = AVL_TB;                   // positions per AV block (long)
+  static_assert(SHORT || PPW == 8, "the long form is instantiated as PPW 8");
+  static_assert(AVL_PW + 1 <= ATT_WAVES && AVL_TB % 8 == 0 && AVL_TBP % 2 == 0, "long AV geometry");
   extern __shared__ double dsm[];
   double *q = dsm;                  // 64
   double *kc = dsm + 64;            // 64 (current position, post-rope)
@@ -349,12 +358,14 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   double *leaf = dsm + 192;         // PW_MAX_LEAVES (= 64)
   double *sc = dsm + 256;           // max_ctx, rounded up to even
   // short: staged V, 2 x AVC x 64 mantissas and 2 x AVC x 4 exponents;
-  // long: product double buffer, 2 x TB rows of 64 doubles
+  // long: product double buffer, 2 x 16 dimensions x AVL_TBP doubles
   int16_t *vsm = reinterpret_cast<int16_t *>(sc + ((a.max_ctx + 1) & ~1));
   int8_t *vse = reinterpret_cast<int8_t *>(vsm + 2 * AVC * 64);
   double *buf = sc + ((a.max_ctx + 1) & ~1);
   __shared__ double red[ATT_WAVES];
-  const int hq = blockIdx.x, b = blockIdx.y;
+  const int hq = SHORT ? blockIdx.x : blockIdx.x / ATT_DSPLIT, b = blockIdx.y;
+  const int dg = SHORT ? 0 : blockIdx.x % ATT_DSPLIT;   // long: the tile of dimensions 16dg ..
+  const bool lead = dg == 0;                             // stores the cache row and the dumps
   const int grp = a.H_Q / a.H_KV, g = hq / grp;
   const int HD = 64;
   const int pos = cur_pos(a);
@@ -369,7 +380,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   int8_t *Ke = a.k_e + (long long)b * a.max_ctx * (kv_tok / 16);
   int16_t *Vm = a.v_m + (long long)b * a.max_ctx * kv_tok;
   int8_t *Ve = a.v_e + (long long)b * a.max_ctx * (kv_tok / 16);
-  const bool writer = (hq % grp) == 0;
+  const bool writer = (hq % grp) == 0 && lead;
 
   // AV staging: chunk c holds rows c*AVC .. c*AVC+AVC-1 (clamped to n-1, so
   // no load sits in a branch); thread tid loads 16-byte part tid%8 of rows
@@ -399,33 +410,36 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     if (tid < AVC) *reinterpret_cast<int *>(vse + ((c) & 1) * AVC * 4 + tid * 4) = ver; \
   }
 
-  // Long contexts: V prefetch ring of the AV phase (filled after the scores).  Producer
-  // wave pw + 1 owns rows pw*2*PPW + 8r + pp (r = 0, 1) of block k,
-  // positions k*TB + row; lane (pp = att_lane_row(l/8), c = l%8) holds
-  // dimensions 8c..8c+7 of both its positions: one 16-byte mantissa load
-  // and one exponent byte per row and block.  Two independent rows per lane
-  // halve the barriers per position and give the product arithmetic ILP.
-  // Every wave issues the same loads on every path (positions past the end
-  // are clamped to a valid row and their products zeroed; wave 0 loads a
-  // copy it does not use), so the compiler can count ATT_DEPTH blocks of
-  // loads in flight instead of draining them.
-  const bool producer = w >= 1;
-  const int pw = producer ? w - 1 : 0, pp = att_lane_row(l >> 3), pc = l & 7;
-  uint4 rm[SHORT ? 1 : ATT_DEPTH][2];
-  int re[SHORT ? 1 : ATT_DEPTH][2];
+  // Long contexts: V prefetch ring of the AV phase (filled after the
+  // scores).  Producer wave pw + 1 owns rows tt0 = 64pw + 2(l%32) and
+  // tt0 + 1 of block k (positions k*TB + row); lane l holds dimensions
+  // 16dg + 8(l/32) .. +7 of both rows: one 16-byte mantissa load and one
+  // exponent byte per row and block.  Every wave issues the same loads on
+  // every path (positions past the end are clamped to a valid row and their
+  // products zeroed; the other waves load a copy they do not use), so the
+  // compiler can count AVL_DEPTH blocks of loads in flight instead of
+  // draining them.
+  const bool producer = w >= 1 && w <= AVL_PW;
+  const int pw = producer ? w - 1 : 0, hh = l >> 5;
+  const int tt0 = 64 * pw + 2 * (l & 31);
+  uint4 rm[SHORT ? 1 : AVL_DEPTH][2];
+  int re[SHORT ? 1 : AVL_DEPTH][2];
   auto load_blk = [&](int k, uint4 (&m)[2], int (&e)[2]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      int t = k * TB + pw * 2 * PPW + 8 * r + pp;
+      int t = k * TB + tt0 + r;
       t = t < n ? t : n - 1;
-      const long long o = ((long long)t * a.H_KV + g) * HD + 8 * pc;
+      const long long o = ((long long)t * a.H_KV + g) * HD + 16 * dg + 8 * hh;
       m[r] = *reinterpret_cast<const uint4 *>(Vm + o);
       e[r] = Ve[o >> 4];
     }
   };
 
   // the first K row of this thread's scores, in flight during the RoPE phase
-  KRow ra, rb;
+  // (long contexts: KR rows per thread in flight, the first since the RoPE
+  // phase, so a pass over 64 * ATT_WAVES * KR positions waits for memory once)
+  constexpr int KR = SHORT ? 1 : 2;
+  KRow kr[KR];
   // contexts of at most 128 (PPW 2) or 256 (PPW 3) positions: each 32-lane
   // half-wave scores one position, lane j (of 32) holding elements j and
   // 32 + j of its K row; all LS_PASS passes' elements are in flight during
@@ -445,7 +459,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
       lse[ps_][1] = Ke[(o + 32) >> 4];
     }
   } else {
-    load_krow(ra, Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
+    load_krow(kr[0], Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
   }
 
   if (w == 0) {            // q head hq
@@ -453,7 +467,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     int e;
     int m = rope_lane(bfp_val(qm[idx], qe[idx >> 4]), cs, e);
     q[l] = bfp_val(m, e);
-    if (a.dump) {
+    if (a.dump && lead) {
       int cm, ce;
       canon_copy(m, e, cm, ce);
       a.dump->m[ST_Q][b * a.dump->mstride[ST_Q] + idx] = (int16_t)cm;
@@ -520,17 +534,28 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   } else if constexpr (SHORT) {
     // contexts of at most NT positions: one row per thread, the one in
     // flight since the RoPE phase
-    if (tid < n) sc[tid] = ddot64_skx_bfp(q, ra.m, ra.e4) / a.inv_sqrt_hd_div;
+    if (tid < n) sc[tid] = ddot64_skx_bfp(q, kr[0].m, kr[0].e4) / a.inv_sqrt_hd_div;
     if (tid == pos) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
   } else {
+    // passes of KR rows per thread: rows t0 + tid + j*NT; kr[0] of the next
+    // pass is loaded as soon as this pass's kr[0] is consumed
     const int last = n - 1;
-    for (int t = tid; t < n; t += 2 * NT) {
-      const int t1 = t + NT, t2 = t + 2 * NT;
-      load_krow(rb, Km, Ke, ((long long)(t1 < n ? t1 : last) * a.H_KV + g) * HD);
-      sc[t] = ddot64_skx_bfp(q, ra.m, ra.e4) / a.inv_sqrt_hd_div;
-      load_krow(ra, Km, Ke, ((long long)(t2 < n ? t2 : last) * a.H_KV + g) * HD);
-      const double s1 = ddot64_skx_bfp(q, rb.m, rb.e4) / a.inv_sqrt_hd_div;
-      if (t1 < n) sc[t1] = s1;
+    for (int t0 = 0; t0 < n; t0 += KR * NT) {
+#pragma unroll
+      for (int j = 1; j < KR; ++j) {
+        const int t = t0 + tid + j * NT;
+        load_krow(kr[j], Km, Ke, ((long long)(t < n ? t : last) * a.H_KV + g) * HD);
+      }
+#pragma unroll
+      for (int j = 0; j < KR; ++j) {
+        const int t = t0 + tid + j * NT;
+        const double sj = ddot64_skx_bfp(q, kr[j].m, kr[j].e4) / a.inv_sqrt_hd_div;
+        if (j == 0) {
+          const int tn = t + KR * NT;
+          load_krow(kr[0], Km, Ke, ((long long)(tn < n ? tn : last) * a.H_KV + g) * HD);
+        }
+        if (t < n) sc[t] = sj;
+      }
     }
     if (tid == pos % NT) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
   }
@@ -538,7 +563,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     BFP_ATT_STORE_V(0)
   } else {
 #pragma unroll
-    for (int d = 0; d < ATT_DEPTH; ++d) load_blk(d, rm[d], re[d]);   // overlaps the softmax
+    for (int d = 0; d < AVL_DEPTH; ++d) load_blk(d, rm[d], re[d]);   // overlaps the softmax
   }
   __syncthreads();
   // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
@@ -598,13 +623,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
       __syncthreads();
     }
   } else {
-    // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281).
-    // Iteration k: the producers write the products of block k into buf[k & 1]
-    // (row tt, chunks swizzled by att_chunk) and refill their ring slot
-    // with block k + ATT_DEPTH; wave 0 adds block k-1 from buf[(k-1) & 1],
-    // one dimension per lane.  The blocks cover positions 0 .. pos-1; row
-    // pos is this launch's V (vc, its writer workgroup may not have stored
-    // it yet) and is added last.
+    // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281),
+    // for the tile's 16 dimensions.  Iteration k: the producers write the
+    // products of block k into buf[k & 1] and refill their ring slot with
+    // block k + AVL_DEPTH; lanes 0-15 of wave 0 add block k-1 from
+    // buf[(k-1) & 1], one dimension per lane.  The blocks cover positions
+    // 0 .. pos-1; row pos is this launch's V (vc, its writer workgroup may
+    // not have stored it yet) and is added last.
     //
     // Product: p * (m * 2^(e-15)) is one rounding of the exact real
     // p*m*2^(e-15); so is ps * m with ps = p * 2^(e-15) whenever ps is exact,
@@ -612,14 +637,12 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     // below the normal range forms p * (m * 2^(e-15)) instead.  Positions
     // >= pos get ps = 0: adding +-0 leaves acc (never -0) unchanged.
     const int nb = (pos + TB - 1) / TB;
-    const int tt0 = pw * 2 * PPW + pp;     // this producer lane's rows in a block: tt0, tt0 + 8
-    const int xs = (pp >> 1) & 1;          // their chunk swizzle ((row >> 1) & 1)
     double pt_nx[2];                       // p of the next block's rows, read a block ahead
 #pragma unroll
-    for (int r = 0; r < 2; ++r) pt_nx[r] = sc[tt0 + 8 * r < pos ? tt0 + 8 * r : 0];
-    for (int k0 = 0; k0 <= nb; k0 += ATT_DEPTH) {
+    for (int r = 0; r < 2; ++r) pt_nx[r] = sc[tt0 + r < pos ? tt0 + r : 0];
+    for (int k0 = 0; k0 <= nb; k0 += AVL_DEPTH) {
 #pragma unroll
-      for (int d = 0; d < ATT_DEPTH; ++d) {
+      for (int d = 0; d < AVL_DEPTH; ++d) {
         const int k = k0 + d;
         if (k <= nb) {                      // uniform: k0, d and nb are
           if (producer) {
@@ -627,7 +650,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
             double pt[2], s[2], ps[2];
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-              const int t = k * TB + tt0 + 8 * r;
+              const int t = k * TB + tt0 + r;
               live[r] = t < pos;
               pt[r] = pt_nx[r];
               pt_nx[r] = sc[t + TB < pos ? t + TB : 0];
@@ -655,61 +678,63 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
                 }
               }
             }
+            double *bp = buf + (k & 1) * 16 * AVL_TBP + 8 * hh * AVL_TBP + tt0;
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-              double2 *bp = reinterpret_cast<double2 *>(buf + (k & 1) * TB * 64 + (tt0 + 8 * r) * 64);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) bp[att_chunk(pc, i, xs)] = make_double2(pr[r][2 * i], pr[r][2 * i + 1]);
-            }
+            for (int i = 0; i < 8; ++i)
+              *reinterpret_cast<double2 *>(bp + i * AVL_TBP) = make_double2(pr[0][i], pr[1][i]);
           }
-          if (w == 0 && k >= 1) {
+          if (w == 0 && l < 16 && k >= 1) {
             // block k-1 in full: its rows past pos - 1 hold products of +-0.
-            // Dimension l of row i is at lb[o[(i >> 1) & 1] + 64 i].
-            const double *lb = buf + ((k - 1) & 1) * TB * 64 + (l & 1);
-            const int o0 = 2 * att_chunk(l >> 3, (l >> 1) & 3, 0), o1 = 2 * att_chunk(l >> 3, (l >> 1) & 3, 1);
-            // groups of AV_G products; the reads of the next two groups are
-            // in flight while a group is added (LDS latency is about 8
-            // dependent adds).  The scheduling barriers keep that shape:
-            // left alone the compiler sinks the reads toward their adds and
-            // the chain waits on each one.
-            constexpr int AV_G = 8, NG = TB / AV_G;
-            static_assert(TB % AV_G == 0 && AV_G % 4 == 0, "AV groups");
-            double v[3][AV_G];
+            // Groups of AV_G products; the reads of the next AV_AHEAD groups
+            // are in flight while a group is added.  The scheduling barriers
+            // keep that shape: left alone the compiler sinks the reads
+            // toward their adds and the chain waits on each one.
+            const double2 *lb =
+                reinterpret_cast<const double2 *>(buf + ((k - 1) & 1) * 16 * AVL_TBP + l * AVL_TBP);
+            constexpr int AV_G = AVL_G, AV_AHEAD = AVL_AHEAD, RING = AV_AHEAD + 1, NG = TB / AV_G;
+            static_assert(TB % AV_G == 0 && AV_G % 2 == 0 && AV_AHEAD * AV_G / 2 <= 15, "AV read groups");
+            double2 v[RING][AV_G / 2];
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < AV_AHEAD; ++q)
 #pragma unroll
-              for (int i = 0; i < AV_G; ++i) v[q][i] = lb[((i >> 1) & 1 ? o1 : o0) + (q * AV_G + i) * 64];
+              for (int i = 0; i < AV_G / 2; ++i) v[q][i] = lb[q * AV_G / 2 + i];
 #pragma unroll
             for (int gq = 0; gq < NG; ++gq) {
-              if (gq + 2 < NG) {
+              if (gq + AV_AHEAD < NG) {
 #pragma unroll
-                for (int i = 0; i < AV_G; ++i)
-                  v[(gq + 2) % 3][i] = lb[((i >> 1) & 1 ? o1 : o0) + ((gq + 2) * AV_G + i) * 64];
+                for (int i = 0; i < AV_G / 2; ++i)
+                  v[(gq + AV_AHEAD) % RING][i] = lb[(gq + AV_AHEAD) * AV_G / 2 + i];
               }
               __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-              for (int i = 0; i < AV_G; ++i) acc = acc + v[gq % 3][i];
+              for (int i = 0; i < AV_G / 2; ++i) {
+                acc = acc + v[gq % RING][i].x;
+                acc = acc + v[gq % RING][i].y;
+              }
               __builtin_amdgcn_sched_barrier(0);
             }
           }
         }
         // outside the branch: a load in a branch makes the compiler drain
         // every outstanding load there
-        load_blk(k + ATT_DEPTH, rm[d], re[d]);
+        load_blk(k + AVL_DEPTH, rm[d], re[d]);
         if (k <= nb) __syncthreads();
       }
     }
-    if (w == 0) acc = acc + sc[pos] * vc[l];
+    if (w == 0) acc = acc + sc[pos] * vc[16 * dg + (l & 15)];
   }
 #undef BFP_ATT_LOAD_V
 #undef BFP_ATT_STORE_V
   if (w == 0) {
+    // lanes 0-15 of the long form hold its tile; all 64 lanes take part
     int e;
     int m = quantize16_lanes(acc, e, true);   // tile_quantize(fp_quantize_vec(attn))
-    int idx = hq * HD + l;
-    a.att_m[b * a.D + idx] = (int16_t)m;
-    if ((l & 15) == 0) a.att_e[b * (a.D / 16) + (idx >> 4)] = (int8_t)e;
-    if (a.dump) {
+    const int idx = hq * HD + (SHORT ? l : 16 * dg + l);
+    if (SHORT || l < 16) {
+      a.att_m[b * a.D + idx] = (int16_t)m;
+      if ((l & 15) == 0) a.att_e[b * (a.D / 16) + (idx >> 4)] = (int8_t)e;
+    }
+    if (a.dump && (SHORT || l < 16)) {
       a.dump->m[ST_ATTN][b * a.dump->mstride[ST_ATTN] + idx] = (int16_t)m;
       if ((l & 15) == 0)
         a.dump->e[ST_ATTN][b * (a.dump->mstride[ST_ATTN] / 16) + (idx >> 4)] = (int8_t)e;
@@ -1419,7 +1444,9 @@ int prepare_layer_kernels(int max_ctx, int D, int FFN) {
 
 static int launch_attn(const LayerArgs &a, hipStream_t s) {
   const int ppw = attn_ppw(a.max_ctx);
-  hipLaunchKernelGGL(attn_kernel(ppw), dim3(a.H_Q, a.batch), dim3(64 * ATT_WAVES),
+  // long contexts: ATT_DSPLIT workgroups per head, one 16-dimension tile each
+  const int split = ppw == 8 ? ATT_DSPLIT : 1;
+  hipLaunchKernelGGL(attn_kernel(ppw), dim3(a.H_Q * split, a.batch), dim3(64 * ATT_WAVES),
                      attn_lds_bytes(a.max_ctx, ppw), s, a);
   return BFP_OK;
 }
