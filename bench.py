@@ -363,20 +363,74 @@ def layer_leg():
             "layer_step_us": round(us, 2), "steps_per_s": round(1e6 / us, 1)}
 
 
-def cpu_decode_baseline(max_steps=3):
-    """The oracle's faithful decode loop (full.py:432-443 restated), timed
-    on the first max_steps steps of config 3 on this host (1 thread)."""
+_ORACLE = {}
+
+
+def _oracle_model():
+    """The oracle's model of the bench's 30-layer synthetic weights (built once)."""
+    if "m" not in _ORACLE:
+        from oracle import bfp_sim as sim
+        from bfp import Dims, synth
+        _ORACLE["m"] = sim.build_model(synth.make_model(Dims(MAX_CTX=2048), seed=0))
+    return _ORACLE["m"]
+
+
+def cpu_decode_baseline():
+    """Config 3 on the oracle: the step time at position 36, the mean
+    position of its 72 steps (the per-position attention loops make the
+    step time grow with the position)."""
+    t36 = _cpu_step_seconds(36)
+    return {"value": round(1.0 / t36, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/bfp_sim.fwd_layer x 30 + head_argmax, one step at position 36 "
+                      f"({t36:.2f} s) over a synthetic KV cache"}
+
+
+def _cpu_step_seconds(pos, reps=2):
+    """One decode step of the oracle (30 fwd_layer calls + the head) at
+    position pos over a synthetic KV cache of pos + 1 rows per layer (its
+    values do not change the work: the per-position loops run pos + 1
+    times whatever they hold); the best of reps, 1 thread."""
+    import numpy as np
     from oracle import bfp_sim as sim
-    from bfp import Dims, synth
-    d = Dims(MAX_CTX=72)
-    om = sim.build_model(synth.make_model(d, seed=0))
-    prompt = [int(t) for t in synth.make_prompt(d, 8, seed=0)]
-    t0 = time.perf_counter()
-    sim.decode(om, prompt[:max_steps], 0, max_ctx=72)
-    dt = time.perf_counter() - t0
-    return {"value": round(max_steps / dt, 4), "unit": "steps/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/bfp_sim.decode, first {max_steps} steps of config 3 "
-                      f"(30 layers) in {dt:.1f} s"}
+    om = _oracle_model()
+    d = om.dims
+    rng = np.random.default_rng(pos)
+    kv = [{"k": rng.standard_normal((pos + 1, d.H_KV, d.HD)),
+           "v": rng.standard_normal((pos + 1, d.H_KV, d.HD))} for _ in range(d.NL)]
+    best = None
+    for _ in range(reps):
+        h = om.embed_row_q(1)
+        t0 = time.perf_counter()
+        for li in range(d.NL):
+            h = sim.fwd_layer(h, om.layers[li], pos=pos, kv=kv[li], kv_pos=pos, dims=d)
+        sim.head_argmax(h, om.norm_w_q, om.embed)
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    return best
+
+
+def cpu_long_context_baseline():
+    """Config 4 on the oracle: step time at positions 48 and 2000 (the
+    per-position attention loops make it linear in the position), the mean
+    over positions 48..2047 interpolated linearly from the two."""
+    t48, t2000 = _cpu_step_seconds(48), _cpu_step_seconds(2000)
+    mean = t48 + (t2000 - t48) * ((48 + 2047) / 2 - 48) / (2000 - 48)
+    return {"value": round(1.0 / mean, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "by_position": {"pos_48": round(1.0 / t48, 4), "pos_2000": round(1.0 / t2000, 4)},
+            "sample": f"oracle/bfp_sim.fwd_layer x 30 + head_argmax, one step at position 48 "
+                      f"({t48:.2f} s) and at 2000 ({t2000:.2f} s) over a synthetic KV cache; "
+                      f"mean over 48..2047 by linear interpolation"}
+
+
+def cpu_batch_baseline():
+    """Config 5 on the oracle, which decodes one sequence at a time: the
+    step time at position 72 (the mean position of 8 + 128 steps) is the
+    time per token."""
+    t72 = _cpu_step_seconds(72)
+    return {"value": round(1.0 / t72, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/bfp_sim.fwd_layer x 30 + head_argmax, one sequence's step at "
+                      f"position 72 ({t72:.2f} s); the oracle has no batched form, so 64 "
+                      f"sequences take 64 such steps"}
 
 
 def stream_probe():
@@ -522,6 +576,10 @@ def main():
         out["cpu_baseline_all_cores"] = cpu_baseline_all_cores(8.0, workers)
         if not args.no_decode:
             out["decode"]["cpu_baseline"] = cpu_decode_baseline()
+            if args.long:
+                out["long_context"]["cpu_baseline"] = cpu_long_context_baseline()
+            if args.batch64:
+                out["batch64"]["cpu_baseline"] = cpu_batch_baseline()
     print(json.dumps(out), flush=True)
 
 
