@@ -342,9 +342,10 @@ __device__ __forceinline__ void load_krow(KRow &r, const int16_t *Km, const int8
 
 // SHORT: max_ctx <= 64 * ATT_WAVES, at most one score per thread (PPW 4) or
 // one per 32-lane half-wave (PPW 2: max_ctx <= 128, PPW 3: <= 256); fewer
-// registers, two workgroups per CU (many sequences at short context).
+// registers -- at most 80 for the lane-split forms, so three workgroups fit
+// a CU, two for PPW 4 -- for many sequences at short context.
 template <int PPW, bool SHORT>
-__global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerArgs a) {
+__global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? (PPW == 4 ? 4 : 6) : 2)) void k_attn(LayerArgs a) {
   constexpr int NT = 64 * ATT_WAVES;
   constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
   constexpr int VL = AVC * 8 / NT;             // 16-byte V loads per thread and chunk
@@ -442,15 +443,19 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
   KRow kr[KR];
   // contexts of at most 128 (PPW 2) or 256 (PPW 3) positions: each 32-lane
   // half-wave scores one position, lane j (of 32) holding elements j and
-  // 32 + j of its K row; all LS_PASS passes' elements are in flight during
-  // the RoPE phase
+  // 32 + j of its K row, in passes of 2*ATT_WAVES positions.  The elements
+  // of LS_PRE passes (128 positions) are in registers at once: the first
+  // group's are in flight during the RoPE phase, a second group's (PPW 3,
+  // more than 128 positions) are loaded after the first is scored.  (Eight
+  // passes keep the PPW 3 form at 80 registers: three workgroups per CU.)
   constexpr bool LANE_SPLIT = SHORT && (PPW == 2 || PPW == 3);
   constexpr int LS_PASS = LANE_SPLIT ? (PPW == 2 ? 128 : 256) / (2 * ATT_WAVES) : 1;
-  int lsm[LS_PASS][2], lse[LS_PASS][2];
-  if constexpr (LANE_SPLIT) {
+  constexpr int LS_PRE = LS_PASS < 8 ? LS_PASS : 8;
+  int lsm[LS_PRE][2], lse[LS_PRE][2];
+  auto ls_load = [&](int g0) {   // passes g0 .. g0 + LS_PRE - 1
 #pragma unroll
-    for (int ps_ = 0; ps_ < LS_PASS; ++ps_) {
-      int t = 2 * ATT_WAVES * ps_ + 2 * w + (l >> 5);
+    for (int ps_ = 0; ps_ < LS_PRE; ++ps_) {
+      int t = 2 * ATT_WAVES * (g0 + ps_) + 2 * w + (l >> 5);
       t = t < n ? t : n - 1;
       const long long o = ((long long)t * a.H_KV + g) * HD + (l & 31);
       lsm[ps_][0] = Km[o];
@@ -458,6 +463,9 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
       lse[ps_][0] = Ke[o >> 4];
       lse[ps_][1] = Ke[(o + 32) >> 4];
     }
+  };
+  if constexpr (LANE_SPLIT) {
+    ls_load(0);
   } else {
     load_krow(kr[0], Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
   }
@@ -517,19 +525,22 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? 4 : 2)) void k_attn(LayerA
     const int j = l & 31;
     const double q0 = q[j], q1 = q[32 + j];
     const double k0 = kc[j], k1 = kc[32 + j];
+    for (int g0 = 0; g0 < LS_PASS && 2 * ATT_WAVES * g0 < n; g0 += LS_PRE) {   // uniform
+      if (g0 > 0) ls_load(g0);
 #pragma unroll
-    for (int ps_ = 0; ps_ < LS_PASS; ++ps_) {
-      if (2 * ATT_WAVES * ps_ >= n) break;   // uniform; every load was issued earlier
-      const int t = 2 * ATT_WAVES * ps_ + 2 * w + (l >> 5);
-      const double y0 = t == pos ? k0 : bfp_val(lsm[ps_][0], lse[ps_][0]);
-      const double y1 = t == pos ? k1 : bfp_val(lsm[ps_][1], lse[ps_][1]);
-      const double acc = fma(q1, y1, fma(q0, y0, 0.0));
-      const double f = acc + peer<4>(acc);
-      const double t01 = peer<16>(f + peer<8>(f));
-      const double sl = (t01 + peer<8>(f)) + f;
-      const double s2 = sl + peer<2>(sl);
-      const double tot = s2 + peer<1>(s2);
-      if (j == 31 && t < n) sc[t] = tot / a.inv_sqrt_hd_div;
+      for (int ps_ = 0; ps_ < LS_PRE; ++ps_) {
+        if (2 * ATT_WAVES * (g0 + ps_) >= n) break;   // uniform
+        const int t = 2 * ATT_WAVES * (g0 + ps_) + 2 * w + (l >> 5);
+        const double y0 = t == pos ? k0 : bfp_val(lsm[ps_][0], lse[ps_][0]);
+        const double y1 = t == pos ? k1 : bfp_val(lsm[ps_][1], lse[ps_][1]);
+        const double acc = fma(q1, y1, fma(q0, y0, 0.0));
+        const double f = acc + peer<4>(acc);
+        const double t01 = peer<16>(f + peer<8>(f));
+        const double sl = (t01 + peer<8>(f)) + f;
+        const double s2 = sl + peer<2>(sl);
+        const double tot = s2 + peer<1>(s2);
+        if (j == 31 && t < n) sc[t] = tot / a.inv_sqrt_hd_div;
+      }
     }
   } else if constexpr (SHORT) {
     // contexts of at most NT positions: one row per thread, the one in
