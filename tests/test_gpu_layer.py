@@ -12,6 +12,9 @@ pytestmark = pytest.mark.gpu
 SMALL = dict(D=64, H_Q=1, H_KV=1, HD=64, FFN=128, NL=1, MAX_CTX=16, VOCAB=256)
 MID = dict(D=192, H_Q=3, H_KV=1, HD=64, FFN=256, NL=1, MAX_CTX=16, VOCAB=256)
 FULL = dict(D=576, H_Q=9, H_KV=3, HD=64, FFN=1536, NL=1, MAX_CTX=16, VOCAB=256)
+# a KV capacity above 512: the long-context attention form (four workgroups
+# per head, each dumping its own 16-dimension tile of the attention output)
+FULL_LONG = dict(FULL, MAX_CTX=600)
 
 
 def _setup(cfg, seed, max_batch=1):
@@ -33,7 +36,7 @@ def _check_stages(stages, dump, b, pos, tag):
         assert (gm_[b] == wm.reshape(-1)).all(), f"{tag} pos {pos}: stage {name} mantissas differ"
 
 
-@pytest.mark.parametrize("cfg", [SMALL, MID, FULL], ids=["small", "mid", "full"])
+@pytest.mark.parametrize("cfg", [SMALL, MID, FULL, FULL_LONG], ids=["small", "mid", "full", "full-long"])
 def test_layer_8_positions(gpu, cfg):
     d, om, gm = _setup(cfg, seed=1)
     print(f"[layer] dims {cfg}", flush=True)
@@ -71,8 +74,10 @@ def test_layer_batched_sequences(gpu):
     gm.close()
 
 
-@pytest.mark.parametrize("cfg,batch", [(MID, 5), (FULL, 6), (MID, 9), (MID, 33), (FULL, 40)],
-                         ids=["mid-b5", "full-b6", "mfma-mid-b9", "mfma-mid-b33", "mfma-full-b40"])
+@pytest.mark.parametrize("cfg,batch", [(MID, 5), (FULL, 6), (MID, 9), (MID, 33), (FULL, 40),
+                                       (FULL_LONG, 9)],
+                         ids=["mid-b5", "full-b6", "mfma-mid-b9", "mfma-mid-b33", "mfma-full-b40",
+                              "mfma-full-long-b9"])
 def test_layer_multi_sequence_path(gpu, cfg, batch):
     """Batches of 4 or more run the multi-sequence kernels (separate norm,
     weight chunks reused across a group of sequences), from 8 on with the
