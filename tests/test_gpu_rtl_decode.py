@@ -57,6 +57,8 @@ def test_rtl_decode_matches_oracle(gpu):
     bad = [s for s in range(len(want)) if not ((hm[s] == want_h[s][0]).all() and (he[s] == want_h[s][1]).all())]
     assert not bad, f"steps with differing last-layer outputs: {bad[:10]}"
     assert list(preds) == list(want)
+    # the loop runs on the device from a fresh state each call; no history
+    assert list(gm.rtl_decode(prompt, n_gen)) == list(want)
     gm.close()
 
 

@@ -542,6 +542,7 @@ static RtlArgs rtl_args(bfp_ctx *c, int layer, int pos, int kv_pos) {
   a.freq = c->rtl_freq;
   a.pos = pos;
   a.kv_pos = kv_pos;
+  a.pos_ptr = nullptr;
   return a;
 }
 
@@ -649,22 +650,56 @@ int bfp_rtl_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, i
   BFP_TRY(rtl_tables_ready(c));
   RtlHeadArgs ha;
   BFP_TRY(rtl_head_ready(c, ha));
+  // The loop runs on the device: one step (embedding row, NL layers at the
+  // device step, the head, k_rtl_ctl) is captured as a graph and replayed
+  // `steps` times; predictions (and the history) are read back once.
+  DevBuf tmp;
+  int *dprompt, *dpreds;
+  BFP_TRY(tmp.alloc((void **)&dprompt, sizeof(int) * n_prompt));
+  BFP_TRY(tmp.alloc((void **)&dpreds, sizeof(int) * steps));
+  int16_t *dhm = nullptr;
+  int8_t *dhe = nullptr;
+  if (hist_m && hist_e) {
+    BFP_TRY(tmp.alloc((void **)&dhm, (size_t)steps * d.D * 2));
+    BFP_TRY(tmp.alloc((void **)&dhe, (size_t)steps * d.D / 16));
+  }
+  HIP_TRY(hipMemcpyAsync(dprompt, prompt, sizeof(int) * n_prompt, hipMemcpyHostToDevice, s));
+  const int st0[2] = {0, prompt[0]};
+  HIP_TRY(hipMemcpyAsync(c->state, st0, sizeof st0, hipMemcpyHostToDevice, s));
   const EmbedArgs ea{d.D, 1, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
-  for (int step = 0; step < steps; ++step) {
-    const int st[2] = {step, step < n_prompt ? prompt[step] : preds[step - 1]};
-    HIP_TRY(hipMemcpyAsync(c->state, st, sizeof st, hipMemcpyHostToDevice, s));
-    BFP_TRY(launch_embed(ea, s));
-    for (int l = 0; l < d.NL; ++l) BFP_TRY(launch_rtl_layer(rtl_args(c, l, step, step), s));
-    if (hist_m && hist_e) {
-      HIP_TRY(hipMemcpyAsync(hist_m + (size_t)step * d.D, c->h_m, (size_t)d.D * 2, hipMemcpyDeviceToHost, s));
-      HIP_TRY(hipMemcpyAsync(hist_e + (size_t)step * d.D / 16, c->h_e, (size_t)d.D / 16,
-                             hipMemcpyDeviceToHost, s));
-    }
-    BFP_TRY(launch_rtl_head(ha, s));
-    int tok = 0;
-    HIP_TRY(hipMemcpyAsync(&tok, c->rtl_tok, sizeof tok, hipMemcpyDeviceToHost, s));
-    HIP_TRY(hipStreamSynchronize(s));
-    preds[step] = tok;
+  const RtlCtlArgs ca{c->state, dprompt, n_prompt, dpreds, c->rtl_tok, c->h_m, c->h_e, dhm, dhe, d.D};
+  hipGraph_t gr = nullptr;
+  hipGraphExec_t ex = nullptr;
+  HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = launch_embed(ea, s);
+  for (int l = 0; l < d.NL && !rc; ++l) {
+    RtlArgs ra = rtl_args(c, l, 0, 0);
+    ra.pos_ptr = c->state;
+    rc = launch_rtl_layer(ra, s);
+  }
+  if (!rc) rc = launch_rtl_head(ha, s);
+  if (!rc) rc = launch_rtl_ctl(ca, s);
+  const hipError_t e1 = hipStreamEndCapture(s, &gr);
+  if (!rc && e1 != hipSuccess) rc = set_err(BFP_EIO, "graph capture: %s", hipGetErrorString(e1));
+  if (!rc) {
+    const hipError_t e2 = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+    if (e2 != hipSuccess) rc = set_err(BFP_EIO, "graph instantiate: %s", hipGetErrorString(e2));
+  }
+  for (int step = 0; step < steps && !rc; ++step) {
+    const hipError_t e = hipGraphLaunch(ex, s);
+    if (e != hipSuccess) rc = set_err(BFP_EIO, "graph launch: %s", hipGetErrorString(e));
+  }
+  if (!rc) {
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = set_err(BFP_EIO, "rtl decode: %s", hipGetErrorString(e));
+  }
+  if (ex) (void)hipGraphExecDestroy(ex);
+  if (gr) (void)hipGraphDestroy(gr);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpy(preds, dpreds, sizeof(int) * steps, hipMemcpyDeviceToHost));
+  if (dhm) {
+    HIP_TRY(hipMemcpy(hist_m, dhm, (size_t)steps * d.D * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(hist_e, dhe, (size_t)steps * d.D / 16, hipMemcpyDeviceToHost));
   }
   return BFP_OK;
 }

@@ -79,4 +79,6 @@ struct RtlArgs;
 int launch_rtl_layer(const RtlArgs &a, hipStream_t s);
 struct RtlHeadArgs;
 int launch_rtl_head(const RtlHeadArgs &a, hipStream_t s);
+struct RtlCtlArgs;
+int launch_rtl_ctl(const RtlCtlArgs &a, hipStream_t s);
 }  // namespace bfp

@@ -59,6 +59,19 @@ struct RtlArgs {
   const int16_t *silu_lut;    // SILU_LUT[65536], indexed by code & 0xFFFF
   const unsigned *freq;       // FREQ_TURNS_Q31[HD/2]
   int pos, kv_pos;            // RoPE position, KV slot (attention over 0..kv_pos)
+  const int *pos_ptr;         // device step counter; when set, pos = kv_pos = *pos_ptr
+};
+
+// The RTL token loop's per-step control (after the head): record the
+// prediction (and the last layer's output), then the next step's input.
+struct RtlCtlArgs {
+  int *state;                                // {step, token id}: the next step's input
+  const int *prompt; int n_prompt;           // device prompt ids
+  int *preds;                                // preds[step] = the head's token
+  const int *tok;                            // the head's token (device)
+  const int16_t *h_m; const int8_t *h_e;     // the last layer's output
+  int16_t *hist_m; int8_t *hist_e;           // optional per-step copies of it
+  int D;
 };
 
 // The FPGA decode head (smollm_decode_head_bfp.sv) on one sequence.

@@ -677,6 +677,10 @@ __global__ __launch_bounds__(64 * NW) void k_rl_mv(RtlArgs a, int op) {
 // RoPE of Q head h (h < H_Q) or K head h - H_Q, then the re-tile of its four
 // tiles (S_ROPEx_RQ_A/B); K heads also write the KV slot kv_pos with the
 // rotated K and the V head (S_KVWR_M/E).  One 64-thread workgroup per head.
+// The step of the RTL layer: a.pos / a.kv_pos, or the device step counter.
+__device__ __forceinline__ int rl_pos(const RtlArgs &a) { return a.pos_ptr ? *a.pos_ptr : a.pos; }
+__device__ __forceinline__ int rl_kv_pos(const RtlArgs &a) { return a.pos_ptr ? *a.pos_ptr : a.kv_pos; }
+
 __global__ __launch_bounds__(64) void k_rl_rope_kv(RtlArgs a) {
   const LayerArgs &L = a.L;
   const int h = blockIdx.x, j = threadIdx.x & 31, HD = 64;
@@ -685,7 +689,7 @@ __global__ __launch_bounds__(64) void k_rl_rope_kv(RtlArgs a) {
   const int off = is_k ? L.D + kh * HD : h * HD;   // element offset in qkv
   const int16_t *x = L.qkv_m + off;
   const int8_t *e = L.qkv_e + off / 16;
-  const long long ang = wrap31((wrap31((long long)a.pos * a.freq[j]) * PI_OVER_8_Q29) >> 29);
+  const long long ang = wrap31((wrap31((long long)rl_pos(a) * a.freq[j]) * PI_OVER_8_Q29) >> 29);
   int cs, sn;
   cordic(ang, cs, sn);
   const int xa = x[j], xb = x[j + 32];
@@ -720,7 +724,7 @@ __global__ __launch_bounds__(64) void k_rl_rope_kv(RtlArgs a) {
     st_pute(sd, st, so / 16 + ((j + 32) >> 4), emhi);
   }
   if (!is_k) return;
-  const size_t slot = (size_t)a.kv_pos * L.H_KV + kh;   // sequence 0
+  const size_t slot = (size_t)rl_kv_pos(a) * L.H_KV + kh;   // sequence 0
   int16_t *km = L.k_m + slot * HD;
   int8_t *ke = L.k_e + slot * (HD / 16);
   km[j] = (int16_t)qlo;
@@ -782,7 +786,7 @@ __global__ __launch_bounds__(RL_ATT_T) void k_rl_attn(RtlArgs a) {
   const LayerArgs &L = a.L;
   const int h = blockIdx.x, tid = threadIdx.x, HD = 64;
   const int g = (h * L.H_KV) / L.H_Q;
-  const int n = a.kv_pos + 1;
+  const int n = rl_kv_pos(a) + 1;
   int *xs = reinterpret_cast<int *>(rl_lds);   // n aligned scores, then LUT values
   int *se = xs + n;                             // n score exponents
   if (tid < 64) qs[tid] = L.qkv_m[h * HD + tid];
@@ -932,6 +936,26 @@ __global__ __launch_bounds__(64 * NW) void k_rl_head_mv(RtlHeadArgs a) {
   }
 }
 
+// One step of the FPGA driver's token loop on the device
+// (autoregress_bfp_top.sv:357-386): record the head's token as this step's
+// prediction (and the last layer's output when a history is kept), then the
+// next step's input -- prompt[step + 1] while the prompt lasts, else this
+// prediction -- and advance the step.  One 64-thread workgroup.
+__global__ __launch_bounds__(64) void k_rtl_ctl(RtlCtlArgs a) {
+  const int tid = threadIdx.x;
+  const int step = a.state[0], tok = *a.tok;
+  if (a.hist_m) {
+    for (int i = tid; i < a.D; i += 64) a.hist_m[(size_t)step * a.D + i] = a.h_m[i];
+    for (int i = tid; i < a.D / 16; i += 64) a.hist_e[(size_t)step * (a.D / 16) + i] = a.h_e[i];
+  }
+  __syncthreads();   // every thread has read the step before it changes
+  if (tid == 0) {
+    a.preds[step] = tok;
+    a.state[1] = step + 1 < a.n_prompt ? a.prompt[step + 1] : tok;
+    a.state[0] = step + 1;
+  }
+}
+
 }  // namespace rtl
 }  // namespace bfp
 
@@ -1065,23 +1089,30 @@ int rl_mv(const RtlArgs &a, int op, int nT, int n_wg, hipStream_t s) {
 int launch_rtl_layer(const RtlArgs &a, hipStream_t s) {
   const LayerArgs &L = a.L;
   const int ntD = L.D / 16, ntF = L.FFN / 16;
-  if (L.batch != 1 || L.HD != 64 || a.kv_pos < 0 || a.kv_pos >= L.max_ctx || a.pos < 0)
+  // with pos_ptr the caller keeps the device step inside the capacity
+  if (L.batch != 1 || L.HD != 64 ||
+      (!a.pos_ptr && (a.kv_pos < 0 || a.kv_pos >= L.max_ctx || a.pos < 0)))
     return set_err(BFP_EINVAL, "rtl layer: batch %d, HD %d, pos %d, kv_pos %d (capacity %d)",
                    L.batch, L.HD, a.pos, a.kv_pos, L.max_ctx);
+  const int n_att = a.pos_ptr ? L.max_ctx : a.kv_pos + 1;   // positions the attention's LDS holds
   const size_t lds_norm = (size_t)ntD * 9 + (size_t)L.D * 2;
   hipLaunchKernelGGL(rtl::k_rl_norm, dim3(1), dim3(64), lds_norm, s, a, 0);
   BFP_TRY(launch_status("rtl layer norm1"));
   BFP_TRY(rl_mv(a, 0, ntD, (L.D + 2 * L.KV) / 16, s));
   hipLaunchKernelGGL(rtl::k_rl_rope_kv, dim3(L.H_Q + L.H_KV), dim3(64), 0, s, a);
   BFP_TRY(launch_status("rtl layer rope"));
-  hipLaunchKernelGGL(rtl::k_rl_attn, dim3(L.H_Q), dim3(rtl::RL_ATT_T),
-                     (size_t)(a.kv_pos + 1) * 8, s, a);
+  hipLaunchKernelGGL(rtl::k_rl_attn, dim3(L.H_Q), dim3(rtl::RL_ATT_T), (size_t)n_att * 8, s, a);
   BFP_TRY(launch_status("rtl layer attention"));
   BFP_TRY(rl_mv(a, 1, ntD, ntD, s));
   hipLaunchKernelGGL(rtl::k_rl_norm, dim3(1), dim3(64), lds_norm, s, a, 1);
   BFP_TRY(launch_status("rtl layer norm2"));
   BFP_TRY(rl_mv(a, 2, ntD, ntF, s));
   return rl_mv(a, 3, ntF, ntD, s);
+}
+
+int launch_rtl_ctl(const RtlCtlArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(rtl::k_rtl_ctl, dim3(1), dim3(64), 0, s, a);
+  return launch_status("rtl loop control");
 }
 
 int launch_rtl_head(const RtlHeadArgs &a, hipStream_t s) {
