@@ -342,10 +342,11 @@ __device__ __forceinline__ void load_krow(KRow &r, const int16_t *Km, const int8
 
 // SHORT: max_ctx <= 64 * ATT_WAVES, at most one score per thread (PPW 4) or
 // one per 32-lane half-wave (PPW 2: max_ctx <= 128, PPW 3: <= 256); fewer
-// registers -- at most 80 for the lane-split forms, so three workgroups fit
-// a CU, two for PPW 4 -- for many sequences at short context.
+// registers -- at most 80 for PPW 3, so three workgroups fit a CU (many
+// sequences at short context), two for PPW 2 and 4 (PPW 2 at 80 registers
+// measured 1.6% slower at batch 1).
 template <int PPW, bool SHORT>
-__global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? (PPW == 4 ? 4 : 6) : 2)) void k_attn(LayerArgs a) {
+__global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? (PPW == 3 ? 6 : 4) : 2)) void k_attn(LayerArgs a) {
   constexpr int NT = 64 * ATT_WAVES;
   constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
   constexpr int VL = AVC * 8 / NT;             // 16-byte V loads per thread and chunk
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? (PPW == 4 ? 4 : 6) : 2)) v
   // of LS_PRE passes (128 positions) are in registers at once: the first
   // group's are in flight during the RoPE phase, a second group's (PPW 3,
   // more than 128 positions) are loaded after the first is scored.  (Eight
-  // passes keep the PPW 3 form at 80 registers: three workgroups per CU.)
+  // passes keep the PPW 3 form within 80 registers: three workgroups per CU.)
   constexpr bool LANE_SPLIT = SHORT && (PPW == 2 || PPW == 3);
   constexpr int LS_PASS = LANE_SPLIT ? (PPW == 2 ? 128 : 256) / (2 * ATT_WAVES) : 1;
   constexpr int LS_PRE = LS_PASS < 8 ? LS_PASS : 8;
