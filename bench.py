@@ -6,9 +6,10 @@
 Workload: the standalone BFP matvec sweep at
 batch 1 -- shapes 576x576, 192x576, 1536x576, 576x1536, 49152x576, 1000
 reps each.  One "step" is the whole sweep: one launch per shape computing
-1000 independent y = W x, each rep reading a distinct weight copy from a
-ring of >= 512 MiB so that the bytes come from HBM, not from the 256 MiB
-MALL.  Weights are N(0, 0.02) float32 quantised to BFP on the device,
+1000 independent y = W x, each rep reading a weight copy from a ring of
+>= 4 GiB (a distinct copy per rep for the four small shapes, 74 copies of
+the 49152x576 one, read in rep order), so the bytes come from HBM, not from
+the 256 MiB MALL.  Weights are N(0, 0.02) float32 quantised to BFP on the device,
 inputs N(0, 1) quantised to BFP; everything is resident in HBM before the
 timed region.  `value` is algorithmic bytes / second over the K timed steps
 (out*in*2 + out*in/16 weight bytes + x and y BFP bytes per rep).
@@ -33,7 +34,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 SHAPES = [(576, 576), (192, 576), (1536, 576), (576, 1536), (49152, 576)]
-RING_BYTES = 512 << 20
+RING_BYTES = 4096 << 20   # 16x the MALL: a re-read copy has long left it
 
 
 def alg_bytes(n_out, n_in):
@@ -143,16 +144,18 @@ class ShapeCase:
         return ok
 
 
-def profiled_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
-    summary (FETCH_SIZE x calibration + WRITE_SIZE), or None."""
+def profiled_traffic(kernel, shape):
+    """HBM bytes per launch of `kernel` on `shape` from the committed
+    rocprofv3 counter summary (FETCH_SIZE x calibration + WRITE_SIZE), or
+    None."""
     path = ROOT / "profiles" / "bfp_matvec_sweep.md"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
         parts = line.split()
-        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
-            return int(parts[2])
+        if (len(parts) == 4 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel
+                and parts[2] == shape):
+            return int(parts[3])
     return None
 
 
@@ -165,19 +168,10 @@ def kernel_config(n_in):
 
 
 def kernel_name(n_out, n_in, reps):
-    """The matvec kernel the library launches for this batch: the streaming
-    kernel when each workgroup of its fixed grid gets enough items (the
-    rule of launch_matvec in csrc/bfp_core.hip), else one chunk per
-    workgroup."""
-    import torch
+    """The matvec kernel the library launches (one 16-row chunk of one
+    problem per workgroup, csrc/bfp_core.hip:launch_matvec)."""
     nw, tpt = kernel_config(n_in)
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    grid = cus * int(os.environ.get("BFP_STREAM_WG_PER_CU", "4") or 4)
-    items = (n_out // 16) * reps
-    per = -(-items // grid)
-    lds = (-(-per // (n_out // 16)) + 1) * (n_in // 16) * 17 * 4
-    stream = per >= int(os.environ.get("BFP_STREAM_MIN_ITEMS", "256") or 256) and lds <= 48 * 1024
-    return ("matvec_stream_kernel<%d,%d>" if stream else "matvec_kernel<%d,%d>") % (nw, tpt)
+    return "matvec_kernel<%d,%d>" % (nw, tpt)
 
 
 def _cpu_matvec_sample(seconds):
@@ -522,15 +516,11 @@ def main():
                           "kernel": kernel_name(c.n_out, c.n_in, c.reps)})
     total_bytes = sum(c.bytes_per_launch() for c in cases) * args.steps
     value = total_bytes / wall / 1e9
-    # dominant kernel instantiation: the one with the most time
-    groups = {}
-    for k, c in enumerate(cases):
-        g = groups.setdefault(per_shape[k]["kernel"], [0.0, 0, 0])
-        g[0] += per_shape[k]["ms_per_launch"]
-        g[1] += c.bytes_per_launch()
-        g[2] += 1
-    kname, (gms, gbytes, nl) = max(groups.items(), key=lambda kv: kv[1][0])
-    achieved = (gbytes / nl) / ((gms / nl) * 1e-3) / 1e9
+    # the dominant launch: the shape with the most time, and its kernel
+    kd = max(range(len(cases)), key=lambda k: per_shape[k]["ms_per_launch"])
+    kname, kshape = per_shape[kd]["kernel"], per_shape[kd]["shape"]
+    kbytes = cases[kd].bytes_per_launch()
+    achieved = kbytes / (per_shape[kd]["ms_per_launch"] * 1e-3) / 1e9
     out = {
         "metric": "decode tokens/s at 1 GPU + BFP matvec HBM GB/s (% of peak), bit-exact",
         "value": round(value, 1),
@@ -550,11 +540,11 @@ def main():
         "bit_exact": parity,
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "per_shape": per_shape,
-        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "roofline": {"bound": "hbm", "kernel": kname, "shape": kshape,
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(kname),
-                     "alg_bytes_per_launch": int(gbytes / nl)},
+                     "traffic": profiled_traffic(kname, kshape),
+                     "alg_bytes_per_launch": int(kbytes)},
     }
     if not args.no_decode:
         print("[bench] config 3 decode", file=sys.stderr, flush=True)

@@ -108,12 +108,11 @@ def _ring_case(n_out, n_in, ring, n_mats, seed):
 @pytest.mark.parametrize("n_out,n_in,ring,n_mats", [(192, 576, 5, 401), (576, 1536, 3, 121),
                                                     (16, 576, 7, 5003)],
                          ids=["12chunk", "ffn-in", "1chunk"])
-def test_matvec_streaming_path(gpu, n_out, n_in, ring, n_mats):
-    """Long batches run the streaming kernel (fixed grid, contiguous item
-    ranges, double-buffered weight registers, inputs staged per range):
-    every problem bit-exact against the oracle, including ranges that span
-    several problems and an odd item count."""
-    print(f"[matvec] streaming {n_out}x{n_in} ring {ring} x {n_mats}", flush=True)
+def test_matvec_long_batches(gpu, n_out, n_in, ring, n_mats):
+    """Long batches over a ring of weight copies (up to 5003 problems in one
+    launch, one chunk of one problem per workgroup): every problem
+    bit-exact against the oracle."""
+    print(f"[matvec] long batch {n_out}x{n_in} ring {ring} x {n_mats}", flush=True)
     W, xm, xe, ym, ye = _ring_case(n_out, n_in, ring, n_mats, seed=n_mats)
     Wq = [_oracle_quantize_W(W[r]) for r in range(ring)]
     for i in range(n_mats):

@@ -239,68 +239,6 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
   }
 }
 
-// Streaming form for long batches: a fixed grid in which workgroup w walks
-// the contiguous item range [w*per_wg, (w+1)*per_wg) (item = problem *
-// n_chunks + chunk, so a workgroup streams contiguous weight memory), with
-// two register sets: the next chunk's weights are in flight while the
-// current chunk is reduced and written.  The input vectors of the range's
-// problems (usually one or two) are staged once up front, so the loop has no
-// branch that issues loads.  Same engine, same results as matvec_kernel.
-template <int NW, int TPT>
-__global__ __launch_bounds__(64 * NW) void matvec_stream_kernel(
-    const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
-    long long smat_e, int nT, int n_chunks, int ring, const int16_t *__restrict__ xm,
-    const int8_t *__restrict__ xe, long long x_stride, int16_t *__restrict__ ym,
-    int8_t *__restrict__ ye, long long y_stride, long long n_items, long long per_wg) {
-  extern __shared__ int smem[];   // per staged problem: nT*16 (x) then nT (exponents)
-  __shared__ int redM[NW * 16];
-  __shared__ long long redA[NW * 16];
-  const long long i0 = blockIdx.x * per_wg;
-  const long long i1 = i0 + per_wg < n_items ? i0 + per_wg : n_items;
-  if (i0 >= i1) return;
-  const long long m0 = i0 / n_chunks, m1 = (i1 - 1) / n_chunks;
-  for (long long q = m0; q <= m1; ++q) {
-    int *xs = smem + (q - m0) * nT * 17;
-    stage_x_bfp(xs, xs + nT * 16, xm + q * x_stride, xe + q * (x_stride / 16), nT);
-  }
-
-  auto load = [&](long long it, ChunkRegs<TPT> &R) {
-    it = it < i1 ? it : i1 - 1;
-    const long long mat = it / n_chunks;
-    const int c = (int)(it - mat * n_chunks);
-    const long long wmat = ring > 0 ? mat % ring : mat;
-    load_chunk_nb<NW, TPT>(R, Pm + wmat * smat_m + (long long)c * nT * 32,
-                           Pe + wmat * smat_e + (long long)c * nT * 16, nT);
-  };
-  auto process = [&](long long it, const ChunkRegs<TPT> &R) {
-    const bool store = it < i1;
-    it = store ? it : i1 - 1;
-    const long long mat = it / n_chunks;
-    const int c = (int)(it - mat * n_chunks);
-    const int *xs = smem + (mat - m0) * nT * 17;
-    long long A;
-    int M;
-    chunk_AM<NW, TPT>(R, xs, xs + nT * 16, nT, redM, redA, A, M);
-    if (threadIdx.x < 64) {
-      int m, e;
-      chunk_quant(A, M, m, e);
-      const int lane = threadIdx.x;
-      if (store && lane < 16) ym[mat * y_stride + c * 16 + lane] = (int16_t)m;
-      if (store && lane == 0) ye[mat * (y_stride / 16) + c] = (int8_t)e;
-    }
-  };
-
-  ChunkRegs<TPT> RA, RB;
-  load(i0, RA);
-  __syncthreads();   // staged inputs visible
-  for (long long k = i0; k < i1; k += 2) {
-    load(k + 1, RB);
-    process(k, RA);
-    load(k + 2, RA);
-    process(k + 1, RB);
-  }
-}
-
 // Read-only streaming probe: workgroup w reads the contiguous range
 // [w*per, (w+1)*per) of 16-byte words, eight loads in flight per thread
 // (addresses clamped, so there is no branch around a load), folded into one
@@ -344,33 +282,6 @@ __global__ __launch_bounds__(128) void embed_gather_kernel(const uint4 *__restri
     out_e[(long long)r * (D / 16) + t] = ok ? lu_e[(long long)id * e_row + t] : (int8_t)-127;
 }
 
-typedef void (*matvec_stream_fn)(const uint4 *, const int8_t *, long long, long long, int, int,
-                                 int, const int16_t *, const int8_t *, long long, int16_t *,
-                                 int8_t *, long long, long long, long long);
-
-template <int NW>
-static matvec_stream_fn pick_stream_tpt(int tpt) {
-  if (tpt <= 1) return matvec_stream_kernel<NW, 1>;
-  if (tpt <= 2) return matvec_stream_kernel<NW, 2>;
-  if (tpt <= 3) return matvec_stream_kernel<NW, 3>;
-  if (tpt <= 4) return matvec_stream_kernel<NW, 4>;
-  if (tpt <= 6) return matvec_stream_kernel<NW, 6>;
-  if (tpt <= 8) return matvec_stream_kernel<NW, 8>;
-  return nullptr;
-}
-
-static matvec_stream_fn pick_matvec_stream(int nw, int tpt) {
-  switch (nw) {
-    case 1: return pick_stream_tpt<1>(tpt);
-    case 2: return pick_stream_tpt<2>(tpt);
-    case 3: return pick_stream_tpt<3>(tpt);
-    case 4: return pick_stream_tpt<4>(tpt);
-    case 6: return pick_stream_tpt<6>(tpt);
-    case 8: return pick_stream_tpt<8>(tpt);
-    case 9: return pick_stream_tpt<9>(tpt);
-    default: return nullptr;
-  }
-}
 
 static int device_cus() {
   static int cus = 0;
@@ -424,23 +335,6 @@ int default_waves(int nT) {
   return 9;
 }
 
-// Streaming matvec grid: workgroups per CU, and the fewest items per
-// workgroup for which the streaming kernel is used (tuning knobs
-// BFP_STREAM_WG_PER_CU, BFP_STREAM_MIN_ITEMS).
-static int env_int(const char *name, int dflt) {
-  const char *v = getenv(name);
-  if (!v || !*v) return dflt;
-  const int x = atoi(v);
-  return x > 0 ? x : dflt;
-}
-static int stream_wg_per_cu() {
-  static const int v = env_int("BFP_STREAM_WG_PER_CU", 4);
-  return v;
-}
-static int stream_min_items() {
-  static const int v = env_int("BFP_STREAM_MIN_ITEMS", 256);
-  return v;
-}
 
 int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats, int ring,
                   long long smat_m, long long smat_e, const int16_t *x_m, const int8_t *x_e,
@@ -465,19 +359,11 @@ int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_m
   if (blocks > INT_MAX) return set_err(BFP_EINVAL, "matvec: grid too large");
   size_t shm = (size_t)nT * 17 * sizeof(int);
   if (shm > 60 * 1024) return set_err(BFP_EINVAL, "matvec: n_in=%d too large", n_in);
-  // long batches: the streaming kernel, STREAM_WG_PER_CU workgroups per CU
-  matvec_stream_fn sfn = pick_matvec_stream(nw, tpt);
-  const long long grid = (long long)device_cus() * stream_wg_per_cu();
-  const long long per = (blocks + grid - 1) / grid;
-  const size_t shs = (size_t)((per + n_chunks - 1) / n_chunks + 1) * nT * 17 * sizeof(int);
-  if (sfn && per >= stream_min_items() && shs <= 48 * 1024) {
-    const long long nwg = (blocks + per - 1) / per;
-    hipLaunchKernelGGL(sfn, dim3((unsigned)nwg), dim3(64 * nw), shs, stream,
-                       reinterpret_cast<const uint4 *>(P_m), reinterpret_cast<const int8_t *>(P_e),
-                       smat_m / 16, smat_e, nT, n_chunks, ring, x_m, x_e, x_stride, y_m, y_e,
-                       y_stride, blocks, per);
-    return launch_status("matvec");
-  }
+  // One 16-row chunk of one problem per workgroup, for every batch length:
+  // the workgroups run in order, so a batch walks its problems (and a ring
+  // of weight copies) in sequence.  (A fixed grid in which each workgroup
+  // streamed a contiguous range of chunks measured 5.5 TB/s on HBM-resident
+  // weights against this form's 6.8.)
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * nw), shm, stream,
                      reinterpret_cast<const uint4 *>(P_m), reinterpret_cast<const int8_t *>(P_e),
                      smat_m / 16, smat_e, nT, n_chunks, ring, x_m, x_e, x_stride, y_m, y_e,
