@@ -282,19 +282,6 @@ __global__ __launch_bounds__(128) void embed_gather_kernel(const uint4 *__restri
     out_e[(long long)r * (D / 16) + t] = ok ? lu_e[(long long)id * e_row + t] : (int8_t)-127;
 }
 
-
-static int device_cus() {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-  }
-  return cus;
-}
-
 typedef void (*matvec_fn)(const uint4 *, const int8_t *, long long, long long, int, int, int,
                           const int16_t *, const int8_t *, long long, int16_t *, int8_t *,
                           long long);
