@@ -193,6 +193,28 @@ def test_tile_quantize_and_decode(gpu):
     assert (api.fp_quantize_vec(v) == sim.fp_quantize_vec(v)).all()
 
 
+def test_tile_quantize_near_power_of_two(gpu):
+    """Tile maxima 1..100 doubles below 2^k: the device exponent follows
+    floor(np.log2(.)) + 1, which rounds up to k + 1 within n_up(k) doubles
+    (e.g. nextafter(256, 0) -> e 9, m 16384), for every k a tile exponent
+    can take, both signs."""
+    import bfp.api as api
+    rng = np.random.default_rng(3)
+    tiles = []
+    for k in range(-128, 129):
+        for n in (1, 2, 5, 6, 11, 12, 22, 23, 44, 45, 88, 89):
+            t = rng.standard_normal(16) * np.ldexp(1.0, k - 4)
+            b = float(np.ldexp(1.0, k) - n * np.ldexp(1.0, k - 53))
+            t[rng.integers(16)] = b if rng.random() < 0.5 else -b
+            tiles.append(t)
+    v = np.concatenate(tiles)
+    m, e = api.tile_quantize(v)
+    wm, we = sim.tile_quantize(v)
+    assert (e == we).all() and (m == wm).all()
+    m, e = api.tile_quantize(np.r_[np.nextafter(256.0, 0.0), np.zeros(15)])
+    assert e[0] == 9 and m[0, 0] == 16384
+
+
 def test_bad_shapes_raise(gpu):
     import bfp.api as api
     from bfp._lib import BfpError

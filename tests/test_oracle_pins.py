@@ -64,6 +64,57 @@ def test_tile_quantize_vs_bigint():
         assert m.tolist() == bm
 
 
+def _below_pow2(k, n):
+    """The double n spacings below 2^k (in the binade [2^(k-1), 2^k))."""
+    return float(np.ldexp(1.0, k) - n * np.ldexp(1.0, k - 53))
+
+
+def test_np_log2_roundup_closed_form():
+    """np.log2 rounds to the integer k for doubles up to n_up(k) spacings
+    below 2^k; the closed form the kernels use (log2_up_ulps) must give that
+    count for every exponent a tile can have."""
+    for k in range(-130, 131):
+        n = 0
+        while np.floor(np.log2(_below_pow2(k, n + 1))) >= k:
+            n += 1
+        assert n == bi.log2_up_ulps(k), k
+
+
+def test_near_power_of_two_tiles_vs_bigint():
+    """Tiles whose max sits 0..100 doubles below a power of two: numpy's
+    quantiser (floor(np.log2) + 1) against the decimal-logarithm model.  A
+    quantiser using the exact floor(log2) (frexp) fails at n <= n_up(k)."""
+    rng = np.random.default_rng(13)
+    hit = 0
+    for k in list(range(-127, -100)) + list(range(-70, 70)) + list(range(100, 128)):
+        for n in (1, 2, 5, 11, 22, 44, 45, 88, 100):
+            v = rng.standard_normal(16) * np.ldexp(1.0, k - 3)
+            v[rng.integers(16)] = _below_pow2(k, n) * (1 if rng.random() < .5 else -1)
+            m, e = sim.tile_quantize(v)
+            bm, be = bi.quantize_vec([float(x) for x in v])
+            assert list(e) == be and m.tolist() == bm, (k, n)
+            hit += n <= bi.log2_up_ulps(k)
+    assert hit > 100
+
+
+def test_epilogue_int_near_power_of_two():
+    """The float-free matvec epilogue's round-up rule (row key 2L + u)
+    against quantize_tile of the exact row values, on rows whose |y| lies
+    just below 2^k with |k| >= 65 (n_up = 44 or 88, so |A| >= 2^47 - 44*32
+    reaches the rule)."""
+    rng = random.Random(14)
+    for M in (64 + 30 - 48, 65 + 30 - 48, 96, -300 + 30 + 48 + 100, -48):
+        for gap in (1, 2, 3, 4, 31, 32, 33, 64):
+            rows = []
+            for r in range(16):
+                A = rng.randrange(-(1 << 46), 1 << 46)
+                rows.append((A, M + rng.randrange(-3, 1)))
+            sign = 1 if rng.random() < .5 else -1
+            rows[5] = (sign * ((1 << 48) - gap), M)
+            vals = [Fraction(A) * Fraction(2) ** (m - 30) for A, m in rows]
+            assert bi.epilogue_int(rows) == bi.quantize_tile(vals), (M, gap)
+
+
 def test_idempotence():
     rng = np.random.default_rng(12)
     v = rng.standard_normal(576) * np.exp(rng.standard_normal(576))

@@ -19,14 +19,37 @@ constexpr int ALIGN_MAX = 47;
 constexpr long long SAT_HI = (1LL << 47) - 1;
 constexpr long long SAT_LO = -(1LL << 47);
 
-// Shared exponent of a tile from its max |v|: floor(log2(amax)) + 1 clipped to
-// [-127, 127].  frexp gives amax = f * 2^x with f in [0.5, 1), so
-// floor(log2(amax)) + 1 == x exactly.  amax == 0 -> -127 (the reference floors
-// amax at 1e-300, whose exponent clips to -127).
+// floor(np.log2(a)) as numpy computes it.  np.log2 is correctly rounded, so
+// for a in [2^(k-1), 2^k) it returns k itself -- not a value below k -- when
+// log2(a) = k - d lies within half a double spacing of k, i.e. when
+// a >= 2^k (1 - n 2^-53) with n = n_up(k) = floor(2^p ln 2), where p is
+// floor(log2 |k|) (less one for a power of two k > 0, whose lower neighbour
+// sits in the binade below).  n_up is 0 for |k| <= 2, 1 for k = 3, 4, -2,
+// -3, ... 44 for k = 65..128 and -64..-127; the tests check every
+// k in [-130, 130] against numpy.  0xB17217F7D1CF79AB is ln 2 in 0.64 fixed
+// point: its top p bits are floor(2^p ln 2).
+__device__ __forceinline__ int log2_up_ulps(int k) {
+  if (k == 0) return 0;
+  const int a = k < 0 ? -k : k;
+  int p = 31 - __clz(a);
+  if (k > 0 && (a & (a - 1)) == 0) --p;
+  if (p <= 0) return 0;
+  if (p > 10) p = 10;
+  return (int)(0xB17217F7D1CF79ABull >> (64 - p));
+}
+
+// Shared exponent of a tile from its max |v|: floor(np.log2(amax)) + 1
+// clipped to [-127, 127] (full.py:92).  frexp gives amax = f * 2^x with f in
+// [0.5, 1), so the exact floor(log2(amax)) + 1 is x; numpy's rounding of
+// log2 makes it x + 1 when f >= 1 - n_up(x) 2^-53 (1 - n 2^-53 is exact).
+// amax == 0 -> -127 (the reference floors amax at 1e-300, whose exponent
+// clips to -127).
 __device__ __forceinline__ int tile_exp_of(double amax) {
   if (!(amax > 0.0)) return -127;
   int x;
-  (void)frexp(amax, &x);
+  const double f = frexp(amax, &x);
+  const int n = log2_up_ulps(x);
+  if (n > 0 && f >= 1.0 - (double)n * 0x1p-53) ++x;
   return x < -127 ? -127 : (x > 127 ? 127 : x);
 }
 
@@ -59,17 +82,31 @@ __device__ __forceinline__ int rne_shr_clip(long long A, int s) {
 
 __device__ __forceinline__ int msb64(unsigned long long a) { return 63 - __clzll(a); }
 
-// floor(log2|y|) of y = A * 2^(M-30), or INT_MIN-ish sentinel when A == 0.
 constexpr int L_NONE = -(1 << 30);
-__device__ __forceinline__ int row_log2(long long A, int M) {
+
+// The chunk exponent's reduction key of one row: 2 L + u, where L =
+// floor(log2|y|) and u = 1 when np.log2(|y|) rounds up to L + 1 (|y| within
+// n_up(L + 1) double spacings below 2^(L+1), see log2_up_ulps).  With |A| in
+// [2^b, 2^(b+1)) that is (2^(b+1) - |A|) 2^(52-b) <= n_up, which needs b >= 44
+// (|A| < 2^48 here, n_up <= 709).  The max of the keys over a tile gives the
+// largest L and whether its largest |y| rounds up.
+__device__ __forceinline__ int row_exp_key(long long A, int M) {
   if (A == 0) return L_NONE;
-  unsigned long long a = A < 0 ? (unsigned long long)(-A) : (unsigned long long)A;
-  return msb64(a) + M - 30;
+  const unsigned long long a = A < 0 ? (unsigned long long)(-A) : (unsigned long long)A;
+  const int b = msb64(a);
+  const int L = b + M - 30;
+  int u = 0;
+  if (b >= 44) {
+    const unsigned long long gap = (2ull << b) - a;            // >= 1
+    u = (gap << (52 - b)) <= (unsigned long long)log2_up_ulps(L + 1) ? 1 : 0;
+  }
+  return 2 * L + u;
 }
 
-__device__ __forceinline__ int chunk_exp_from_lmax(int Lmax) {
-  if (Lmax == L_NONE) return -127;
-  int e = Lmax + 1;
+// Tile exponent from the max of row_exp_key over the tile.
+__device__ __forceinline__ int chunk_exp_from_key(int key) {
+  if (key == L_NONE) return -127;
+  const int e = (key >> 1) + 1 + (key & 1);
   return e < -127 ? -127 : (e > 127 ? 127 : e);
 }
 

@@ -293,12 +293,12 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
 // Quantise the chunk's 16 rows (wave 0; lanes r and r+16k hold row r): the
 // raw tile_quantize of the exact outputs, as fp_quantize_vec forms it.
 __device__ __forceinline__ void chunk_quant(long long A, int M, int &m, int &e) {
-  int L = row_log2(A, M);
-  L = pmax<1>(L);
-  L = pmax<2>(L);
-  L = pmax<4>(L);
-  L = pmax<8>(L);
-  e = chunk_exp_from_lmax(L);
+  int key = row_exp_key(A, M);
+  key = pmax<1>(key);
+  key = pmax<2>(key);
+  key = pmax<4>(key);
+  key = pmax<8>(key);
+  e = chunk_exp_from_key(key);
   m = rne_shr_clip(A, e + 15 - M);
 }
 
