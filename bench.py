@@ -41,6 +41,55 @@ def alg_bytes(n_out, n_in):
     return n_out * n_in * 2 + n_out * n_in // 16 + n_in * 2 + n_in // 16 + n_out * 2 + n_out // 16
 
 
+# ----------------------------------------------------------- decode bytes
+def layer_weight_bytes(d):
+    """BFP weights + exponents one layer step reads: Q|K|V, O, G|U, D."""
+    elems = (d.D + 2 * d.KV) * d.D + d.D * d.D + 2 * d.FFN * d.D + d.D * d.FFN
+    return elems * 2 + elems // 16
+
+
+def kv_bytes_per_position(d):
+    """K and V of one position of one layer: mantissas + tile exponents."""
+    return 2 * (d.KV * 2 + d.KV // 16)
+
+
+def head_bytes(d):
+    """The sim-faithful head reads the raw float32 tied embedding once per
+    step (full.py:439), whatever the batch."""
+    return d.VOCAB * d.D * 4
+
+
+def step_bytes(d, pos, batch=1, head=True):
+    """Algorithmic HBM bytes of one decode step at position pos: every
+    layer's weights once, each sequence's KV rows 0..pos (pos+1 rows: the
+    cache read plus this step's row), and the head's embedding."""
+    return (d.NL * (layer_weight_bytes(d) + batch * kv_bytes_per_position(d) * (pos + 1))
+            + (head_bytes(d) if head else 0))
+
+
+def hbm_roofline(nbytes, seconds, basis):
+    gbs = nbytes / seconds / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": int(nbytes), "basis": basis}
+
+
+def cpu_info():
+    """The host the CPU baselines ran on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    return {"model": model, "nproc": nproc, "cpu_count": os.cpu_count()}
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -52,6 +101,7 @@ def parse():
     ap.add_argument("--cpu-workers", type=int, default=0,
                     help="processes for the all-cores CPU baseline (0: min(cpu count, 16))")
     ap.add_argument("--cpu-worker", type=float, default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-decode-worker", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-3 decode leg")
     ap.add_argument("--decode-reps", type=int, default=3)
@@ -88,22 +138,27 @@ class ShapeCase:
         g.manual_seed(seed)
         self.Pm = torch.empty(self.ring * self.bm, dtype=torch.uint8, device="cuda")
         self.Pe = torch.empty(self.ring * self.be, dtype=torch.uint8, device="cuda")
+        # the reps checked against the oracle: first, last and three between
+        # (their ring slots' float32 weights are kept on the host)
+        self.check_reps = sorted({int(r) for r in
+                                  (0, reps - 1, reps // 4, reps // 2, (3 * reps) // 4)})
+        slots = {r % self.ring for r in self.check_reps}
+        self.W_host = {}
         # generate and pack in slabs to bound the fp32 staging memory
         per = max(1, (256 << 20) // (n_out * n_in * 4))
-        self.W0 = None
         for r0 in range(0, self.ring, per):
             k = min(per, self.ring - r0)
             W = torch.randn((k * n_out, n_in), generator=g, device="cuda", dtype=torch.float32)
             W.mul_(0.02)
-            if r0 == 0:
-                self.W0 = W[:n_out].cpu().numpy()
+            for sl in slots:
+                if r0 <= sl < r0 + k:
+                    self.W_host[sl] = W[(sl - r0) * n_out:(sl - r0 + 1) * n_out].cpu().numpy()
             call("bfp_quantize_pack_f32_d", W.data_ptr(), k * n_out, n_in,
                  self.Pm.data_ptr() + r0 * self.bm, self.Pe.data_ptr() + r0 * self.be,
                  _dev.stream())
             del W
         X = torch.randn((reps, n_in), generator=g, device="cuda", dtype=torch.float32)
-        self.X_last = X[reps - 1].cpu().numpy()
-        self.X0 = X[0].cpu().numpy()
+        self.X_host = {r: X[r].cpu().numpy() for r in self.check_reps}
         self.xm = torch.empty(reps * n_in, dtype=torch.int16, device="cuda")
         self.xe = torch.empty(reps * n_in // 16, dtype=torch.int8, device="cuda")
         call("bfp_tile_quantize_f32_d", X.data_ptr(), reps * n_in, self.xm.data_ptr(),
@@ -126,20 +181,22 @@ class ShapeCase:
         return alg_bytes(self.n_out, self.n_in) * self.reps
 
     def check(self):
-        """Reps 0 and reps-1 against the CPU oracle, bit for bit."""
+        """The sampled reps (first, last and three between; each reads ring
+        slot rep % ring) against the CPU oracle, bit for bit."""
         import numpy as np
         from oracle import bfp_sim as sim
         ym = self.ym.cpu().numpy().reshape(self.reps, -1)
         ye = self.ye.cpu().numpy().reshape(self.reps, -1)
-        Wm, We = sim.tile_quantize(self.W0.astype(np.float64))
         nt = self.n_in // 16
-        Wm, We = Wm.reshape(self.n_out, nt, 16), We.reshape(self.n_out, nt)
+        packed = {}
         ok = True
-        for r, x in ((0, self.X0), (self.reps - 1, self.X_last)):
-            if r % self.ring != 0:
-                continue                      # only ring slot 0 is mirrored on the host
-            xm, xe = sim.tile_quantize(x.astype(np.float64))
-            wm, we = sim.tile_quantize(sim.matvec_hw_golden(xm, xe, Wm, We))
+        for r in self.check_reps:
+            sl = r % self.ring
+            if sl not in packed:
+                Wm, We = sim.tile_quantize(self.W_host[sl].astype(np.float64))
+                packed[sl] = (Wm.reshape(self.n_out, nt, 16), We.reshape(self.n_out, nt))
+            xm, xe = sim.tile_quantize(self.X_host[r].astype(np.float64))
+            wm, we = sim.matvec_bfp(xm, xe, *packed[sl])
             ok &= bool((ym[r] == wm.reshape(-1)).all() and (ye[r] == we).all())
         return ok
 
@@ -208,7 +265,7 @@ def cpu_baseline(seconds):
     os.environ.setdefault("OPENBLAS_NUM_THREADS", "1")
     total_b, total_t, done = _cpu_matvec_sample(seconds)
     return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
+            "kind": "port", "cpu": cpu_info(),
             "sample": "oracle/bfp_sim.matvec_hw_golden (numpy, 1 thread), reps per shape "
                       + ", ".join(done) + f" in {total_t:.1f} s"}
 
@@ -232,8 +289,15 @@ def cpu_baseline_all_cores(seconds, workers):
     total_b = sum(r["bytes"] for r in res)
     t = max(r["seconds"] for r in res)
     return {"value": round(total_b / t / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
+            "cpu": cpu_info(),
             "sample": f"{workers} concurrent single-threaded processes, each the 1-thread sample "
                       f"({seconds:.0f} s budget), slowest {t:.1f} s"}
+
+
+def _fixture(name):
+    import numpy as np
+    path = ROOT / "tests" / "golden" / name
+    return np.load(path) if path.exists() else None
 
 
 def decode_leg(reps):
@@ -242,7 +306,6 @@ def decode_leg(reps):
     bfp_decode (device time of the steps that emit the 64 tokens, and of all
     72 steps); tokens checked against the reference's own run
     (tests/golden/ref_decode_cfg3.npz)."""
-    import numpy as np
     from bfp import Dims, synth
     from bfp.model import BfpModel
     n_prompt, n_gen = 8, 64
@@ -261,26 +324,29 @@ def decode_leg(reps):
         tot_ms.append(t)
         gen_ms.append(g)
     gm.close()
-    ref = ROOT / "tests" / "golden" / "ref_decode_cfg3.npz"
+    f = _fixture("ref_decode_cfg3.npz")
     exact = None
-    if ref.exists():
-        f = np.load(ref)
+    if f is not None:
         exact = bool(list(toks[0]) == [int(t) for t in f["tokens"]]
                      and list(prompt) == [int(t) for t in f["prompt"]])
     g = min(gen_ms)
+    nbytes = sum(step_bytes(d, p) for p in range(n_prompt, n_prompt + n_gen))
     return {"workload": "config 3: 30 layers, prompt 8, 64 greedy tokens, batch 1",
             "tokens_per_s": round(n_gen / (g * 1e-3), 1),
             "ms_per_token": round(g / n_gen, 4),
             "steps_per_s_all": round((n_prompt + n_gen) / (min(tot_ms) * 1e-3), 1),
             "wall_s_per_decode": round(min(walls), 4),
-            "tokens_match_reference": exact}
+            "tokens_match_reference": exact,
+            "roofline": hbm_roofline(nbytes, g * 1e-3,
+                                     "per generated step: 30 layers' BFP weights + the fp32 "
+                                     "embedding the head reads + KV rows 0..pos")}
 
 
 def long_context_leg():
     """30 layers, 48-token prompt, greedy decode through
     position 2047 (2000 new tokens); tokens/s overall and per position
-    window from per-step HIP events."""
-    import numpy as np
+    window from per-step HIP events; tokens checked against the reference's
+    own run (tests/golden/ref_decode_cfg4.npz) when it is present."""
     from bfp import Dims, synth
     from bfp.model import BfpModel
     n_prompt, n_gen = 48, 2000
@@ -289,22 +355,35 @@ def long_context_leg():
     gm.load_fp32(synth.make_model(d, seed=0))
     prompt = synth.make_prompt(d, n_prompt, seed=4)
     gm.decode(prompt[None, :], 16)                       # warm-up
-    gm.decode(prompt[None, :], n_gen, step_times=True)
+    toks, _ = gm.decode(prompt[None, :], n_gen, step_times=True)
     st = gm.step_times_ms()
     t, g = gm.decode_time_ms()
     gm.close()
     win = {}
     for lo, hi in ((48, 112), (496, 560), (1008, 1072), (1984, 2048)):
         win[f"pos_{lo}_{hi - 1}"] = round((hi - lo) / (float(st[lo:hi].sum()) * 1e-3), 1)
+    f = _fixture("ref_decode_cfg4.npz")
+    exact = None
+    if f is not None:
+        exact = bool(list(toks[0]) == [int(x) for x in f["tokens"]]
+                     and list(prompt) == [int(x) for x in f["prompt"]])
+    nbytes = sum(step_bytes(d, p) for p in range(n_prompt, n_prompt + n_gen))
+    lo, hi = 1984, 2048
+    tail_bytes = sum(step_bytes(d, p) for p in range(lo, hi))
     return {"workload": "config 4: 30 layers, prompt 48, decode to position 2047 (2000 tokens)",
             "tokens_per_s": round(n_gen / (g * 1e-3), 1), "ms_per_token_mean": round(g / n_gen, 4),
-            "tokens_per_s_by_position": win}
+            "tokens_per_s_by_position": win, "tokens_match_reference": exact,
+            "roofline": hbm_roofline(nbytes, g * 1e-3,
+                                     "per generated step: 30 layers' BFP weights + the fp32 "
+                                     "embedding the head reads + KV rows 0..pos"),
+            "roofline_pos_1984_2047": hbm_roofline(tail_bytes, float(st[lo:hi].sum()) * 1e-3,
+                                                   "the same over positions 1984..2047")}
 
 
 def batch_leg(n_gen=128):
     """64 independent sequences, 8-token prompts, 128
-    greedy tokens each; aggregate tokens/s.  Sequence 0 uses config 3's
-    prompt: its first 64 tokens must equal the reference's config-3 tokens."""
+    greedy tokens each; aggregate tokens/s.  Every sequence's tokens are
+    checked against the reference's own runs (tests/golden/ref_decode_cfg5.npz)."""
     import numpy as np
     from bfp import Dims, synth
     from bfp.model import BfpModel
@@ -318,14 +397,18 @@ def batch_leg(n_gen=128):
     toks, _ = gm.decode(prompts, n_gen)
     t, g = gm.decode_time_ms()
     gm.close()
-    ref = ROOT / "tests" / "golden" / "ref_decode_cfg3.npz"
+    f = _fixture("ref_decode_cfg5.npz")
     exact = None
-    if ref.exists():
-        want = [int(x) for x in np.load(ref)["tokens"]][:n_gen]
-        exact = bool(list(toks[0][:len(want)]) == want)
+    if f is not None:
+        exact = bool((f["prompts"] == prompts).all() and
+                     (toks[:, :n_gen] == f["tokens"][:, :n_gen]).all())
+    nbytes = sum(step_bytes(d, p, batch=B) for p in range(n_prompt, n_prompt + n_gen))
     return {"workload": f"config 5: 64 sequences, prompt 8, {n_gen} greedy tokens each",
             "tokens_per_s": round(B * n_gen / (g * 1e-3), 1),
-            "ms_per_step": round(g / n_gen, 4), "seq0_matches_reference": exact}
+            "ms_per_step": round(g / n_gen, 4), "all_tokens_match_reference": exact,
+            "roofline": hbm_roofline(nbytes, g * 1e-3,
+                                     "per generated step: 30 layers' BFP weights once + the "
+                                     "fp32 embedding once + each sequence's KV rows 0..pos")}
 
 
 def layer_leg():
@@ -353,99 +436,146 @@ def layer_leg():
         t[nl] = float(best.mean())
         gm.close()
     us = (t[10] - t[2]) / 8 * 1e3
+    d = Dims(NL=1, MAX_CTX=8)
+    nbytes = sum(layer_weight_bytes(d) + kv_bytes_per_position(d) * (p + 1) for p in range(7)) / 7
     return {"workload": "config 1: one SmolLM2-135M-shaped layer, batch 1, positions 0-6",
-            "layer_step_us": round(us, 2), "steps_per_s": round(1e6 / us, 1)}
+            "layer_step_us": round(us, 2), "steps_per_s": round(1e6 / us, 1),
+            "roofline": hbm_roofline(nbytes, us * 1e-6,
+                                     "one layer's BFP weights + KV rows 0..pos, mean over "
+                                     "positions 0-6")}
 
 
-_ORACLE = {}
-
-
-def _oracle_model():
-    """The oracle's model of the bench's 30-layer synthetic weights (built once)."""
-    if "m" not in _ORACLE:
-        from oracle import bfp_sim as sim
-        from bfp import Dims, synth
-        _ORACLE["m"] = sim.build_model(synth.make_model(Dims(MAX_CTX=2048), seed=0))
-    return _ORACLE["m"]
-
-
-def cpu_decode_baseline():
-    """Config 3 on the oracle: the step time at position 36, the mean
-    position of its 72 steps (the per-position attention loops make the
-    step time grow with the position)."""
-    t36 = _cpu_step_seconds(36)
-    return {"value": round(1.0 / t36, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/bfp_sim.fwd_layer x 30 + head_argmax, one step at position 36 "
-                      f"({t36:.2f} s) over a synthetic KV cache"}
-
-
-def _cpu_step_seconds(pos, reps=2):
-    """One decode step of the oracle (30 fwd_layer calls + the head) at
-    position pos over a synthetic KV cache of pos + 1 rows per layer (its
-    values do not change the work: the per-position loops run pos + 1
-    times whatever they hold); the best of reps, 1 thread."""
+# ------------------------------------------------------------ CPU baselines
+# The oracle (oracle/bfp_sim.py, line-faithful to full.py) and its
+# numpy-vectorised restatement (oracle/bfp_vec.py), timed in child
+# processes so that each run sets its own BLAS thread count before numpy
+# loads.  A child builds the bench's synthetic model once and times one
+# decode step (NL fwd_layer calls, and the head for the 30-layer model) at
+# each asked position over a synthetic KV cache of pos + 1 rows per layer
+# (the per-position loops run pos + 1 times whatever the rows hold).
+def _cpu_decode_worker(spec):
     import numpy as np
+    from bfp import Dims, synth
     from oracle import bfp_sim as sim
-    om = _oracle_model()
-    d = om.dims
-    rng = np.random.default_rng(pos)
-    kv = [{"k": rng.standard_normal((pos + 1, d.H_KV, d.HD)),
-           "v": rng.standard_normal((pos + 1, d.H_KV, d.HD))} for _ in range(d.NL)]
-    best = None
-    for _ in range(reps):
-        h = om.embed_row_q(1)
-        t0 = time.perf_counter()
-        for li in range(d.NL):
-            h = sim.fwd_layer(h, om.layers[li], pos=pos, kv=kv[li], kv_pos=pos, dims=d)
-        sim.head_argmax(h, om.norm_w_q, om.embed)
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
-    return best
+    from oracle import bfp_vec as vec
+    mod = vec if spec["kind"] == "vec" else sim
+    nl = spec.get("nl", 30)
+    d = Dims(NL=nl, MAX_CTX=2048, VOCAB=49152 if nl == 30 else 256)
+    t0 = time.perf_counter()
+    om = mod.build_model(synth.make_model(d, seed=0 if nl == 30 else 1))
+    build_s = time.perf_counter() - t0
+    out = {"build_s": round(build_s, 2), "steps": {}}
+    for pos in spec["positions"]:
+        rng = np.random.default_rng(pos)
+        kv = [{"k": sim.fp_quantize_vec(rng.standard_normal((pos + 1) * d.KV)).reshape(
+                   pos + 1, d.H_KV, d.HD),
+               "v": sim.fp_quantize_vec(rng.standard_normal((pos + 1) * d.KV)).reshape(
+                   pos + 1, d.H_KV, d.HD)} for _ in range(nl)]
+        best = None
+        for _ in range(spec.get("reps", 2) if pos < 1000 else 1):
+            h = om.embed_row_q(1) if nl == 30 else sim.fp_quantize_vec(rng.standard_normal(d.D))
+            t0 = time.perf_counter()
+            for li in range(nl):
+                h = mod.fwd_layer(h, om.layers[li], pos=pos, kv=kv[li], kv_pos=pos, dims=om.dims)
+            if nl == 30:
+                sim.head_argmax(h, om.norm_w_q, om.embed)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        out["steps"][str(pos)] = best
+    print(json.dumps(out), flush=True)
 
 
-def cpu_long_context_baseline():
-    """Config 4 on the oracle: step time at positions 48 and 2000 (the
-    per-position attention loops make it linear in the position), the mean
-    over positions 48..2047 interpolated linearly from the two."""
-    t48, t2000 = _cpu_step_seconds(48), _cpu_step_seconds(2000)
-    mean = t48 + (t2000 - t48) * ((48 + 2047) / 2 - 48) / (2000 - 48)
-    return {"value": round(1.0 / mean, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "by_position": {"pos_48": round(1.0 / t48, 4), "pos_2000": round(1.0 / t2000, 4)},
-            "sample": f"oracle/bfp_sim.fwd_layer x 30 + head_argmax, one step at position 48 "
-                      f"({t48:.2f} s) and at 2000 ({t2000:.2f} s) over a synthetic KV cache; "
-                      f"mean over 48..2047 by linear interpolation"}
+def _run_cpu_workers(spec, threads, n=1):
+    """n concurrent children running spec with `threads` BLAS threads each;
+    returns their results."""
+    import subprocess
+    env = dict(os.environ, OPENBLAS_NUM_THREADS=str(threads), OMP_NUM_THREADS=str(threads))
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--cpu-decode-worker", json.dumps(spec)]
+    procs = [subprocess.Popen(cmd, stdout=subprocess.PIPE, env=env, text=True) for _ in range(n)]
+    res = []
+    for p in procs:
+        out, _ = p.communicate()
+        if p.returncode != 0:
+            raise RuntimeError(f"cpu decode worker exited with {p.returncode}")
+        res.append(json.loads(out.strip().splitlines()[-1]))
+    return res
 
 
-def cpu_batch_baseline():
-    """Config 5 on the oracle, which decodes one sequence at a time: the
-    step time at position 72 (the mean position of 8 + 128 steps) is the
-    time per token."""
-    t72 = _cpu_step_seconds(72)
-    return {"value": round(1.0 / t72, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/bfp_sim.fwd_layer x 30 + head_argmax, one sequence's step at "
-                      f"position 72 ({t72:.2f} s); the oracle has no batched form, so 64 "
-                      f"sequences take 64 such steps"}
+def cpu_decode_baselines():
+    """The decode configs on the CPU: line-faithful and vectorised, 1 BLAS
+    thread and all cores.  Returns {leg: {name: cpu_baseline dict}}."""
+    info = cpu_info()
+    nproc = info["nproc"]
+    P = [36, 48, 72, 2000]
+    runs = {("port", 1): _run_cpu_workers({"kind": "faithful", "positions": P}, 1)[0],
+            ("vec", 1): _run_cpu_workers({"kind": "vec", "positions": P}, 1)[0],
+            ("vec", nproc): _run_cpu_workers({"kind": "vec", "positions": P}, nproc)[0]}
+    par = min(nproc, 16)
+    batch_par = _run_cpu_workers({"kind": "vec", "positions": [72]}, 1, n=par)
+    layer = {k: _run_cpu_workers({"kind": k, "positions": list(range(7)), "nl": 1}, 1)[0]
+             for k in ("faithful", "vec")}
+    name = {"port": "oracle/bfp_sim (line-faithful numpy restatement of full.py)",
+            "vec": "oracle/bfp_vec (numpy-vectorised restatement, bit-identical)"}
+
+    def entry(kind, threads, value, sample):
+        return {"value": round(value, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+                "variant": "line-faithful" if kind == "port" else "vectorised",
+                "sample": f"{name[kind]}, OPENBLAS_NUM_THREADS={threads}: {sample}", "cpu": info}
+
+    out = {"decode": {}, "long_context": {}, "batch64": {}, "layer": {}}
+    for (kind, thr), r in runs.items():
+        st = r["steps"]
+        key = f"{'faithful' if kind == 'port' else 'vectorised'}_{thr}t"
+        out["decode"][key] = entry(kind, thr, 1.0 / st["36"],
+                                   f"one 30-layer step at position 36 (the mean of config 3's "
+                                   f"72 steps), {st['36']:.3f} s")
+        t48, t2000 = st["48"], st["2000"]
+        mean = t48 + (t2000 - t48) * ((48 + 2047) / 2 - 48) / (2000 - 48)
+        out["long_context"][key] = entry(kind, thr, 1.0 / mean,
+                                         f"steps at positions 48 ({t48:.3f} s) and 2000 "
+                                         f"({t2000:.3f} s), mean over 48..2047 by linear "
+                                         f"interpolation (the step time is linear in the "
+                                         f"position)")
+        out["batch64"][key] = entry(kind, thr, 1.0 / st["72"],
+                                    f"one sequence's step at position 72 ({st['72']:.3f} s); "
+                                    f"the simulator decodes one sequence at a time")
+    t72 = max(r["steps"]["72"] for r in batch_par)
+    out["batch64"][f"vectorised_{par}proc"] = entry(
+        "vec", par, par / t72, f"{par} concurrent single-threaded processes, one sequence's step "
+        f"at position 72 each (independent sequences), slowest {t72:.3f} s")
+    for k, r in layer.items():
+        ts = [r["steps"][str(p)] for p in range(7)]
+        kk = "port" if k == "faithful" else "vec"
+        e = entry(kk, 1, 7.0 / sum(ts), f"one D=576 layer (fwd_layer) at positions 0-6, "
+                  f"{sum(ts) / 7 * 1e3:.2f} ms per step")
+        e["unit"] = "layer steps/s"
+        out["layer"][f"{'faithful' if k == 'faithful' else 'vectorised'}_1t"] = e
+    return out
 
 
 def stream_probe():
     """Practical HBM ceilings: a 1 GiB device-to-device copy (read + write
-    bytes) and a plain 16-byte-load streaming read of 2 GiB (the library's
-    bfp_probe_read_d, contiguous range per workgroup, 4 workgroups per CU)."""
+    bytes) and a 4 GiB streaming read with the library's bfp_probe_read_d
+    (16-byte loads, a contiguous range per workgroup, 4 workgroups per CU),
+    with ordinary and with non-temporal loads (the matvec's weight-stream
+    policy).  The best read is the ceiling the matvec is compared with."""
     import torch
     from bfp import _dev
     from bfp._lib import call
     a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
     a.fill_(1)
-    f = torch.ones(1 << 29, dtype=torch.float32, device="cuda")
+    f = torch.ones(1 << 30, dtype=torch.float32, device="cuda")       # 4 GiB
     n_wg = torch.cuda.get_device_properties(0).multi_processor_count * 4
     fold = torch.empty(n_wg, dtype=torch.int32, device="cuda")
 
-    def read():
-        call("bfp_probe_read_d", f.data_ptr(), 2 << 30, fold.data_ptr(), n_wg, _dev.stream())
+    def read(nt):
+        return lambda: call("bfp_probe_read_d", f.data_ptr(), 4 << 30, fold.data_ptr(), n_wg,
+                            nt, _dev.stream())
     res = {}
     for name, fn, nbytes in (("copy_1GiB", lambda: b.copy_(a), 2 << 30),
-                             ("read_2GiB", read, 2 << 30)):
+                             ("read_4GiB", read(0), 4 << 30),
+                             ("read_nt_4GiB", read(1), 4 << 30)):
         fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -455,6 +585,7 @@ def stream_probe():
         e1.record()
         torch.cuda.synchronize()
         res[name + "_GB_s"] = round(nbytes * 5 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    res["read_ceiling_GB_s"] = max(res["read_4GiB_GB_s"], res["read_nt_4GiB_GB_s"])
     del a, b, f
     return res
 
@@ -464,6 +595,9 @@ def main():
     if args.cpu_worker is not None:   # child of cpu_baseline_all_cores: CPU only
         b, t, _ = _cpu_matvec_sample(args.cpu_worker)
         print(json.dumps({"bytes": b, "seconds": t}), flush=True)
+        return
+    if args.cpu_decode_worker is not None:   # child of cpu_decode_baselines: CPU only
+        _cpu_decode_worker(json.loads(args.cpu_decode_worker))
         return
     if args.gpus != 1:
         print(f"bench.py: only --gpus 1 is supported on this build (asked for {args.gpus}); "
@@ -559,17 +693,22 @@ def main():
             print("[bench] config 5 batch 64", file=sys.stderr, flush=True)
             out["batch64"] = batch_leg()
     if args.probe:
+        print("[bench] HBM read ceiling probe", file=sys.stderr, flush=True)
         out["stream_ceiling"] = stream_probe()
+        out["roofline"]["frac_of_read_ceiling"] = round(
+            achieved / out["stream_ceiling"]["read_ceiling_GB_s"], 4)
     if not args.no_cpu:
+        print("[bench] CPU baselines", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-        workers = args.cpu_workers or min(os.cpu_count() or 1, 16)
+        workers = args.cpu_workers or min(cpu_info()["nproc"], 16)
         out["cpu_baseline_all_cores"] = cpu_baseline_all_cores(8.0, workers)
         if not args.no_decode:
-            out["decode"]["cpu_baseline"] = cpu_decode_baseline()
-            if args.long:
-                out["long_context"]["cpu_baseline"] = cpu_long_context_baseline()
-            if args.batch64:
-                out["batch64"]["cpu_baseline"] = cpu_batch_baseline()
+            cb = cpu_decode_baselines()
+            for leg, key in (("decode", "decode"), ("layer", "layer"),
+                             ("long_context", "long_context"), ("batch64", "batch64")):
+                if leg in out:
+                    out[leg]["cpu_baseline"] = cb[key]["faithful_1t"]
+                    out[leg]["cpu_baselines"] = cb[key]
     print(json.dumps(out), flush=True)
 
 

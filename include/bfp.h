@@ -92,6 +92,41 @@ int bfp_quantize_pack_f32_d(const float *W, int n_out, int n_in, void *P_m, void
                             void *stream);
 /* tile_decode (full.py:100-102): (m, e) -> float64, exact. */
 int bfp_tile_decode_d(const int16_t *m, const int8_t *e, size_t n, double *v, void *stream);
+/* The encoding of values that are already BFP, as the reference's float64
+ * arrays hold them (full.py:105-107: every stage keeps decoded tiles):
+ * tile_quantize's tile, except where that tile would round a value -- the
+ * raw form of a tile whose largest magnitude is the mantissa -32768, which
+ * tile_quantize maps to exponent e+1, halving odd mantissas -- in which case
+ * the tile one exponent lower that holds every value exactly.  Decoding the
+ * result gives v back whenever v is BFP-exact; other tiles are quantised as
+ * tile_quantize does, and set *inexact = 1 (inexact: optional device int,
+ * left alone otherwise).  The inverse of bfp_tile_decode_d on decoded
+ * tiles. */
+int bfp_tile_encode_f64_d(const double *v, size_t n, int16_t *m, int8_t *e, int *inexact,
+                          void *stream);
+
+/* ------------------------------------------------------- float64 leaf ops */
+/* The reference simulator's float64 leaf ops (full.py:236-258), float64 in
+ * and out (device pointers), stream-ordered.  Sums use numpy's pairwise
+ * order, every product and quotient is rounded separately. */
+/* rmsnorm_fp (full.py:236-238) of batch rows of n (n % 16 == 0, n <= 4096),
+ * gamma shared: y = fp_quantize_vec((x*gamma) / sqrt(mean(x*x) + eps)). */
+int bfp_rmsnorm_fp_d(const double *x, const double *gamma, int n, int batch, double eps,
+                     double *y, void *stream);
+/* silu_fp (full.py:241-242): y = fp_quantize_vec(x / (1 + exp(-x))), n % 16 == 0. */
+int bfp_silu_fp_d(const double *x, size_t n, double *y, void *stream);
+/* softmax_fp (full.py:245-247) of batch rows of n (n <= 4096):
+ * y = exp(x - max) / sum, float64 (not quantised). */
+int bfp_softmax_fp_d(const double *x, int n, int batch, double *y, void *stream);
+/* The (cos, sin) pairs rope_fp (full.py:250-258) rotates by at position pos:
+ * cs[2j], cs[2j+1] = cos, sin of 1.0 / (base ** (2*j/head_dim)) * pos for
+ * j < head_dim/2, with the host's libm as CPython evaluates them.  Host
+ * code (no device). */
+int bfp_rope_cos_sin(int pos, int head_dim, double base, double *cs);
+/* rope_fp of n_heads heads of 64 (x, y: n_heads*64 float64): out[j] =
+ * a*c - b*s, out[j+32] = b*c + a*s (a = x[j], b = x[j+32]), fp_quantize_vec
+ * per head.  cs: device copy of bfp_rope_cos_sin(pos, 64, base). */
+int bfp_rope_fp_d(const double *x, int n_heads, const double *cs, double *y, void *stream);
 
 /* ---------------------------------------------------------------- matvec */
 /* matvec_hw_golden (full.py:217-233) for n_mats independent problems in one
@@ -116,10 +151,12 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
                       int8_t *y_e, long long y_stride, int waves, void *stream);
 
 /* Measurement probe, no reference counterpart: reads [p, p + bytes) once
- * with 16-byte loads, each of n_wg workgroups of 256 threads streaming one
- * contiguous range, writing one fold word per workgroup to out (n_wg words).  Its bytes / time is the
- * practical HBM read ceiling the matvec is compared with.  bytes % 16 == 0. */
-int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, void *stream);
+ * with 16-byte loads (non-temporal when nt != 0, the matvec's weight-stream
+ * policy), each of n_wg workgroups of 256 threads streaming one contiguous
+ * range, writing one fold word per workgroup to out (n_wg words).  Its
+ * bytes / time is the practical HBM read ceiling the matvec is compared
+ * with.  bytes % 16 == 0, and every workgroup gets at least one word. */
+int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, int nt, void *stream);
 
 /* Host-buffer convenience form of matvec_hw_golden: W in the reference
  * layout, x and y in host memory.  Allocates and frees device memory. */
@@ -223,6 +260,32 @@ typedef struct bfp_stage_dump {
  * this layer. */
 int bfp_layer_step(bfp_ctx *ctx, int layer, int pos, int batch, const int16_t *h_m,
                    const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump);
+
+/* fwd_layer(h, lw, pos, kv, kv_pos) (full.py:261-293) with pos and kv_pos
+ * apart, as the single-layer harness drives them
+ * (gen_smollm_blockfp_bfp.py:42-43,332-344): RoPE at position pos (any
+ * pos >= 0; positions past MAX_CTX get their cos/sin row computed on the
+ * host), K and V written to slot kv_pos (< MAX_CTX) of this layer's cache,
+ * attention over slots 0..kv_pos.  bfp_layer_step is this with
+ * kv_pos = pos. */
+int bfp_layer_step_kv(bfp_ctx *ctx, int layer, int pos, int kv_pos, int batch, const int16_t *h_m,
+                      const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump);
+
+/* bfp_kv_io in the reference's own cache form: k, v are n x H_KV x HD
+ * float64 host arrays, rows [t0, t0+n) of kv['k'] / kv['v']
+ * (full.py:270-272,426-428).  write != 0 encodes them into the cache with
+ * bfp_tile_encode_f64_d (values the reference wrote keep their tiles) and
+ * fails with BFP_EINVAL, the cache rows then undefined, when a value is not
+ * BFP-exact; write == 0 decodes the cache into them (exact). */
+int bfp_kv_io_f64(bfp_ctx *ctx, int layer, int seq, int t0, int n, double *k, double *v,
+                  int write);
+
+/* matvec_hw_golden (full.py:217-233) of batch input vectors with one of the
+ * context's loaded matrices (which = BFP_WQ .. BFP_WD of layer): x (batch x
+ * n_in BFP, host) -> y (batch x n_out BFP, host), the raw (m, e) that
+ * fp_quantize_vec forms over 16-row tiles. */
+int bfp_matvec(bfp_ctx *ctx, const int16_t *x_m, const int8_t *x_e, int which, int layer,
+               int batch, int16_t *y_m, int8_t *y_e);
 
 /* The FPGA's decoder layer (rtl/vc707/src/smollm/smollm_layer_bfp.sv:
  * 1603-2600, the RTL engines of the bfp_rtl_* ops wired in its FSM order) on

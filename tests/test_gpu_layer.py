@@ -110,6 +110,31 @@ def test_fwd_layer_float_api(gpu):
         want = sim.fwd_layer(h, om.layers[0], pos=p, kv=kv, kv_pos=p, dims=om.dims)
         got = gm.fwd_layer(h, 0, p)
         assert (got == want).all()
-    with pytest.raises(ValueError):
-        gm.fwd_layer(h, 0, 3, kv_pos=2)
+    # RoPE position and cache slot apart: slot 2 is overwritten
+    want = sim.fwd_layer(h, om.layers[0], pos=3, kv=kv, kv_pos=2, dims=om.dims)
+    assert (gm.fwd_layer(h, 0, 3, kv_pos=2) == want).all()
     gm.close()
+
+
+def test_second_context_keeps_lds_limit(gpu):
+    """A context made after a larger one of the same attention form must
+    not lower the kernel's dynamic-LDS limit under the first: the first
+    still runs at a position past the second's capacity, and matches the
+    oracle."""
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    d1 = Dims(NL=1, MAX_CTX=2048, VOCAB=256)
+    fm = synth.make_model(d1, seed=41)
+    om = sim.build_model(fm)
+    big = BfpModel(d1)
+    big.load_fp32(fm)
+    small = BfpModel(Dims(NL=1, MAX_CTX=600, VOCAB=256))
+    rng = np.random.default_rng(41)
+    kv = sim.new_kv(om.dims, 2048)
+    h = sim.fp_quantize_vec(rng.standard_normal(d1.D))
+    want = sim.fwd_layer(h, om.layers[0], pos=1500, kv=kv, kv_pos=1500, dims=om.dims)
+    hm, he = sim.tile_quantize(h)
+    om_, oe_, _ = big.layer_step_bfp(0, 1500, hm.reshape(1, -1), he.reshape(1, -1))
+    assert (sim.tile_decode(om_[0].reshape(-1, 16), oe_[0]) == want).all()
+    small.close()
+    big.close()

@@ -35,6 +35,43 @@ def test_baker_stage_dumps(name):
         assert (pm.reshape(-1) == f[f"{tag}_m"]).all() and (pe == f[f"{tag}_e"]).all()
 
 
+def _last_head_scores(c):
+    """The scores and probabilities of the last query head at the baker's
+    KV_POS, from the oracle's post-RoPE Q and its cache (what the baker
+    saves, gen_smollm_blockfp_bfp.py:343-357)."""
+    cfg, dims = c["cfg"], c["dims"]
+    kv = {k: v.copy() for k, v in c["kv"].items()}
+    dump = {}
+    sim.fwd_layer(c["h"], c["lw"], pos=cfg["POS"], kv=kv, kv_pos=cfg["KV_POS"], dims=dims,
+                  dump=dump)
+    hq = cfg["H_Q"] - 1
+    g = hq // (cfg["H_Q"] // cfg["H_KV"])
+    q = dump["Q"][hq * 64:(hq + 1) * 64]
+    sc = np.array([float(np.dot(q, kv["k"][t, g])) / 8.0 for t in range(cfg["KV_POS"] + 1)])
+    return sc, sim.softmax_fp(sc)
+
+
+def _pad16(x, max_ctx):
+    p = np.zeros(16)
+    p[:len(x)] = x
+    return p[:16]
+
+
+@pytest.mark.parametrize("name", ["small", "full"])
+def test_baker_scores_and_probs(name):
+    """STAGE_SCORES / STAGE_PROBS: the last head's float64 scores and softmax
+    output, padded to 16 slots and tile-quantised as the baker writes them
+    (gen_smollm_blockfp_bfp.py:362-372): pins the score and softmax order
+    beyond the quantised ATTN stage."""
+    c = baker_case(name)
+    f, MC = c["fixture"], c["cfg"]["MAX_CTX"]
+    sc, pr = _last_head_scores(c)
+    for tag, v in (("SCORES", sc), ("PROBS", pr)):
+        m, e = sim.tile_quantize(_pad16(v, MC))
+        assert (m.reshape(-1)[:MC] == f[f"{tag}_m"]).all(), tag
+        assert (np.full(MC, e[0]) == f[f"{tag}_e"]).all(), tag
+
+
 def _cfg1_case():
     from bfp import Dims, synth
     f = np.load(GOLDEN / "ref_layer_cfg1.npz")

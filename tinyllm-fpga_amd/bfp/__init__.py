@@ -14,8 +14,9 @@ binding of libbfp.so).
 from .dims import Dims, TILE, LANES  # noqa: F401
 
 
-_API = ("tile_quantize", "tile_decode", "fp_quantize_vec", "quantize_W", "matvec_hw_golden",
-        "matvec_bfp", "PackedMatrix")
+_API = ("tile_quantize", "tile_decode", "fp_quantize_vec", "tile_encode", "quantize_W",
+        "matvec_hw_golden", "matvec_bfp", "PackedMatrix", "rmsnorm_fp", "silu_fp", "softmax_fp",
+        "rope_fp", "fwd_layer")
 
 
 def __getattr__(name):

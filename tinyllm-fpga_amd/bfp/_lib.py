@@ -51,11 +51,17 @@ SIGNATURES = {
     "bfp_tile_quantize_f32_d": (i32, [vp, sz, vp, vp, vp]),
     "bfp_quantize_pack_f32_d": (i32, [vp, i32, i32, vp, vp, vp]),
     "bfp_tile_decode_d": (i32, [vp, vp, sz, vp, vp]),
+    "bfp_tile_encode_f64_d": (i32, [vp, sz, vp, vp, vp, vp]),
+    "bfp_rmsnorm_fp_d": (i32, [vp, vp, i32, i32, C.c_double, vp, vp]),
+    "bfp_silu_fp_d": (i32, [vp, sz, vp, vp]),
+    "bfp_softmax_fp_d": (i32, [vp, i32, i32, vp, vp]),
+    "bfp_rope_cos_sin": (i32, [i32, i32, C.c_double, vp]),
+    "bfp_rope_fp_d": (i32, [vp, i32, vp, vp, vp]),
     "bfp_matvec_d": (i32, [vp, vp, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64, i32, vp]),
     "bfp_matvec_ring_d": (i32, [vp, vp, i32, i32, i32, i32, i64, i64, vp, vp, i64, vp, vp, i64,
                                 i32, vp]),
     "bfp_matvec_h": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
-    "bfp_probe_read_d": (i32, [vp, sz, vp, i32, vp]),
+    "bfp_probe_read_d": (i32, [vp, sz, vp, i32, i32, vp]),
     "bfp_pack_wide_d": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "bfp_load_weights_wide": (i32, [vp, i32, i32, vp, vp]),
     "bfp_rtl_tables": (i32, [vp, vp, vp, i32, C.c_double]),
@@ -74,6 +80,9 @@ SIGNATURES = {
     "bfp_reset_kv": (i32, [vp]),
     "bfp_kv_io": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32]),
     "bfp_layer_step": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, C.POINTER(StageDumpC)]),
+    "bfp_layer_step_kv": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, C.POINTER(StageDumpC)]),
+    "bfp_kv_io_f64": (i32, [vp, i32, i32, i32, i32, vp, vp, i32]),
+    "bfp_matvec": (i32, [vp, vp, vp, i32, i32, i32, vp, vp]),
     "bfp_rtl_layer_step": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, C.POINTER(StageDumpC)]),
     "bfp_head": (i32, [vp, i32, vp, vp, vp, vp]),
     "bfp_rtl_head": (i32, [vp, vp, vp, vp, vp, vp]),

@@ -51,6 +51,82 @@ def fp_quantize_vec(v):
     return tile_decode(*tile_quantize(v))
 
 
+def tile_encode(v, strict=True):
+    """The BFP tiles of float64 values that are already BFP (decoded tiles,
+    as the reference's arrays hold them): tile_decode(*tile_encode(v)) == v.
+    Equal to tile_quantize except for the raw form of a tile whose largest
+    magnitude is the mantissa -32768, which tile_quantize would re-round.
+    strict: raise ValueError when v holds a value that is not BFP-exact."""
+    a = _flat_f64(v)
+    n = a.size
+    dv = _dev.to_dev(a)
+    m = _dev.empty(n, "int16")
+    e = _dev.empty(n // TILE, "int8")
+    flag = _dev.zeros(1, "int32")
+    call("bfp_tile_encode_f64_d", _dev.ptr(dv), n, _dev.ptr(m), _dev.ptr(e), _dev.ptr(flag),
+         _dev.stream())
+    if strict and int(_dev.to_host(flag)[0]):
+        raise ValueError("values are not BFP tiles (16 int16 mantissas sharing an exponent)")
+    return _dev.to_host(m).reshape(-1, TILE), _dev.to_host(e)
+
+
+# ------------------------------------------------------------ float64 leaf ops
+def rmsnorm_fp(x, gamma, eps=1e-5):
+    """full.py:236-238: fp_quantize_vec((x*gamma) / np.sqrt(np.mean(x*x) + eps))."""
+    xa, ga = _flat_f64(x), _flat_f64(gamma)
+    if xa.size != ga.size:
+        raise ValueError(f"x has {xa.size} values, gamma {ga.size}")
+    dx, dg = _dev.to_dev(xa), _dev.to_dev(ga)
+    y = _dev.empty(xa.size, "float64")
+    call("bfp_rmsnorm_fp_d", _dev.ptr(dx), _dev.ptr(dg), xa.size, 1, float(eps), _dev.ptr(y),
+         _dev.stream())
+    return _dev.to_host(y)
+
+
+def silu_fp(x):
+    """full.py:241-242: fp_quantize_vec(x / (1.0 + np.exp(-x)))."""
+    xa = _flat_f64(x)
+    dx = _dev.to_dev(xa)
+    y = _dev.empty(xa.size, "float64")
+    call("bfp_silu_fp_d", _dev.ptr(dx), xa.size, _dev.ptr(y), _dev.stream())
+    return _dev.to_host(y)
+
+
+def softmax_fp(x):
+    """full.py:245-247: e = np.exp(x - x.max()); e / e.sum() (float64)."""
+    xa = np.ascontiguousarray(np.asarray(x, dtype=np.float64).reshape(-1))
+    if xa.size == 0:
+        raise ValueError("softmax of an empty vector")
+    dx = _dev.to_dev(xa)
+    y = _dev.empty(xa.size, "float64")
+    call("bfp_softmax_fp_d", _dev.ptr(dx), xa.size, 1, _dev.ptr(y), _dev.stream())
+    return _dev.to_host(y)
+
+
+def rope_fp(x, pos, base=10000.0):
+    """full.py:250-258 on one 64-wide head (or several, each rotated on its
+    own): out[j] = a*c - b*s, out[j+32] = b*c + a*s, then fp_quantize_vec."""
+    xa = np.ascontiguousarray(np.asarray(x, dtype=np.float64).reshape(-1))
+    if xa.size % 64 or xa.size == 0:
+        raise ValueError(f"rope_fp works on heads of 64 values, got {xa.size}")
+    cs = np.empty(64, np.float64)
+    call("bfp_rope_cos_sin", int(pos), 64, float(base), cs.ctypes.data)
+    dx, dc = _dev.to_dev(xa), _dev.to_dev(cs)
+    y = _dev.empty(xa.size, "float64")
+    call("bfp_rope_fp_d", _dev.ptr(dx), xa.size // 64, _dev.ptr(dc), _dev.ptr(y), _dev.stream())
+    return _dev.to_host(y)
+
+
+def fwd_layer(h, lw, pos, kv, kv_pos):
+    """full.py:261-293 with the reference's own arguments: ``lw`` a dict of
+    (m, e) weight tuples 'Wq'..'Wd' (quantize_W layout) and BFP-exact float64
+    gammas 'g1', 'g2'; ``kv`` {'k', 'v'} float64 arrays (MAX_CTX, H_KV, HD),
+    updated in place at ``kv_pos``.  RoPE at ``pos``, attention over slots
+    0..kv_pos.  Returns the float64 layer output.  See bfp.layer."""
+    from .layer import fwd_layer as _fwd
+    return _fwd(h, lw, pos, kv, kv_pos)
+
+
 def quantize_W(W):
     """full.py:110-119: row-wise tile quantisation -> (m (out, in/16, 16),
     e (out, in/16))."""

@@ -118,9 +118,39 @@ class BfpModel:
         d = self.dims
         return {"K": d.KV, "V": d.KV, "G": d.FFN, "U": d.FFN, "MLP": d.FFN}.get(name, d.D)
 
-    def layer_step_bfp(self, layer, pos, h_m, h_e, dump=False):
-        """fwd_layer on BFP input (batch, D) / (batch, D/16); returns
-        (out_m, out_e, stages) where stages maps stage name -> (m, e)."""
+    def kv_io_f64(self, layer, seq, t0, n, k=None, v=None):
+        """The cache rows [t0, t0+n) as the reference holds them: float64
+        (n, H_KV, HD) arrays.  Read (k, v None) or write (exact encoding;
+        ValueError-like BfpError for values that are not BFP tiles)."""
+        d = self.dims
+        if k is None:
+            kk = np.zeros((n, d.H_KV, d.HD), np.float64)
+            vv = np.zeros_like(kk)
+            call("bfp_kv_io_f64", self._h, layer, seq, t0, n, _p(kk), _p(vv), 0)
+            return kk, vv
+        kk = np.ascontiguousarray(np.asarray(k, dtype=np.float64)).reshape(n, d.KV)
+        vv = np.ascontiguousarray(np.asarray(v, dtype=np.float64)).reshape(n, d.KV)
+        call("bfp_kv_io_f64", self._h, layer, seq, t0, n, _p(kk), _p(vv), 1)
+
+    def matvec(self, name, layer, x_m, x_e):
+        """matvec_hw_golden with this context's matrix `name` ('Wq'..'Wd')
+        of `layer` on BFP input (batch, n_in) / (batch, n_in/16): returns
+        the raw BFP output (y_m (batch, n_out), y_e (batch, n_out/16))."""
+        d = self.dims
+        n_out, n_in = {"Wq": (d.D, d.D), "Wk": (d.KV, d.D), "Wv": (d.KV, d.D), "Wo": (d.D, d.D),
+                       "Wg": (d.FFN, d.D), "Wu": (d.FFN, d.D), "Wd": (d.D, d.FFN)}[name]
+        x_m = _c16(x_m).reshape(-1, n_in)
+        batch = x_m.shape[0]
+        x_e = _c8(x_e).reshape(batch, n_in // 16)
+        ym = np.empty((batch, n_out), np.int16)
+        ye = np.empty((batch, n_out // 16), np.int8)
+        call("bfp_matvec", self._h, _p(x_m), _p(x_e), WHICH[name], layer, batch, _p(ym), _p(ye))
+        return ym, ye
+
+    def layer_step_bfp(self, layer, pos, h_m, h_e, dump=False, kv_pos=None):
+        """fwd_layer on BFP input (batch, D) / (batch, D/16) with RoPE at pos
+        and the K/V slot kv_pos (default pos); returns (out_m, out_e,
+        stages) where stages maps stage name -> (m, e)."""
         h_m = _c16(h_m).reshape(-1, self.dims.D)
         batch = h_m.shape[0]
         h_e = _c8(h_e).reshape(batch, self.dims.D // 16)
@@ -137,8 +167,8 @@ class BfpModel:
                 stages[name] = (sm, se)
                 sd.m[i] = _p(sm)
                 sd.e[i] = _p(se)
-        call("bfp_layer_step", self._h, layer, pos, batch, _p(h_m), _p(h_e), _p(out_m), _p(out_e),
-             C.byref(sd) if sd is not None else None)
+        call("bfp_layer_step_kv", self._h, layer, pos, pos if kv_pos is None else kv_pos, batch,
+             _p(h_m), _p(h_e), _p(out_m), _p(out_e), C.byref(sd) if sd is not None else None)
         return out_m, out_e, stages
 
     def rtl_layer_step(self, layer, pos, h_m, h_e, kv_pos=None, dump=False):
@@ -194,12 +224,13 @@ class BfpModel:
     def fwd_layer(self, h, layer, pos, kv_pos=None):
         """The reference's fwd_layer(h, lw, pos, kv, kv_pos) (full.py:261-293)
         with the layer's weights and KV cache resident in the context:
-        float64 BFP-exact h (D,) in, float64 out."""
+        float64 BFP-exact h (D,) in, float64 out; RoPE at pos, K/V at slot
+        kv_pos (default pos).  bfp.api.fwd_layer takes the reference's own
+        caller-owned lw and kv instead."""
         from . import api
-        if kv_pos is not None and kv_pos != pos:
-            raise ValueError("the device layer step uses kv_pos == pos (as the decode loop does)")
-        m, e = api.tile_quantize(h)
-        om, oe, _ = self.layer_step_bfp(layer, pos, m.reshape(1, -1), e.reshape(1, -1))
+        m, e = api.tile_encode(h)
+        om, oe, _ = self.layer_step_bfp(layer, pos, m.reshape(1, -1), e.reshape(1, -1),
+                                        kv_pos=kv_pos)
         return api.tile_decode(om[0], oe[0])
 
     # ----------------------------------------------------------------- head

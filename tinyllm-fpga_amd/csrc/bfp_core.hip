@@ -87,10 +87,18 @@ __global__ void unpack_e_kernel(const int8_t *__restrict__ Pe, long long total, 
 }
 
 // ------------------------------------------------------------ quantisation
-// One thread per 16-element tile.
-template <typename T>
+// One thread per 16-element tile.  EXACT: the encoding of values that are
+// already BFP (decoded tiles, as the reference's float64 arrays hold them):
+// tile_quantize's (canonical) tile, unless it rounds a value, in which case
+// the tile with exponent one lower is taken when it holds every value
+// exactly -- the raw form of a tile whose largest magnitude is the mantissa
+// -32768 (value -2^e), which tile_quantize maps to exponent e + 1 and
+// rounds odd mantissas.  Values that are not BFP-exact either way get
+// tile_quantize's tile.
+template <typename T, bool EXACT = false>
 __global__ void tile_quantize_kernel(const T *__restrict__ v, long long n_tiles,
-                                     int16_t *__restrict__ m, int8_t *__restrict__ e) {
+                                     int16_t *__restrict__ m, int8_t *__restrict__ e,
+                                     int *__restrict__ inexact = nullptr) {
   long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x;
   if (i >= n_tiles) return;
   double x[TILE];
@@ -104,6 +112,28 @@ __global__ void tile_quantize_kernel(const T *__restrict__ v, long long n_tiles,
   int mm[TILE];
 #pragma unroll
   for (int k = 0; k < TILE; ++k) mm[k] = tile_mant_of(x[k], ex);
+  if constexpr (EXACT) {
+    bool same = true;
+#pragma unroll
+    for (int k = 0; k < TILE; ++k) same = same && ldexp((double)mm[k], ex - 15) == x[k];
+    if (!same) {
+      bool raw = ex > -127;
+      int rm[TILE];
+#pragma unroll
+      for (int k = 0; k < TILE; ++k) {
+        const double s = ldexp(x[k], 16 - ex);
+        raw = raw && s == rint(s) && s >= -32768.0 && s <= 32767.0;
+        rm[k] = raw ? (int)s : 0;
+      }
+      if (raw) {
+        --ex;
+#pragma unroll
+        for (int k = 0; k < TILE; ++k) mm[k] = rm[k];
+      } else if (inexact) {
+        *inexact = 1;   // not BFP-exact: tile_quantize's tile stands
+      }
+    }
+  }
   uint4 lo, hi;
   lo.x = (mm[0] & 0xffff) | (mm[1] << 16);
   lo.y = (mm[2] & 0xffff) | (mm[3] << 16);
@@ -211,7 +241,7 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
     const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
     long long smat_e, int nT, int n_chunks, int ring, const int16_t *__restrict__ xm,
     const int8_t *__restrict__ xe, long long x_stride, int16_t *__restrict__ ym,
-    int8_t *__restrict__ ye, long long y_stride) {
+    int8_t *__restrict__ ye, long long y_stride, int cstride) {
   extern __shared__ int smem[];
   int *xs = smem;              // nT * 16
   int *xes = smem + nT * 16;   // nT
@@ -223,8 +253,9 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
   const int wmat = ring > 0 ? mat % ring : mat;
 
   ChunkRegs<TPT> R;
-  load_chunk<NW, TPT, true>(R, Pm + wmat * smat_m + (long long)c * nT * 32,
-                            Pe + wmat * smat_e + (long long)c * nT * 16, nT);
+  const long long cc = (long long)c * cstride;   // chunk c of this matrix in the layout
+  load_chunk<NW, TPT, true>(R, Pm + wmat * smat_m + cc * nT * 32, Pe + wmat * smat_e + cc * nT * 16,
+                            nT);
   stage_x_bfp(xs, xes, xm + mat * x_stride, xe + mat * (x_stride / 16), nT);
   __syncthreads();
   long long A;
@@ -242,8 +273,10 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
 // Read-only streaming probe: workgroup w reads the contiguous range
 // [w*per, (w+1)*per) of 16-byte words, eight loads in flight per thread
 // (addresses clamped, so there is no branch around a load), folded into one
-// word per workgroup so the loads cannot be dropped.  Measures the
-// practical HBM read ceiling with the access pattern of the streaming matvec.
+// word per workgroup so the loads cannot be dropped.  NT: the loads carry
+// the non-temporal cache policy, as the matvec's weight stream does.
+// Measures the practical HBM read ceiling the matvec is compared with.
+template <bool NT>
 __global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *__restrict__ p,
                                                          long long n16, long long per,
                                                          unsigned *__restrict__ out) {
@@ -255,7 +288,8 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *__restrict
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       long long i = b + k * 256 + threadIdx.x;
-      v[k] = p[i < i1 ? i : i1 - 1];
+      i = i < i1 ? i : i1 - 1;
+      v[k] = NT ? ld_nt(p + i) : p[i];
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
@@ -284,7 +318,7 @@ __global__ __launch_bounds__(128) void embed_gather_kernel(const uint4 *__restri
 
 typedef void (*matvec_fn)(const uint4 *, const int8_t *, long long, long long, int, int, int,
                           const int16_t *, const int8_t *, long long, int16_t *, int8_t *,
-                          long long);
+                          long long, int);
 
 template <int NW>
 static matvec_fn pick_tpt(int tpt) {
@@ -326,8 +360,9 @@ int default_waves(int nT) {
 int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats, int ring,
                   long long smat_m, long long smat_e, const int16_t *x_m, const int8_t *x_e,
                   long long x_stride, int16_t *y_m, int8_t *y_e, long long y_stride, int waves,
-                  hipStream_t stream) {
-  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || n_mats <= 0 || ring < 0)
+                  hipStream_t stream, int cstride) {
+  if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 16 || n_mats <= 0 || ring < 0 ||
+      cstride < 1)
     return set_err(BFP_EINVAL, "matvec: bad shape n_out=%d n_in=%d n_mats=%d ring=%d", n_out,
                    n_in, n_mats, ring);
   if (!P_m || !P_e || !x_m || !x_e || !y_m || !y_e)
@@ -354,7 +389,7 @@ int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_m
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * nw), shm, stream,
                      reinterpret_cast<const uint4 *>(P_m), reinterpret_cast<const int8_t *>(P_e),
                      smat_m / 16, smat_e, nT, n_chunks, ring, x_m, x_e, x_stride, y_m, y_e,
-                     y_stride);
+                     y_stride, cstride);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return set_err(BFP_EIO, "matvec launch: %s", hipGetErrorString(err));
   return BFP_OK;
@@ -405,6 +440,16 @@ int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e,
   hipLaunchKernelGGL(quantize_pack_f32_kernel, dim3(nblk(total, 256)), dim3(256), 0, s, W, total,
                      nT, cstride, reinterpret_cast<uint4 *>(P_m), reinterpret_cast<int8_t *>(P_e));
   return launch_status("quantize_pack");
+}
+
+int tile_encode_f64(const double *v, size_t n, int16_t *m, int8_t *e, int *inexact,
+                    hipStream_t s) {
+  if (n % 16 || !v || !m || !e) return set_err(BFP_EINVAL, "tile_encode: n=%zu", n);
+  if (n == 0) return BFP_OK;
+  long long nt = (long long)(n / 16);
+  hipLaunchKernelGGL((tile_quantize_kernel<double, true>), dim3(nblk(nt, 256)), dim3(256), 0, s, v,
+                     nt, m, e, inexact);
+  return launch_status("tile_encode");
 }
 
 int tile_quantize_f64(const double *v, size_t n, int16_t *m, int8_t *e, hipStream_t s) {
@@ -458,6 +503,11 @@ int bfp_tile_quantize_f64_d(const double *v, size_t n, int16_t *m, int8_t *e, vo
   return bfp::tile_quantize_f64(v, n, m, e, (hipStream_t)stream);
 }
 
+int bfp_tile_encode_f64_d(const double *v, size_t n, int16_t *m, int8_t *e, int *inexact,
+                          void *stream) {
+  return bfp::tile_encode_f64(v, n, m, e, inexact, (hipStream_t)stream);
+}
+
 int bfp_tile_quantize_f32_d(const float *v, size_t n, int16_t *m, int8_t *e, void *stream) {
   if (n % 16 || !v || !m || !e) return set_err(BFP_EINVAL, "tile_quantize: n=%zu", n);
   if (n == 0) return BFP_OK;
@@ -501,14 +551,17 @@ int bfp_pack_wide_d(const void *wide_m, const void *wide_e, int n_out, int n_in,
   return bfp::pack_wide(wide_m, wide_e, n_out, n_in, P_m, P_e, (hipStream_t)stream);
 }
 
-int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, void *stream) {
-  if (!p || !out || n_wg <= 0 || bytes % 16)
+int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, int nt,
+                     void *stream) {
+  if (!p || !out || n_wg <= 0 || bytes % 16 || bytes == 0)
     return set_err(BFP_EINVAL, "probe_read: bad arguments (bytes=%zu n_wg=%d)", bytes, n_wg);
   const long long n16 = (long long)(bytes / 16);
   const long long per = (n16 + n_wg - 1) / n_wg;
-  hipLaunchKernelGGL(probe_read_kernel, dim3(n_wg), dim3(256), 0, (hipStream_t)stream,
-                     reinterpret_cast<const uint4 *>(p), n16, per,
-                     reinterpret_cast<unsigned *>(out));
+  if ((long long)(n_wg - 1) * per >= n16)
+    return set_err(BFP_EINVAL, "probe_read: %d workgroups leave some without words", n_wg);
+  hipLaunchKernelGGL(nt ? probe_read_kernel<true> : probe_read_kernel<false>, dim3(n_wg),
+                     dim3(256), 0, (hipStream_t)stream, reinterpret_cast<const uint4 *>(p), n16,
+                     per, reinterpret_cast<unsigned *>(out));
   return launch_status("probe_read");
 }
 

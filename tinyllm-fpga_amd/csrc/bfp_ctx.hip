@@ -23,6 +23,7 @@ struct bfp_ctx {
   size_t s_qkv_m = 0, s_o_m = 0, s_gu_m = 0, s_d_m = 0;
   size_t s_qkv_e = 0, s_o_e = 0, s_gu_e = 0, s_d_e = 0;
   double *g1 = nullptr, *g2 = nullptr, *norm_w = nullptr, *rope = nullptr;
+  double *rope_row = nullptr;   // one (cos, sin) row for a position past the table
   float *embed = nullptr;
   // activations (max_batch sequences)
   int16_t *h_m = nullptr, *h1_m = nullptr, *qkv_am = nullptr, *att_m = nullptr, *mlp_m = nullptr;
@@ -87,18 +88,11 @@ int check_dims(const bfp_dims &d) {
   return BFP_OK;
 }
 
-// RoPE table with the reference's own float expressions (full.py:253-254):
-// theta = 1.0 / (base ** (2*j/HD)) * pos, evaluated by the host's libm as
-// CPython's float ** and math.cos/sin do (both call pow/cos/sin).
+// RoPE table of positions 0 .. max_ctx-1 with the reference's own float
+// expressions (full.py:253-254, rope_row).
 void rope_table(std::vector<double> &t, int max_ctx, int HD) {
   t.resize((size_t)max_ctx * HD);
-  const int h2 = HD / 2;
-  for (int pos = 0; pos < max_ctx; ++pos)
-    for (int j = 0; j < h2; ++j) {
-      double theta = 1.0 / pow(10000.0, (double)(2 * j) / (double)HD) * (double)pos;
-      t[((size_t)pos * h2 + j) * 2] = cos(theta);
-      t[((size_t)pos * h2 + j) * 2 + 1] = sin(theta);
-    }
+  for (int pos = 0; pos < max_ctx; ++pos) rope_row(t.data() + (size_t)pos * HD, pos, HD, 10000.0);
 }
 
 // Workgroups of the head for `batch` sequences, and the most any batch uses.
@@ -159,6 +153,7 @@ LayerArgs layer_args(bfp_ctx *c, int layer, int batch) {
   a.v_e = c->v_e + layer * c->s_kv_e;
   a.layer = layer;
   a.NL = d.NL;
+  a.kv_pos_const = -1;
   return a;
 }
 
@@ -227,6 +222,7 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->g2, sizeof(double) * d.D * d.NL)) ||
       (rc = c->alloc((void **)&c->norm_w, sizeof(double) * d.D)) ||
       (rc = c->alloc((void **)&c->rope, sizeof(double) * rope.size())) ||
+      (rc = c->alloc((void **)&c->rope_row, sizeof(double) * d.HD)) ||
       (rc = c->alloc((void **)&c->embed, sizeof(float) * (size_t)d.VOCAB * d.D)) ||
       (rc = c->alloc((void **)&c->h_m, 2 * B * d.D)) || (rc = c->alloc((void **)&c->h_e, B * d.D / 16)) ||
       (rc = c->alloc((void **)&c->h1_m, 2 * B * d.D)) ||
@@ -466,23 +462,33 @@ int bfp_kv_io(bfp_ctx *c, int layer, int seq, int t0, int n, int16_t *k_m, int8_
   return BFP_OK;
 }
 
-// fwd_layer (full.py:261-293) for `batch` sequences at position pos
-// (kv_pos = pos).  h in/out are host arrays (batch x D mantissas, batch x
-// D/16 exponents); dump (optional) receives every stage.
-int bfp_layer_step(bfp_ctx *c, int layer, int pos, int batch, const int16_t *h_m,
-                   const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump) {
+// fwd_layer (full.py:261-293) for `batch` sequences: RoPE at position pos,
+// K/V written at slot kv_pos, attention over slots 0..kv_pos.  h in/out are
+// host arrays (batch x D mantissas, batch x D/16 exponents); dump (optional)
+// receives every stage.
+int bfp_layer_step_kv(bfp_ctx *c, int layer, int pos, int kv_pos, int batch, const int16_t *h_m,
+                      const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump) {
   if (!c || !h_m || !h_e || !out_m || !out_e) return set_err(BFP_EINVAL, "null argument");
   const bfp_dims &d = c->d;
   if (layer < 0 || layer >= d.NL) return set_err(BFP_EINVAL, "layer %d out of range", layer);
   if (batch <= 0 || batch > c->max_batch) return set_err(BFP_EINVAL, "batch %d out of range", batch);
-  if (pos < 0 || pos >= c->max_ctx)
-    return set_err(BFP_ERANGE, "pos %d outside the KV capacity %d", pos, c->max_ctx);
+  if (kv_pos < 0 || kv_pos >= c->max_ctx)
+    return set_err(BFP_ERANGE, "kv_pos %d outside the KV capacity %d", kv_pos, c->max_ctx);
+  if (pos < 0) return set_err(BFP_ERANGE, "pos %d is negative", pos);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t s = c->stream;
   HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)batch * d.D * 2, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)batch * d.D / 16, hipMemcpyHostToDevice, s));
   LayerArgs a = layer_args(c, layer, batch);
   a.pos_const = pos;
+  a.kv_pos_const = kv_pos;
+  std::vector<double> row;
+  if (pos >= c->max_ctx) {   // past the table: this position's row, same expressions
+    row.resize(d.HD);
+    rope_row(row.data(), pos, d.HD, 10000.0);
+    HIP_TRY(hipMemcpyAsync(c->rope_row, row.data(), sizeof(double) * d.HD, hipMemcpyHostToDevice, s));
+    a.rope_row = c->rope_row;
+  }
   DevBuf tmp;
   StageDump sd;
   int len[ST_COUNT];
@@ -509,6 +515,111 @@ int bfp_layer_step(bfp_ctx *c, int layer, int pos, int batch, const int16_t *h_m
                                hipMemcpyDeviceToHost, s));
     }
   }
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+int bfp_layer_step(bfp_ctx *c, int layer, int pos, int batch, const int16_t *h_m,
+                   const int8_t *h_e, int16_t *out_m, int8_t *out_e, bfp_stage_dump *dump) {
+  return bfp_layer_step_kv(c, layer, pos, pos, batch, h_m, h_e, out_m, out_e, dump);
+}
+
+int bfp_kv_io_f64(bfp_ctx *c, int layer, int seq, int t0, int n, double *k, double *v,
+                  int write) {
+  if (!c || (n > 0 && (!k || !v))) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  if (layer < 0 || layer >= d.NL || seq < 0 || seq >= c->max_batch || t0 < 0 || n < 0 ||
+      t0 + n > c->max_ctx)
+    return set_err(BFP_ERANGE, "kv_io_f64: layer %d seq %d positions [%d, %d) out of range",
+                   layer, seq, t0, t0 + n);
+  if (n == 0) return BFP_OK;
+  HIP_TRY(hipSetDevice(c->device));
+  const size_t KV = (size_t)d.H_KV * d.HD, cnt = (size_t)n * KV;
+  const size_t om = layer * c->s_kv_m + ((size_t)seq * c->max_ctx + t0) * KV;
+  const size_t oe = layer * c->s_kv_e + ((size_t)seq * c->max_ctx + t0) * KV / 16;
+  hipStream_t s = c->stream;
+  DevBuf tmp;
+  double *dk, *dv;
+  int *flag;
+  BFP_TRY(tmp.alloc((void **)&dk, cnt * sizeof(double)));
+  BFP_TRY(tmp.alloc((void **)&dv, cnt * sizeof(double)));
+  BFP_TRY(tmp.alloc((void **)&flag, sizeof(int)));
+  if (write) {
+    int inexact = 0;
+    HIP_TRY(hipMemcpyAsync(flag, &inexact, sizeof(int), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(dk, k, cnt * sizeof(double), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(dv, v, cnt * sizeof(double), hipMemcpyHostToDevice, s));
+    BFP_TRY(tile_encode_f64(dk, cnt, c->k_m + om, c->k_e + oe, flag, s));
+    BFP_TRY(tile_encode_f64(dv, cnt, c->v_m + om, c->v_e + oe, flag, s));
+    HIP_TRY(hipMemcpyAsync(&inexact, flag, sizeof(int), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (inexact)
+      return set_err(BFP_EINVAL, "kv_io_f64: positions [%d, %d) hold values that are not BFP tiles",
+                     t0, t0 + n);
+    return BFP_OK;
+  } else {
+    BFP_TRY(bfp_tile_decode_d(c->k_m + om, c->k_e + oe, cnt, dk, s));
+    BFP_TRY(bfp_tile_decode_d(c->v_m + om, c->v_e + oe, cnt, dv, s));
+    HIP_TRY(hipMemcpyAsync(k, dk, cnt * sizeof(double), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(v, dv, cnt * sizeof(double), hipMemcpyDeviceToHost, s));
+  }
+  HIP_TRY(hipStreamSynchronize(s));
+  return BFP_OK;
+}
+
+int bfp_matvec(bfp_ctx *c, const int16_t *x_m, const int8_t *x_e, int which, int layer,
+               int batch, int16_t *y_m, int8_t *y_e) {
+  if (!c || !x_m || !x_e || !y_m || !y_e) return set_err(BFP_EINVAL, "null argument");
+  const bfp_dims &d = c->d;
+  const int KV = d.H_KV * d.HD;
+  if (layer < 0 || layer >= d.NL) return set_err(BFP_EINVAL, "layer %d out of range", layer);
+  if (batch <= 0) return set_err(BFP_EINVAL, "batch %d must be positive", batch);
+  int n_out = d.D, n_in = d.D, cstride = 1;
+  const uint8_t *Pm = nullptr;
+  const int8_t *Pe = nullptr;
+  switch (which) {
+    case BFP_WQ: case BFP_WK: case BFP_WV: {
+      const int row0 = which == BFP_WQ ? 0 : (which == BFP_WK ? d.D : d.D + KV);
+      n_out = which == BFP_WQ ? d.D : KV;
+      Pm = c->qkv_m + layer * c->s_qkv_m + (size_t)row0 * d.D * 2;
+      Pe = c->qkv_e + layer * c->s_qkv_e + (size_t)row0 * d.D / 16;
+      break;
+    }
+    case BFP_WO:
+      Pm = c->o_m + layer * c->s_o_m;
+      Pe = c->o_e + layer * c->s_o_e;
+      break;
+    case BFP_WG: case BFP_WU: {
+      n_out = d.FFN;
+      cstride = 2;                                  // chunks interleaved G0 U0 G1 U1 ...
+      const size_t off = which == BFP_WG ? 0 : 1;
+      Pm = c->gu_m + layer * c->s_gu_m + off * (size_t)16 * d.D * 2;
+      Pe = c->gu_e + layer * c->s_gu_e + off * (size_t)16 * d.D / 16;
+      break;
+    }
+    case BFP_WD:
+      n_in = d.FFN;
+      Pm = c->d_m + layer * c->s_d_m;
+      Pe = c->d_e + layer * c->s_d_e;
+      break;
+    default:
+      return set_err(BFP_EINVAL, "matvec: slot %d is not a matrix (BFP_WQ .. BFP_WD)", which);
+  }
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  DevBuf tmp;
+  int16_t *dxm, *dym;
+  int8_t *dxe, *dye;
+  BFP_TRY(tmp.alloc((void **)&dxm, (size_t)batch * n_in * 2));
+  BFP_TRY(tmp.alloc((void **)&dxe, (size_t)batch * n_in / 16));
+  BFP_TRY(tmp.alloc((void **)&dym, (size_t)batch * n_out * 2));
+  BFP_TRY(tmp.alloc((void **)&dye, (size_t)batch * n_out / 16));
+  HIP_TRY(hipMemcpyAsync(dxm, x_m, (size_t)batch * n_in * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(dxe, x_e, (size_t)batch * n_in / 16, hipMemcpyHostToDevice, s));
+  BFP_TRY(launch_matvec(Pm, Pe, n_out, n_in, batch, 1, 0, 0, dxm, dxe, n_in, dym, dye, n_out, 0, s,
+                        cstride));
+  HIP_TRY(hipMemcpyAsync(y_m, dym, (size_t)batch * n_out * 2, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(y_e, dye, (size_t)batch * n_out / 16, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   return BFP_OK;
 }

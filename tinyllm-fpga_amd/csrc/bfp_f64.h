@@ -214,4 +214,20 @@ __device__ __forceinline__ int quantize16_lanes(double v, int &e, bool canonical
 
 __device__ __forceinline__ double bfp_val(int m, int e) { return ldexp((double)m, e - 15); }
 
+// RoPE of one 64-wide head held one value per lane of a wave (lane l holds
+// element l, pre-rotation x), re-quantised: returns the lane's mantissa.
+__device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
+  const int l = threadIdx.x & 63;
+  const int j = l & 31;
+  double other = peer<32>(x);              // the partner element j+32 / j
+  double c = cs[2 * j], s = cs[2 * j + 1];
+  double out;
+  if (l < 32) {
+    out = x * c - other * s;                 // a*c - b*s
+  } else {
+    out = x * c + other * s;                 // b*c + a*s
+  }
+  return quantize16_lanes(out, e);
+}
+
 }  // namespace bfp

@@ -51,7 +51,7 @@ int default_waves(int nT);
 int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_mats, int ring,
                   long long smat_m, long long smat_e, const int16_t *x_m, const int8_t *x_e,
                   long long x_stride, int16_t *y_m, int8_t *y_e, long long y_stride, int waves,
-                  hipStream_t stream);
+                  hipStream_t stream, int cstride = 1);
 int pack(const int16_t *W_m, const int8_t *W_e, int n_out, int n_in, void *P_m, void *P_e,
          hipStream_t s, int cstride = 1);
 int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e, hipStream_t s,
@@ -59,6 +59,9 @@ int quantize_pack_f32(const float *W, int n_out, int n_in, void *P_m, void *P_e,
 int pack_wide(const void *wide_m, const void *wide_e, int n_out, int n_in, void *P_m, void *P_e,
               hipStream_t s, int cstride = 1);
 int tile_quantize_f64(const double *v, size_t n, int16_t *m, int8_t *e, hipStream_t s);
+int tile_encode_f64(const double *v, size_t n, int16_t *m, int8_t *e, int *inexact,
+                    hipStream_t s);
+void rope_row(double *cs, int pos, int HD, double base);
 
 }  // namespace bfp
 

@@ -43,7 +43,11 @@ struct LayerArgs {
   int16_t *k_m; int8_t *k_e;
   int16_t *v_m; int8_t *v_e;
   const int *pos_ptr;       // device position (== kv_pos); read when non-null
-  int pos_const;
+  int pos_const;            // RoPE position when pos_ptr is null
+  int kv_pos_const;         // KV slot when pos_ptr is null and >= 0 (attention over
+                            // slots 0..kv_pos); -1: kv_pos = pos
+  const double *rope_row;   // when non-null: the (HD/2) x (cos, sin) row of this
+                            // launch's RoPE position (positions past the table)
   const StageDump *dump;    // device pointer or null
   // h_out history for per-(step, layer) checks: ((b*hist_steps + pos)*NL + layer)*D
   int16_t *hist_m; int8_t *hist_e;

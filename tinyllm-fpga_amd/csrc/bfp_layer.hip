@@ -12,6 +12,10 @@
 // Every launch handles `batch` independent sequences (grid.y).
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "bfp.h"
 #include "bfp_device.h"
 #include "bfp_f64.h"
@@ -31,6 +35,14 @@ __device__ __forceinline__ void canon_copy(int m, int e, int &cm, int &ce) {
 
 __device__ __forceinline__ int cur_pos(const LayerArgs &a) {
   return a.pos_ptr ? *a.pos_ptr : a.pos_const;
+}
+
+// The KV slot of this step: the position itself in the decode loop
+// (full.py:436), or the caller's kv_pos (fwd_layer's separate argument,
+// full.py:261, which the single-layer harness sets apart from pos,
+// gen_smollm_blockfp_bfp.py:42-43).
+__device__ __forceinline__ int cur_kv_pos(const LayerArgs &a) {
+  return a.pos_ptr ? *a.pos_ptr : (a.kv_pos_const >= 0 ? a.kv_pos_const : a.pos_const);
 }
 
 // rmsnorm_fp (full.py:236-238) of a BFP vector, re-quantised, into the
@@ -263,21 +275,6 @@ __global__ __launch_bounds__(64 * NW) void k_qkv(LayerArgs a) {
 }
 
 // ------------------------------------------------------------------ attn
-// RoPE of one 64-wide head held one value per lane of a wave (lane l holds
-// element l, pre-rotation x), re-quantised: returns the lane's mantissa.
-__device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
-  const int l = threadIdx.x & 63;
-  const int j = l & 31;
-  double other = peer<32>(x);              // the partner element j+32 / j
-  double c = cs[2 * j], s = cs[2 * j + 1];
-  double out;
-  if (l < 32) {
-    out = x * c - other * s;                 // a*c - b*s
-  } else {
-    out = x * c + other * s;                 // b*c + a*s
-  }
-  return quantize16_lanes(out, e);
-}
 
 // Attention of one q head (full.py:268-283) in workgroups of ATT_WAVES
 // waves:
@@ -370,13 +367,14 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? (PPW == 3 ? 6 : 4) : 2)) v
   const bool lead = dg == 0;                             // stores the cache row and the dumps
   const int grp = a.H_Q / a.H_KV, g = hq / grp;
   const int HD = 64;
-  const int pos = cur_pos(a);
+  const int pos = cur_kv_pos(a);                       // KV slot: attention over 0..pos
   const int n = pos + 1;
   const int nq = a.D + 2 * a.KV;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int16_t *qm = a.qkv_m + b * nq;
   const int8_t *qe = a.qkv_e + b * (nq / 16);
-  const double *cs = a.rope + (long long)pos * HD;     // (HD/2) x (cos, sin)
+  const double *cs = a.rope_row ? a.rope_row                 // (HD/2) x (cos, sin)
+                                : a.rope + (long long)cur_pos(a) * HD;
   const long long kv_tok = (long long)a.H_KV * HD;     // elements per position
   int16_t *Km = a.k_m + (long long)b * a.max_ctx * kv_tok;
   int8_t *Ke = a.k_e + (long long)b * a.max_ctx * (kv_tok / 16);
@@ -1433,13 +1431,29 @@ static lk_fn attn_kernel(int ppw) {
   return ppw == 2 ? k_attn<2, true> : (ppw == 3 ? k_attn<3, true> : (ppw == 4 ? k_attn<4, true> : k_attn<8, false>));
 }
 
+// Raise a kernel's dynamic-LDS limit on the current device to at least
+// `bytes`, never lowering it: the limit is process-wide per device, and
+// another context may already launch the same kernel with a larger need.
+static int raise_lds_limit(const void *f, int bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void *>, int> limit;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  int &cur = limit[std::make_pair(dev, f)];
+  if (bytes > cur) {
+    HIP_TRY(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    cur = bytes;
+  }
+  return BFP_OK;
+}
+
 // Per device, before the first launch (outside any stream capture): allow
 // the dynamic LDS the attention and multi-sequence kernels take.
 int prepare_layer_kernels(int max_ctx, int D, int FFN) {
   const int ppw = attn_ppw(max_ctx);
-  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel(ppw)),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)attn_lds_bytes(max_ctx, ppw)));
+  BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(attn_kernel(ppw)),
+                          (int)attn_lds_bytes(max_ctx, ppw)));
   int nw, tpt, nwf, tptf;
   shape_for(D / 16, nw, tpt);
   shape_for(FFN / 16, nwf, tptf);
@@ -1450,7 +1464,7 @@ int prepare_layer_kernels(int max_ctx, int D, int FFN) {
                        reinterpret_cast<const void *>(pick_dres_m(nwf, tptf))};
   const int sh[4] = {shD, shD, shD, shF};
   for (int i = 0; i < 4; ++i)
-    if (fs[i]) HIP_TRY(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, sh[i]));
+    if (fs[i]) BFP_TRY(raise_lds_limit(fs[i], sh[i]));
   return BFP_OK;
 }
 
@@ -1460,7 +1474,7 @@ static int launch_attn(const LayerArgs &a, hipStream_t s) {
   const int split = ppw == 8 ? ATT_DSPLIT : 1;
   hipLaunchKernelGGL(attn_kernel(ppw), dim3(a.H_Q * split, a.batch), dim3(64 * ATT_WAVES),
                      attn_lds_bytes(a.max_ctx, ppw), s, a);
-  return BFP_OK;
+  return launch_status("attn");
 }
 
 // Waves per workgroup of an MFMA matvec over nT tiles with n_blocks blocks:
@@ -1551,12 +1565,9 @@ int head_workgroups(int vocab, int D, int rows_single, int batch) {
 
 int prepare_head_kernels(int D) {
   const int sh = head_seq_group(D) * D * 8;
-  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<9, 2, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, sh));
-  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<9, 2, false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, sh));
-  HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(k_head_gemv<27, 1, false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, sh));
+  BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<9, 2, true>), sh));
+  BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<9, 2, false>), sh));
+  BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<27, 1, false>), sh));
   return BFP_OK;
 }
 
