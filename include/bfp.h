@@ -205,6 +205,15 @@ int bfp_rtl_residual_d(const int16_t *a_m, const int8_t *a_e, const int16_t *b_m
  * per element); work: 3*batch*n/16 int32 of device scratch. */
 int bfp_rtl_argmax_d(const int16_t *m, const int8_t *e, int n, int batch, int32_t *work,
                      int32_t *idx, void *stream);
+/* No counterpart in the reference: bfp_rtl_argmax_d for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The same kernel and result; its
+ * workspace is the library's static device scratch (3 MiB per GPU, held
+ * until the process ends), so it calls no allocator.  batch * n/16 must be
+ * at most 262144 (e.g. 64 rows of a 65536-entry vocabulary), else
+ * BFP_EINVAL.  Calls that overlap on one GPU share the scratch and race. */
+int bfp_rtl_argmax_static_d(const int16_t *m, const int8_t *e, int n, int batch, int32_t *idx,
+                            void *stream);
 
 /* ------------------------------------------------------------- model */
 /* A context owns one GPU's copy of the model (BFP weights in the device

@@ -73,6 +73,7 @@ SIGNATURES = {
     "bfp_rtl_swiglu_d": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, vp]),
     "bfp_rtl_residual_d": (i32, [vp, vp, vp, vp, i32, vp, vp, vp]),
     "bfp_rtl_argmax_d": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "bfp_rtl_argmax_static_d": (i32, [vp, vp, i32, i32, vp, vp]),
     "bfp_create": (vp, [C.POINTER(DimsC), i32, i32]),
     "bfp_destroy": (None, [vp]),
     "bfp_get_dims": (i32, [vp, C.POINTER(DimsC)]),

@@ -8,6 +8,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "bfp.h"
 #include "bfp_device.h"
 #include "bfp_internal.h"
@@ -959,6 +961,42 @@ __global__ __launch_bounds__(64) void k_rtl_ctl(RtlCtlArgs a) {
 }  // namespace rtl
 }  // namespace bfp
 
+// ---------------------------------------------- allocation-free argmax
+// Scratch of bfp_rtl_argmax_static_d: the per-chunk bests (mantissa,
+// exponent, index) of at most ARGMAX_STATIC_CHUNKS chunks (batch * n/16),
+// in one device-global array per GPU: 3 MiB, held until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): argmax_scratch() looks its address up
+// once per device with hipGetSymbolAddress and hands that out.
+namespace bfp {
+namespace {
+constexpr long long ARGMAX_STATIC_CHUNKS = 262144;
+static __device__ __align__(256) int scratch[3 * ARGMAX_STATIC_CHUNKS];
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+int *g_scratch[SCRATCH_MAX_DEVICES] = {};
+
+int argmax_scratch(int **out) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+    return set_err(BFP_EINVAL, "rtl_argmax_static: device %d beyond the %d supported", dev,
+                   SCRATCH_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return set_err(BFP_EIO, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                     hipGetErrorString(err));
+    g_scratch[dev] = static_cast<int *>(p);
+  }
+  *out = g_scratch[dev];
+  return BFP_OK;
+}
+}  // namespace
+}  // namespace bfp
+
 using namespace bfp;
 
 static inline unsigned nb(long long n, int bs) { return (unsigned)((n + bs - 1) / bs); }
@@ -1051,6 +1089,27 @@ int bfp_rtl_residual_d(const int16_t *a_m, const int8_t *a_e, const int16_t *b_m
   hipLaunchKernelGGL(rtl::k_rtl_residual, dim3(nb(n, 64)), dim3(64), 0, (hipStream_t)stream, a_m,
                      a_e, b_m, b_e, n, y_m, y_e);
   return launch_status("rtl_residual");
+}
+
+// bfp_rtl_argmax_d with its workspace in the library's static device
+// scratch (no allocation).  The kernel writes every chunk's entry before it
+// reads it, so nothing needs clearing between calls; calls that overlap on
+// one GPU share the scratch and race.
+int bfp_rtl_argmax_static_d(const int16_t *m, const int8_t *e, int n, int batch, int32_t *idx,
+                            void *stream) {
+  if (n <= 0 || n % 16 || batch <= 0 || !m || !e || !idx)
+    return set_err(BFP_EINVAL, "rtl_argmax_static: n=%d batch=%d", n, batch);
+  const long long nc = (long long)batch * (n / 16);
+  if (nc > bfp::ARGMAX_STATIC_CHUNKS)
+    return set_err(BFP_EINVAL,
+                   "rtl_argmax_static: batch * n/16 = %lld chunks exceeds the static scratch's "
+                   "%lld (use bfp_rtl_argmax_d with a workspace)",
+                   nc, bfp::ARGMAX_STATIC_CHUNKS);
+  int *w = nullptr;
+  BFP_TRY(bfp::argmax_scratch(&w));
+  hipLaunchKernelGGL(rtl::k_rtl_argmax, dim3(batch), dim3(256), 0, (hipStream_t)stream, m, e, n, w,
+                     w + nc, w + 2 * nc, idx);
+  return launch_status("rtl_argmax_static");
 }
 
 // work: 3 * batch * n/16 ints of device scratch supplied by the caller.
