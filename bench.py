@@ -105,6 +105,9 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode leg")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-3 decode leg")
     ap.add_argument("--decode-reps", type=int, default=3)
+    ap.add_argument("--decode-tokens", type=int, default=64,
+                    help="tokens generated in the config-3 leg (64 = the config; fewer for "
+                         "counter profiles)")
     ap.add_argument("--long", dest="long", action="store_true", default=True,
                     help="run config 4 (long context; on by default)")
     ap.add_argument("--no-long", dest="long", action="store_false", help="skip config 4")
@@ -120,6 +123,9 @@ def parse():
                     help="time a 1 GiB device copy and a 2 GiB streaming read (practical HBM "
                          "ceiling; the copy calibrates rocprof counters; on by default)")
     ap.add_argument("--no-probe", dest="probe", action="store_false")
+    ap.add_argument("--decode-probe", action="store_true",
+                    help="with --decode-only: also run the HBM ceiling probe (its fixed read "
+                         "and copy sizes calibrate rocprof's FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -300,7 +306,7 @@ def _fixture(name):
     return np.load(path) if path.exists() else None
 
 
-def decode_leg(reps):
+def decode_leg(reps, n_gen=64):
     """30-layer SmolLM2-135M-shaped random-init model,
     8-token prompt, 64 greedy tokens.  Timed with HIP events inside
     bfp_decode (device time of the steps that emit the 64 tokens, and of all
@@ -308,15 +314,15 @@ def decode_leg(reps):
     (tests/golden/ref_decode_cfg3.npz)."""
     from bfp import Dims, synth
     from bfp.model import BfpModel
-    n_prompt, n_gen = 8, 64
-    d = Dims(MAX_CTX=n_prompt + n_gen)
+    n_prompt = 8
+    d = Dims(MAX_CTX=n_prompt + 64)
     fm = synth.make_model(d, seed=0)
     prompt = synth.make_prompt(d, n_prompt, seed=0)
     gm = BfpModel(d)
     gm.load_fp32(fm)
     toks, _ = gm.decode(prompt[None, :], n_gen)          # warm-up + graph build
     gen_ms, tot_ms, walls = [], [], []
-    for _ in range(reps):
+    for _ in range(max(reps, 1)):
         t0 = time.perf_counter()
         toks, _ = gm.decode(prompt[None, :], n_gen)
         walls.append(time.perf_counter() - t0)
@@ -327,11 +333,11 @@ def decode_leg(reps):
     f = _fixture("ref_decode_cfg3.npz")
     exact = None
     if f is not None:
-        exact = bool(list(toks[0]) == [int(t) for t in f["tokens"]]
+        exact = bool(list(toks[0]) == [int(t) for t in f["tokens"]][:n_gen]
                      and list(prompt) == [int(t) for t in f["prompt"]])
     g = min(gen_ms)
     nbytes = sum(step_bytes(d, p) for p in range(n_prompt, n_prompt + n_gen))
-    return {"workload": "config 3: 30 layers, prompt 8, 64 greedy tokens, batch 1",
+    return {"workload": f"config 3: 30 layers, prompt 8, {n_gen} greedy tokens, batch 1",
             "tokens_per_s": round(n_gen / (g * 1e-3), 1),
             "ms_per_token": round(g / n_gen, 4),
             "steps_per_s_all": round((n_prompt + n_gen) / (min(tot_ms) * 1e-3), 1),
@@ -517,10 +523,11 @@ def cpu_decode_baselines():
     name = {"port": "oracle/bfp_sim (line-faithful numpy restatement of full.py)",
             "vec": "oracle/bfp_vec (numpy-vectorised restatement, bit-identical)"}
 
-    def entry(kind, threads, value, sample):
+    def entry(kind, threads, value, sample, blas=None):
+        blas = threads if blas is None else blas
         return {"value": round(value, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
                 "variant": "line-faithful" if kind == "port" else "vectorised",
-                "sample": f"{name[kind]}, OPENBLAS_NUM_THREADS={threads}: {sample}", "cpu": info}
+                "sample": f"{name[kind]}, OPENBLAS_NUM_THREADS={blas}: {sample}", "cpu": info}
 
     out = {"decode": {}, "long_context": {}, "batch64": {}, "layer": {}}
     for (kind, thr), r in runs.items():
@@ -542,7 +549,7 @@ def cpu_decode_baselines():
     t72 = max(r["steps"]["72"] for r in batch_par)
     out["batch64"][f"vectorised_{par}proc"] = entry(
         "vec", par, par / t72, f"{par} concurrent single-threaded processes, one sequence's step "
-        f"at position 72 each (independent sequences), slowest {t72:.3f} s")
+        f"at position 72 each (independent sequences), slowest {t72:.3f} s", blas=1)
     for k, r in layer.items():
         ts = [r["steps"][str(p)] for p in range(7)]
         kk = "port" if k == "faithful" else "vec"
@@ -610,13 +617,24 @@ def main():
     from bfp import _lib
     _lib.lib()
     if args.decode_only:
-        res = {} if args.no_config3 else {"decode": decode_leg(args.decode_reps)}
+        def note(msg):
+            print(f"[bench] {msg}", file=sys.stderr, flush=True)
+        res = {}
+        if not args.no_config3:
+            note("config 3 decode")
+            res["decode"] = decode_leg(args.decode_reps, args.decode_tokens)
         if not args.no_layer:
+            note("config 1 layer step")
             res["layer"] = layer_leg()
         if args.long:
+            note("config 4 long context")
             res["long_context"] = long_context_leg()
         if args.batch64:
+            note("config 5 batch 64")
             res["batch64"] = batch_leg(args.batch64_tokens)
+        if args.decode_probe:
+            note("HBM ceiling probe")
+            res["stream_ceiling"] = stream_probe()
         print(json.dumps(res), flush=True)
         return
     print(f"[bench] building device rings for {len(SHAPES)} shapes x {args.reps} reps",

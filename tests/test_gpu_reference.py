@@ -96,3 +96,71 @@ def test_config3_decode_on_gpu(gpu):
         assert (hm[0, s, d.NL - 1] == f["last_m"][s]).all()
     assert list(toks[0]) == [int(t) for t in f["tokens"]]
     gm.close()
+
+
+def _digests(hm, he, b, steps, nl):
+    out = []
+    for s in range(steps):
+        h = hashlib.sha256()
+        for li in range(nl):
+            h.update(hm[b, s, li].tobytes())
+            h.update(he[b, s, li].tobytes())
+        out.append(h.digest())
+    return out
+
+
+def test_config4_decode_on_gpu(gpu):
+    """BASELINE config 4 on the 30-layer model: 48-token prompt decoded
+    through position 2047 (the long-context attention form, 9 heads over 3
+    KV groups, up to 2048 positions), every step's 30 layer outputs (as a
+    digest) and every token against the reference's own run."""
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    path = GOLDEN / "ref_decode_cfg4.npz"
+    if not path.exists():
+        pytest.skip("ref_decode_cfg4.npz not generated")
+    f = np.load(path)
+    prompt = f["prompt"]
+    n_gen = len(f["tokens"])
+    steps = len(prompt) + n_gen
+    d = Dims(MAX_CTX=steps)
+    print("[gpu-ref] config 4: building the 30-layer model", flush=True)
+    gm = BfpModel(d)
+    gm.load_fp32(synth.make_model(d, seed=int(f["seed"])))
+    print("[gpu-ref] config 4: decoding 2048 steps", flush=True)
+    toks, (hm, he) = gm.decode(prompt[None, :], n_gen, hist=True)
+    gm.close()
+    got = _digests(hm, he, 0, steps, d.NL)
+    bad = [s for s in range(steps) if got[s] != f["digests"][s].tobytes()]
+    assert not bad, f"layer outputs differ from the reference at steps {bad[:8]} ({len(bad)} steps)"
+    for k, s in enumerate(f["last_steps"]):
+        assert (hm[0, s, d.NL - 1] == f["last_m"][k]).all() and (he[0, s, d.NL - 1] == f["last_e"][k]).all()
+    assert list(toks[0]) == [int(t) for t in f["tokens"]]
+
+
+def test_config5_decode_on_gpu(gpu):
+    """the 64 sequences decoded together (the batched
+    matrix-core path), every sequence's per-step layer-output digests and
+    its 128 tokens against the reference's own single-sequence runs."""
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    path = GOLDEN / "ref_decode_cfg5.npz"
+    if not path.exists():
+        pytest.skip("ref_decode_cfg5.npz not generated")
+    f = np.load(path)
+    prompts = f["prompts"]
+    B, n_prompt = prompts.shape
+    n_gen = f["tokens"].shape[1]
+    steps = n_prompt + n_gen
+    d = Dims(MAX_CTX=steps)
+    print("[gpu-ref] config 5: building the 30-layer model", flush=True)
+    gm = BfpModel(d, max_batch=B)
+    gm.load_fp32(synth.make_model(d, seed=int(f["seed"])))
+    print(f"[gpu-ref] config 5: decoding {B} sequences x {steps} steps", flush=True)
+    toks, (hm, he) = gm.decode(prompts, n_gen, hist=True)
+    gm.close()
+    for b in range(B):
+        got = _digests(hm, he, b, steps, d.NL)
+        bad = [s for s in range(steps) if got[s] != f["digests"][b, s].tobytes()]
+        assert not bad, f"sequence {b}: layer outputs differ at steps {bad[:8]}"
+    assert (toks == f["tokens"]).all()

@@ -83,3 +83,36 @@ def test_config1_rounding_margins():
     # a few-ulp float64 difference cannot change any BFP output of config 1
     assert worst_m > 64
     assert worst_e > 1e-12
+
+
+def test_long_context_rounding_margins():
+    """The same measure for one SmolLM2-shaped layer at the end of config
+    4's range (positions 2040-2047, attention over up to 2048 cached rows):
+    the attention output is a 2048-term float64 sum, so this is where a
+    one-ulp difference in np.exp could first reach a BFP mantissa."""
+    from bfp import Dims, synth
+    d = Dims(NL=1, MAX_CTX=2048, VOCAB=256)
+    om = sim.build_model(synth.make_model(d, seed=2))
+    lw = om.layers[0]
+    rng = np.random.default_rng(2)
+    kv = sim.new_kv(om.dims, 2048)
+    for t in range(2040):
+        kv["k"][t] = sim.fp_quantize_vec(rng.standard_normal(d.KV) * 0.5).reshape(d.H_KV, d.HD)
+        kv["v"][t] = sim.fp_quantize_vec(rng.standard_normal(d.KV) * 0.5).reshape(d.H_KV, d.HD)
+    worst = np.inf
+    for p in range(2040, 2048):
+        h = sim.fp_quantize_vec(rng.standard_normal(d.D))
+        dump = {}
+        sim.fwd_layer(h, lw, pos=p, kv=kv, kv_pos=p, dims=om.dims, dump=dump)
+        attn = np.zeros(d.D)
+        for hq in range(d.H_Q):
+            g = hq // (d.H_Q // d.H_KV)
+            qh = dump["Q"][hq * 64:(hq + 1) * 64]
+            sc = np.array([float(np.dot(qh, kv["k"][t, g])) / 8.0 for t in range(p + 1)])
+            pr = sim.softmax_fp(sc)
+            for t in range(p + 1):
+                attn[hq * 64:(hq + 1) * 64] += pr[t] * kv["v"][t, g]
+        mm, _ = _margins(attn)
+        worst = min(worst, mm)
+    print(f"long context: min attention mantissa margin {worst:.0f} ulps")
+    assert worst > 64

@@ -1115,10 +1115,13 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
   const int d64 = a.D / 64, r0 = wg * a.rows_per_wg;
   // a pass's embedding words, every load unconditional (a load behind a
   // branch is waited out there); the first pass is in flight during the
-  // final norm, each later one during the previous pass's arithmetic
+  // final norm, each later one during the previous pass's arithmetic.  The
+  // prefetch past the last pass re-reads that pass's own rows (just
+  // fetched, so it hits the caches; re-reading the first pass's rows cost a
+  // quarter more HBM traffic than the table).
   float4 cur[MAXD64], nxt[MAXD64];
   auto load_rows = [&](int rr, float4 (&f)[MAXD64]) {
-    rr = rr < a.rows_per_wg ? rr : sub;
+    rr = rr < a.rows_per_wg ? rr : rr - 16;
     const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)(r0 + rr) * a.D);
 #pragma unroll
     for (int i = 0; i < MAXD64; ++i) f[i] = e4[(EXACT || i < d64 ? i : d64 - 1) * 16 + l16];
