@@ -349,14 +349,45 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * prompt token); every step's argmax is recorded, so tokens_out holds
  * batch x (n_prompt + n_gen) tokens (the RTL's result_buf / RTL_TOKENS). */
 #define BFP_DECODE_RTL_LOOP 4
+/* Batch 1 runs the whole decode as one persistent cooperative launch (one
+ * workgroup per compute unit, stages handing over through device-coherent
+ * memory) when the dimensions allow it (D <= 576, FFN <= 1536, NL >= 2, the
+ * Q|K|V, O, G/U and D chunks of a layer within the compute units) and the
+ * KV capacity is at most 512 (the environment variable BFP_PERSIST=1 takes
+ * it for every capacity); else, or with this flag or BFP_PERSIST=0, each
+ * step is a replayed graph of per-stage kernels.  Both give identical
+ * outputs. */
+#define BFP_DECODE_NO_PERSIST 8
+/* Persistent path only: record the device clock (100 MHz) as each stage's
+ * input becomes ready and as its output is stored, in the first workgroup of
+ * each role, for bfp_decode_trace. */
+#define BFP_DECODE_TRACE 16
 int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int batch,
                int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags);
+/* How the last bfp_decode ran: BFP_PATH_PERSIST (one persistent launch),
+ * BFP_PATH_GRAPH (a replayed graph per step) or BFP_PATH_EAGER (per-stage
+ * launches, BFP_DECODE_NO_GRAPH); -1 before any decode. */
+#define BFP_PATH_GRAPH 0
+#define BFP_PATH_PERSIST 1
+#define BFP_PATH_EAGER 2
+int bfp_decode_path(const bfp_ctx *ctx);
+/* The stage trace of the last decode run with BFP_DECODE_TRACE on the
+ * persistent path: per (step, layer) 16 stamps -- 0/1 Q|K|V input ready /
+ * output stored, 2 (unused), 3 attention output stored, 4/5 O, 6/7 G/U, 8/9 D
+ * input ready / output stored, 10/11 Q|K|V norm / matvec done, 12/13 G/U
+ * norm / matvecs done, 14 D matvec done, 15 O matvec done -- then per step 3
+ * head stamps (h ready, slice argmax stored, token known; 0 where the step
+ * ran no head).
+ * Copies up to n values and returns how many were recorded (0 if none). */
+int bfp_decode_trace(const bfp_ctx *ctx, uint64_t *out, size_t n);
 
 /* Device time (HIP events) of the last bfp_decode: all steps, and the steps
  * from n_prompt on. */
 int bfp_decode_time(const bfp_ctx *ctx, float *total_ms, float *gen_ms);
 /* Per-step device times of the last decode run with BFP_DECODE_STEP_TIMES;
- * copies up to n values, returns the number of steps recorded. */
+ * copies up to n values, returns the number of steps recorded.  (On the
+ * persistent path they are read from the device clock at each step's start
+ * in workgroup 0, always recorded.) */
 int bfp_decode_step_times(const bfp_ctx *ctx, float *ms, int n);
 
 /* ------------------------------------------------------------ vocabulary */

@@ -87,6 +87,7 @@ def test_config3_decode_on_gpu(gpu):
     gm.load_fp32(fm)
     print("[gpu-ref] config 3: decoding", flush=True)
     toks, (hm, he) = gm.decode(prompt[None, :], n_gen, hist=True)
+    assert gm.decode_path() == "persist"
     for s in range(len(prompt) + n_gen):
         h = hashlib.sha256()
         for li in range(d.NL):
@@ -109,26 +110,32 @@ def _digests(hm, he, b, steps, nl):
     return out
 
 
-def test_config4_decode_on_gpu(gpu):
+@pytest.mark.parametrize("path_env", ["default", "persist"])
+def test_config4_decode_on_gpu(gpu, path_env, monkeypatch):
     """BASELINE config 4 on the 30-layer model: 48-token prompt decoded
     through position 2047 (the long-context attention form, 9 heads over 3
     KV groups, up to 2048 positions), every step's 30 layer outputs (as a
-    digest) and every token against the reference's own run."""
+    digest) and every token against the reference's own run -- on the
+    default path (the per-stage graph at this capacity) and on the
+    persistent kernel."""
     from bfp import Dims, synth
     from bfp.model import BfpModel
     path = GOLDEN / "ref_decode_cfg4.npz"
     if not path.exists():
         pytest.skip("ref_decode_cfg4.npz not generated")
+    if path_env == "persist":
+        monkeypatch.setenv("BFP_PERSIST", "1")
     f = np.load(path)
     prompt = f["prompt"]
     n_gen = len(f["tokens"])
     steps = len(prompt) + n_gen
     d = Dims(MAX_CTX=steps)
-    print("[gpu-ref] config 4: building the 30-layer model", flush=True)
+    print(f"[gpu-ref] config 4 ({path_env}): building the 30-layer model", flush=True)
     gm = BfpModel(d)
     gm.load_fp32(synth.make_model(d, seed=int(f["seed"])))
     print("[gpu-ref] config 4: decoding 2048 steps", flush=True)
     toks, (hm, he) = gm.decode(prompt[None, :], n_gen, hist=True)
+    assert gm.decode_path() == ("persist" if path_env == "persist" else "graph")
     gm.close()
     got = _digests(hm, he, 0, steps, d.NL)
     bad = [s for s in range(steps) if got[s] != f["digests"][s].tobytes()]

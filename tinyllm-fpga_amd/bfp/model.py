@@ -246,7 +246,8 @@ class BfpModel:
         return am, lg
 
     # --------------------------------------------------------------- decode
-    def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False, rtl_loop=False):
+    def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False, rtl_loop=False,
+               persist=True, trace=False):
         """Greedy decode (full.py:426-443) of a batch of prompts
         (batch, n_prompt).  Returns (tokens (batch, n_gen), hist) where hist
         is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16)).
@@ -254,7 +255,11 @@ class BfpModel:
         rtl_loop=True runs the FPGA driver's loop policy instead
         (autoregress_bfp_top.sv:357-386): the step after the prompt feeds
         the last prediction, and the tokens returned are every step's
-        prediction, (batch, n_prompt + n_gen)."""
+        prediction, (batch, n_prompt + n_gen).
+
+        persist=False keeps batch 1 off the persistent single-launch kernel
+        (decode_path() tells which path the last decode took); trace=True
+        records its stage stamps (decode_trace())."""
         P = np.ascontiguousarray(np.atleast_2d(np.asarray(prompts, dtype=np.int32)))
         batch, n_prompt = P.shape
         steps = n_prompt + n_gen
@@ -265,7 +270,8 @@ class BfpModel:
         if hist:
             hm = np.zeros((batch, steps, d.NL, d.D), np.int16)
             he = np.zeros((batch, steps, d.NL, d.D // 16), np.int8)
-        flags = (0 if graph else 1) | (2 if step_times else 0) | (4 if rtl_loop else 0)
+        flags = ((0 if graph else 1) | (2 if step_times else 0) | (4 if rtl_loop else 0)
+                 | (0 if persist else 8) | (16 if trace else 0))
         call("bfp_decode", self._h, _p(P), n_prompt, n_gen, batch, _p(toks),
              _p(hm) if hist else None, _p(he) if hist else None, flags)
         return toks[:, :n_out], ((hm, he) if hist else None)
@@ -277,6 +283,23 @@ class BfpModel:
         if n > 0:
             lib().bfp_decode_step_times(self._h, _p(out), n)
         return out
+
+    def decode_path(self):
+        """'persist', 'graph' or 'eager': how the last decode ran."""
+        return {0: "graph", 1: "persist", 2: "eager"}.get(lib().bfp_decode_path(self._h), None)
+
+    def decode_trace(self):
+        """Stage stamps (device clock, 100 MHz) of the last decode(trace=True)
+        on the persistent path: (layer stamps (steps, NL, 16), head stamps
+        (steps, 3)), or None."""
+        n = lib().bfp_decode_trace(self._h, None, 0)
+        if n <= 0:
+            return None
+        out = np.zeros(n, np.uint64)
+        lib().bfp_decode_trace(self._h, _p(out), n)
+        nl = self.dims.NL
+        steps = n // (nl * 16 + 3)
+        return out[:steps * nl * 16].reshape(steps, nl, 16), out[steps * nl * 16:].reshape(steps, 3)
 
     def decode_time_ms(self):
         t, g = C.c_float(), C.c_float()

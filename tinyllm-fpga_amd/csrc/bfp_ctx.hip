@@ -10,6 +10,7 @@
 #include "bfp.h"
 #include "bfp_internal.h"
 #include "bfp_layer.h"
+#include "bfp_persist.h"
 
 using namespace bfp;
 
@@ -49,9 +50,18 @@ struct bfp_ctx {
   int8_t *rtl_emb_e = nullptr, *rtl_lg_e = nullptr, *rtl_xn_e = nullptr;
   int16_t *rtl_lg_m = nullptr, *rtl_xn_m = nullptr;
   int *rtl_work = nullptr, *rtl_tok = nullptr;
+  // the persistent decode's tagged hand-off words, per-layer argument blocks
+  // and step clock, made on its first use
+  unsigned *pt_words = nullptr;
+  size_t pt_nwords = 0;
+  LayerArgs *pt_layers = nullptr;
+  PersistArgs *pt_args = nullptr;
+  unsigned long long *pt_clock = nullptr;
   std::vector<void *> allocs;
+  int last_path = -1;   // BFP_PATH_* of the last decode
   float last_decode_ms = 0.f, last_gen_ms = 0.f;
   std::vector<float> step_ms;   // per-step device time of the last decode (BFP_DECODE_STEP_TIMES)
+  std::vector<unsigned long long> trace;   // stage stamps of the last traced persistent decode
 
   int alloc(void **p, size_t bytes) {
     *p = nullptr;
@@ -161,6 +171,122 @@ void stage_lens(const bfp_dims &d, int len[ST_COUNT]) {
   const int KV = d.H_KV * d.HD;
   const int L[ST_COUNT] = {d.D, d.D, KV, KV, d.D, d.D, d.D, d.D, d.FFN, d.FFN, d.FFN, d.D, d.D};
   for (int i = 0; i < ST_COUNT; ++i) len[i] = L[i];
+}
+
+// BFP_PERSIST: unset -> the persistent kernel for the short attention forms
+// (capacity <= 512; above it the long form inside the persistent kernel is
+// slower than the graph's own launch); "1" -> every form; "0" -> never.
+bool persist_enabled(int max_ctx) {
+  const char *v = getenv("BFP_PERSIST");
+  if (v && v[0] == '0') return false;
+  if (v && v[0] == '1') return true;
+  return attn_ppw(max_ctx) != 8;
+}
+
+// The whole batch-1 decode as one persistent launch (bfp_persist.hip).
+int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int n_prompt,
+                   int n_gen, int *dout, int16_t *dhm, int8_t *dhe, bool rtl_loop, bool trace) {
+  const bfp_dims &d = c->d;
+  hipStream_t s = c->stream;
+  const int steps = n_prompt + n_gen;
+  DevBuf tmp;
+  unsigned long long *dtrace = nullptr;
+  const size_t ntrace = persist_trace_len(steps, d.NL);
+  c->trace.clear();
+  if (trace) {
+    BFP_TRY(tmp.alloc((void **)&dtrace, ntrace * sizeof(unsigned long long)));
+    HIP_TRY(hipMemsetAsync(dtrace, 0, ntrace * sizeof(unsigned long long), s));
+  }
+  if (!c->pt_words) {
+    const size_t nw = persist_words(d, grid);
+    BFP_TRY(c->alloc((void **)&c->pt_words, nw * 4));
+    BFP_TRY(c->alloc((void **)&c->pt_layers, sizeof(LayerArgs) * d.NL));
+    BFP_TRY(c->alloc((void **)&c->pt_args, sizeof(PersistArgs)));
+    BFP_TRY(c->alloc((void **)&c->pt_clock, sizeof(unsigned long long) * (c->max_ctx + 1)));
+    std::vector<LayerArgs> la(d.NL);
+    for (int l = 0; l < d.NL; ++l) la[l] = layer_args(c, l, 1);
+    HIP_TRY(hipMemcpy(c->pt_layers, la.data(), sizeof(LayerArgs) * d.NL, hipMemcpyHostToDevice));
+    c->pt_nwords = nw;
+  }
+  const size_t D = d.D, nq = D + 2 * (size_t)d.H_KV * d.HD, F = d.FFN;
+  unsigned *w = c->pt_words;
+  pa.t_h = w;
+  pa.t_h1 = (w += 2 * D);
+  pa.t_att = (w += 2 * D);
+  pa.t_qkv = (w += 2 * D);
+  pa.t_mlp = (w += 2 * nq);
+  pa.t_part = (w += 2 * F);
+  pa.abort_flag = (w += 2 * 4 * (size_t)grid);
+  pa.L = c->pt_layers;
+  pa.steps = steps;
+  pa.n_prompt = n_prompt;
+  pa.n_gen = n_gen;
+  pa.rtl_loop = rtl_loop ? 1 : 0;
+  pa.prompt = dprompt;
+  pa.out = dout;
+  pa.last = c->last;
+  pa.embed = c->embed;
+  pa.norm_w = c->norm_w;
+  pa.clock = c->pt_clock;
+  pa.hist_m = dhm;
+  pa.hist_e = dhe;
+  pa.hist_steps = dhm ? steps : 0;
+  pa.trace = dtrace;
+  HIP_TRY(hipMemsetAsync(c->pt_words, 0, c->pt_nwords * 4, s));
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  HIP_TRY(hipEventCreate(&ev0));
+  HIP_TRY(hipEventCreate(&ev1));
+  (void)hipEventRecord(ev0, s);
+  int rc = launch_decode_persist(pa, c->pt_args, grid, c->max_ctx, s);
+  (void)hipEventRecord(ev1, s);
+  if (!rc) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = set_err(BFP_EIO, "persistent decode: %s", hipGetErrorString(e));
+  }
+  unsigned aborted = 0;
+  std::vector<unsigned long long> clk(steps + 1);
+  if (!rc) {
+    hipError_t e = hipMemcpy(&aborted, pa.abort_flag, 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess)
+      e = hipMemcpy(clk.data(), c->pt_clock, sizeof(unsigned long long) * (steps + 1),
+                    hipMemcpyDeviceToHost);
+    if (e != hipSuccess) rc = set_err(BFP_EIO, "persistent decode read-back: %s", hipGetErrorString(e));
+    else if (aborted) rc = set_err(BFP_EIO, "persistent decode: a hand-off wait timed out");
+  }
+  if (!rc) {
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, ev0, ev1);
+    int khz = 0;
+    (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, c->device);
+    const double tick_ms = khz > 0 ? 1.0 / khz : 1e-5;   // the clock runs at 100 MHz
+    c->last_decode_ms = ms;
+    c->last_gen_ms = n_gen > 0 ? (float)((double)(clk[steps] - clk[n_prompt]) * tick_ms) : 0.f;
+    c->step_ms.resize(steps);
+    for (int k = 0; k < steps; ++k) c->step_ms[k] = (float)((double)(clk[k + 1] - clk[k]) * tick_ms);
+    c->last_path = BFP_PATH_PERSIST;
+    if (dtrace) {
+      c->trace.resize(ntrace);
+      hipError_t e = hipMemcpy(c->trace.data(), dtrace, ntrace * sizeof(unsigned long long),
+                               hipMemcpyDeviceToHost);
+      if (e != hipSuccess) rc = set_err(BFP_EIO, "persistent decode trace: %s", hipGetErrorString(e));
+    }
+  }
+  (void)hipEventDestroy(ev0);
+  (void)hipEventDestroy(ev1);
+  return rc;
+}
+
+// Tokens and the optional history back to the host.
+int decode_copy_out(bfp_ctx *c, int batch, int steps, int n_out, const int *dout, int32_t *tokens_out,
+                    const int16_t *dhm, const int8_t *dhe, int16_t *hist_m, int8_t *hist_e) {
+  const bfp_dims &d = c->d;
+  if (n_out > 0)
+    HIP_TRY(hipMemcpy(tokens_out, dout, sizeof(int) * batch * n_out, hipMemcpyDeviceToHost));
+  if (dhm) {
+    HIP_TRY(hipMemcpy(hist_m, dhm, (size_t)batch * steps * d.NL * d.D * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(hist_e, dhe, (size_t)batch * steps * d.NL * d.D / 16, hipMemcpyDeviceToHost));
+  }
+  return BFP_OK;
 }
 
 }  // namespace
@@ -888,6 +1014,16 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   for (int b = 0; b < batch; ++b) st[1 + b] = prompt[b * n_prompt];
   HIP_TRY(hipMemcpyAsync(c->state, st.data(), sizeof(int) * (batch + 1), hipMemcpyHostToDevice, s));
 
+  PersistArgs pa{};
+  int grid = 0;
+  if (batch == 1 && !(flags & (BFP_DECODE_NO_GRAPH | BFP_DECODE_NO_PERSIST)) && persist_enabled(c->max_ctx) &&
+      persist_plan(d, c->max_ctx, c->device, pa, grid)) {
+    BFP_TRY(decode_persist(c, pa, grid, dprompt, n_prompt, n_gen, dout, dhm, dhe, rtl_loop,
+                           (flags & BFP_DECODE_TRACE) != 0));
+    return decode_copy_out(c, batch, steps, n_out, dout, tokens_out, dhm, dhe, hist_m, hist_e);
+  }
+  c->last_path = (flags & BFP_DECODE_NO_GRAPH) ? BFP_PATH_EAGER : BFP_PATH_GRAPH;
+
   EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
   HeadArgs ha = head_args(c, batch, nullptr);
   CtlArgs ca{batch, n_prompt, n_gen, ha.n_wg, 0, c->state, dprompt, dout, c->part_v,
@@ -977,13 +1113,16 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   if (ev1) (void)hipEventDestroy(ev1);
   if (evg) (void)hipEventDestroy(evg);
   if (rc) return rc;
-  if (n_out > 0)
-    HIP_TRY(hipMemcpy(tokens_out, dout, sizeof(int) * batch * n_out, hipMemcpyDeviceToHost));
-  if (dhm) {
-    HIP_TRY(hipMemcpy(hist_m, dhm, (size_t)batch * steps * d.NL * d.D * 2, hipMemcpyDeviceToHost));
-    HIP_TRY(hipMemcpy(hist_e, dhe, (size_t)batch * steps * d.NL * d.D / 16, hipMemcpyDeviceToHost));
-  }
-  return BFP_OK;
+  return decode_copy_out(c, batch, steps, n_out, dout, tokens_out, dhm, dhe, hist_m, hist_e);
+}
+
+int bfp_decode_path(const bfp_ctx *c) { return c ? c->last_path : -1; }
+
+int bfp_decode_trace(const bfp_ctx *c, uint64_t *out, size_t n) {
+  if (!c || (!out && n > 0)) return set_err(BFP_EINVAL, "null argument");
+  const size_t k = c->trace.size();
+  for (size_t i = 0; i < k && i < n; ++i) out[i] = c->trace[i];
+  return (int)k;
 }
 
 // Per-step device times of the last bfp_decode run with BFP_DECODE_STEP_TIMES:

@@ -130,6 +130,17 @@ __device__ __forceinline__ T xor_sum(T v, int mask) {
 // result as the xor butterfly: after the steps for the larger masks the
 // values are symmetric under them, and rotate and xor partners differ only
 // by such masks (float addition is commutative).
+// Workgroup barrier over LDS data only: every wave's LDS accesses complete
+// before it, but its global loads and stores in flight do not have to (a
+// __syncthreads() after a global store waits for all of the wave's memory
+// operations, e.g. a weight prefetch issued for a later stage).  No code
+// here passes data between the threads of a workgroup through global memory.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Non-temporal loads (the nt cache policy): for data read once per pass,
 // such as weight matrices streamed from HBM.  A plain streaming read of
 // 4 GiB measured 7.1-7.2 TB/s this way against 6.0-6.4 TB/s with ordinary

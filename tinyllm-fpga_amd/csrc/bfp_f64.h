@@ -34,7 +34,7 @@ __device__ __forceinline__ double pw_combine_blocks(int lo, int n, const double 
 // Sum of get(0) .. get(n-1) (1 <= n <= 4096) in numpy order, plus numpy's
 // initial 0.0; get(i) is called for the elements of this lane's leaf (and
 // for index 0 by lanes that own none), so it may read global memory.
-// Called by all threads of a workgroup (uses __syncthreads);
+// Called by all threads of a workgroup (uses lds_barrier);
 // leafbuf holds PW_MAX_LEAVES doubles of LDS.  Returns the sum in every
 // thread.
 //
@@ -93,9 +93,9 @@ __device__ __forceinline__ double pairwise_sum_block_g(Get get, int n, double *l
       leafbuf[gq] = res;
     }
   }
-  __syncthreads();
+  lds_barrier();
   double s = 0.0 + pw_combine_blocks<PW_DEPTH>(0, n, leafbuf);
-  __syncthreads();
+  lds_barrier();
   return s;
 }
 

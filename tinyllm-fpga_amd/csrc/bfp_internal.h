@@ -73,6 +73,9 @@ struct EmbedArgs;
 int launch_layer(const LayerArgs &a, hipStream_t s);
 int prepare_layer_kernels(int max_ctx, int D, int FFN);
 int prepare_head_kernels(int D);
+// Raise a kernel's dynamic-LDS limit on the current device to at least
+// `bytes` (never lowering it: the limit is process-wide per device).
+int raise_lds_limit(const void *f, int bytes);
 int head_workgroups(int vocab, int D, int rows_single, int batch);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);

@@ -100,6 +100,13 @@ struct HeadArgs {
   double *hn;                              // (batch, D) normed hidden, batch > 1 path
 };
 
+// Attention form by KV capacity: products per producer wave and AV block
+// (2 -> 14 positions, 4 -> 28, 8 -> 56); 2, 3 and 4 are the short forms (one
+// workgroup per head), 8 the long one (four workgroups per head).
+inline int attn_ppw(int max_ctx) {
+  return max_ctx <= 128 ? 2 : (max_ctx <= 256 ? 3 : (max_ctx <= 512 ? 4 : 8));
+}
+
 // Rows per workgroup of the batch > 1 head: 16 row slots x 2 rows for
 // D <= 576, x 1 row above (register budget).
 inline int head_rows_multi(int D) { return D <= 576 ? 32 : 16; }

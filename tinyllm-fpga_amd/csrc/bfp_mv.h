@@ -150,7 +150,7 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
   M = pmax<32>(M);
   if (NW > 1) {
     if (tq == 0) redM[w * 16 + r] = M;
-    __syncthreads();
+    lds_barrier();
     M = redM[r];
 #pragma unroll
     for (int i = 1; i < NW; ++i) M = redM[i * 16 + r] > M ? redM[i * 16 + r] : M;
@@ -165,13 +165,13 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
   A = psum<32>(A);
   if (NW > 1) {
     if (tq == 0) redA[w * 16 + r] = A;
-    __syncthreads();
+    lds_barrier();
     if (w == 0) {
       A = redA[r];
 #pragma unroll
       for (int i = 1; i < NW; ++i) A += redA[i * 16 + r];
     }
-    __syncthreads();   // redM/redA may be reused by a following chunk
+    lds_barrier();   // redM/redA may be reused by a following chunk
   }
   A = A < SAT_LO ? SAT_LO : (A > SAT_HI ? SAT_HI : A);
   A_out = A;
@@ -244,7 +244,7 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
     if (tq == 0)
 #pragma unroll
       for (int s = 0; s < S; ++s) redM[(w * 16 + r) * S + s] = M[s];
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       int m = redM[r * S + s];
@@ -270,7 +270,7 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
     if (tq == 0)
 #pragma unroll
       for (int s = 0; s < S; ++s) redA[(w * 16 + r) * S + s] = A[s];
-    __syncthreads();
+    lds_barrier();
     if (w == 0)
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -287,7 +287,7 @@ __device__ __forceinline__ void chunk_AM_multi(const ChunkRegs<TPT> &R, const in
       Ao[r * S + s] = a;
       Mo[r * S + s] = M[s];
     }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Quantise the chunk's 16 rows (wave 0; lanes r and r+16k hold row r): the
