@@ -73,6 +73,20 @@ struct bfp_ctx {
     allocs.push_back(*p);
     return BFP_OK;
   }
+  // Fine-grained device memory: device-coherent (SC1) accesses to it are
+  // faster than to ordinary allocations (a cross-XCD hand-off measured
+  // 396 ns one way against 580 ns).
+  int alloc_fine(void **p, size_t bytes) {
+    *p = nullptr;
+    hipError_t e = hipExtMallocWithFlags(p, bytes ? bytes : 16, hipDeviceMallocFinegrained);
+    if (e != hipSuccess) {
+      *p = nullptr;
+      return set_err(BFP_ENOMEM, "hipExtMallocWithFlags(%zu, fine-grained): %s", bytes,
+                     hipGetErrorString(e));
+    }
+    allocs.push_back(*p);
+    return BFP_OK;
+  }
   ~bfp_ctx() {
     if (stream) (void)hipStreamSynchronize(stream);
     for (void *p : allocs) (void)hipFree(p);
@@ -199,7 +213,7 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
   }
   if (!c->pt_words) {
     const size_t nw = persist_words(d, grid);
-    BFP_TRY(c->alloc((void **)&c->pt_words, nw * 4));
+    BFP_TRY(c->alloc_fine((void **)&c->pt_words, nw * 4));
     BFP_TRY(c->alloc((void **)&c->pt_layers, sizeof(LayerArgs) * d.NL));
     BFP_TRY(c->alloc((void **)&c->pt_args, sizeof(PersistArgs)));
     BFP_TRY(c->alloc((void **)&c->pt_clock, sizeof(unsigned long long) * (c->max_ctx + 1)));

@@ -16,19 +16,64 @@ namespace bfp {
 constexpr int PW_DEPTH = 6;        // n <= 128 * 2^6 = 8192
 constexpr int PW_MAX_LEAVES = 64;  // leaf slots: one per 64-element block, n <= 4096
 
-// numpy's leaves combined in its order; the leaf starting at element lo is
-// leaf[lo / 64] (see pairwise_sum_block).
-template <int DEPTH>
-__device__ __forceinline__ double pw_combine_blocks(int lo, int n, const double *leaf) {
-  if constexpr (DEPTH > 0) {
-    if (n > 128) {
-      int n2 = n / 2;
+// numpy's combination of the leaves of a range of n elements: split at
+// n2 = n/2 rounded down to a multiple of 8 while longer than 128, each node
+// the sum left + right; the leaf starting at element lo is leaf[lo / 64]
+// (see pairwise_sum_block_g).  Evaluated across the 64 lanes of a wave
+// (every lane of the wave calls; every lane returns the root).  Lane i, with
+// q = 63 - i, follows the path from the root that the bits of q give, most
+// significant first (1 = right part of a split); it starts with the value
+// of the leaf it reaches when the remaining bits of q are all 0 (the first
+// q of the leaf's span of 64 >> depth), else with none.  Step k adds the
+// value at q + 2^k (lane i - 2^k: a row rotate for k < 4, a permlane swap
+// for 16 and 32) into q (bits 0..k of q clear): where both hold a value the
+// span is an internal node and that addition is numpy's left + right; where
+// only the left part holds one it is a leaf covering both halves.  q = 0
+// (lane 63) ends with the root.
+__device__ __forceinline__ double pw_combine_wave(int n, const double *leaf) {
+  const int q = 63 - (int)(threadIdx.x & 63);
+  int lo = 0, len = n, span = 64;
+#pragma unroll
+  for (int d = 0; d < PW_DEPTH; ++d) {
+    if (len > 128) {
+      int n2 = len / 2;
       n2 -= n2 % 8;
-      return pw_combine_blocks<DEPTH - 1>(lo, n2, leaf) +
-             pw_combine_blocks<DEPTH - 1>(lo + n2, n - n2, leaf);
+      span >>= 1;
+      if (q & span) {
+        lo += n2;
+        len -= n2;
+      } else {
+        len = n2;
+      }
     }
   }
-  return leaf[lo >> 6];
+  int have = (q & (span - 1)) == 0;
+  double v = have ? leaf[lo >> 6] : 0.0;
+  // the deepest leaves span 2^(6 - depth) lanes: the steps below that span
+  // have no pair to add (a range of at most 128 elements is one leaf)
+  int depth = 0;
+  for (int m = n; m > 128; ++depth) {
+    int n2 = m / 2;
+    n2 -= n2 % 8;
+    m -= n2;   // the right part is the longer one
+  }
+  const int first = PW_DEPTH - depth;   // wave-uniform
+  auto step = [&](double o, int oh, int m) {
+    if (!(q & m) && oh) {
+      v = have ? v + o : o;
+      have = 1;
+    }
+  };
+  if (first <= 0) step(peer<1>(v), peer<1>(have), 1);
+  if (first <= 1) step(peer<2>(v), peer<2>(have), 2);
+  if (first <= 2) step(peer<4>(v), peer<4>(have), 4);
+  if (first <= 3) step(peer<8>(v), peer<8>(have), 8);
+  if (first <= 4) step(peer<16>(v), peer<16>(have), 16);
+  if (first <= 5) step(peer<32>(v), peer<32>(have), 32);
+  const long long b = __double_as_longlong(v);
+  const int lo32 = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), 63);
+  const int hi32 = __builtin_amdgcn_readlane((int)(b >> 32), 63);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi32 << 32) | (unsigned)lo32));
 }
 
 // Sum of get(0) .. get(n-1) (1 <= n <= 4096) in numpy order, plus numpy's
@@ -36,7 +81,8 @@ __device__ __forceinline__ double pw_combine_blocks(int lo, int n, const double 
 // for index 0 by lanes that own none), so it may read global memory.
 // Called by all threads of a workgroup (uses lds_barrier);
 // leafbuf holds PW_MAX_LEAVES doubles of LDS.  Returns the sum in every
-// thread.
+// thread; waves may still read leafbuf on return, so it is written again
+// only after a later barrier.
 //
 // numpy splits a range longer than 128 at n/2 rounded down to a multiple of
 // 8, so every leaf of a range longer than 128 has at least 64 elements and
@@ -94,9 +140,7 @@ __device__ __forceinline__ double pairwise_sum_block_g(Get get, int n, double *l
     }
   }
   lds_barrier();
-  double s = 0.0 + pw_combine_blocks<PW_DEPTH>(0, n, leafbuf);
-  lds_barrier();
-  return s;
+  return 0.0 + pw_combine_wave(n, leafbuf);
 }
 
 // The same sum of a[0..n) held in LDS.
@@ -213,6 +257,62 @@ __device__ __forceinline__ int quantize16_lanes(double v, int &e, bool canonical
 }
 
 __device__ __forceinline__ double bfp_val(int m, int e) { return ldexp((double)m, e - 15); }
+
+// An 8-lane group's maximum / or (lanes 8g .. 8g+7): row half-mirror (lane
+// i with 7 - i), then quad swaps i ^ 1 and i ^ 2 -- after the three steps
+// every lane has combined all eight.
+template <class F>
+__device__ __forceinline__ int group8_u32(int v, F op) {
+  v = op(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, false));   // row_half_mirror
+  v = op(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false));    // quad_perm 1,0,3,2
+  return op(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false)); // quad_perm 2,3,0,1
+}
+__device__ __forceinline__ double group8_max(double v) {
+  auto dpp = [](double x, int ctrl) {
+    const long long b = __double_as_longlong(x);
+    int lo = (int)(b & 0xffffffffLL), hi = (int)(b >> 32);
+    switch (ctrl) {
+      case 0x141:
+        lo = __builtin_amdgcn_mov_dpp(lo, 0x141, 0xf, 0xf, false);
+        hi = __builtin_amdgcn_mov_dpp(hi, 0x141, 0xf, 0xf, false);
+        break;
+      case 0xB1:
+        lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xf, 0xf, false);
+        hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xf, 0xf, false);
+        break;
+      default:
+        lo = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xf, 0xf, false);
+        hi = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xf, 0xf, false);
+        break;
+    }
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+  };
+  v = fmax(v, dpp(v, 0x141));
+  v = fmax(v, dpp(v, 0xB1));
+  return fmax(v, dpp(v, 0x4E));
+}
+
+// tile_quantize of the 16 values held two per lane by an 8-lane group
+// (elements 2j and 2j+1 in lane j of the group): the tile exponent in e and
+// this lane's two mantissas, canonical when `canonical` (the same values as
+// quantize16_lanes over the same 16 values).  All 64 lanes participate.
+__device__ __forceinline__ void quantize16_pairs(double y0, double y1, int &m0, int &m1, int &e,
+                                                 bool canonical) {
+  const double a = group8_max(fmax(fabs(y0), fabs(y1)));
+  e = tile_exp_of(a);
+  m0 = tile_mant_of(y0, e);
+  m1 = tile_mant_of(y1, e);
+  if (canonical) {
+    const int hit = group8_u32((m0 == -32768 || m1 == -32768) ? 1 : 0, [](int x, int y) { return x | y; });
+    if (hit && e < 127) {
+      e += 1;
+      int q = m0 >> 1;
+      m0 = (m0 & 1) ? q + (q & 1) : q;
+      q = m1 >> 1;
+      m1 = (m1 & 1) ? q + (q & 1) : q;
+    }
+  }
+}
 
 // RoPE of one 64-wide head held one value per lane of a wave (lane l holds
 // element l, pre-rotation x), re-quantised: returns the lane's mantissa.

@@ -34,21 +34,17 @@ __device__ __forceinline__ int cur_kv_pos(const LayerArgs &a) {
 
 // rmsnorm_fp (full.py:236-238) of a BFP vector, re-quantised, into the
 // matvec's LDS input form.  v = pairwise_sum(x*x)/D + 1e-5, y = (x*g)/sqrt(v).
-// dbuf: D shorts of LDS, leaf: PW_MAX_LEAVES doubles.  Thread tid keeps
-// elements tid + k*bs (k < 4) and their gammas in registers from one batch
-// of loads; the owners of numpy's pairwise leaves load their x elements
-// themselves (pairwise_sum_block_g), so nothing is staged in LDS before the
-// sum, and the up-to-four divisions and tile quantisations of a thread are
-// independent chains.  All threads call.
-//
-// gamma(k, i): the gamma of element i, the thread's k-th (i = base + tid +
-// k*bs); rmsnorm_to_x below reads it from global memory, the persistent
-// decode kernel passes values it prefetched into registers.
-template <class Gamma>
+// dbuf: 3*D doubles of LDS, leaf: PW_MAX_LEAVES doubles.  Thread tid keeps
+// elements tid + k*bs (k < KE) and their gammas in registers from one batch
+// of loads, so its up-to-KE divisions and tile quantisations are
+// independent chains; the owners of numpy's pairwise leaves load their x
+// elements themselves (pairwise_sum_block_g), so nothing is staged in LDS
+// before the sum.  gamma(k, i): the gamma of element i, the thread's k-th
+// (i = base + tid + k*bs).  All threads call.
+template <int KE, class Gamma>
 __device__ __forceinline__ void rmsnorm_to_x_g(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
                                                Gamma gamma, int D, int *xs, int *xes, double *dbuf,
                                                double *leaf, int16_t *dm, int8_t *de) {
-  constexpr int KE = 4;
   const int bs = blockDim.x, tid = threadIdx.x;
   int m[KE], e[KE];
   double gg[KE];
@@ -70,8 +66,7 @@ __device__ __forceinline__ void rmsnorm_to_x_g(const int16_t *__restrict__ hm, c
       },
       D, leaf);
   const double rt = sqrt(s / (double)D + 1e-5);
-  short *mq = reinterpret_cast<short *>(dbuf);
-  for (int base = 0; base < D; base += KE * bs) {   // one pass when D <= 4*bs
+  for (int base = 0; base < D; base += KE * bs) {   // one pass when D <= KE*bs
     if (base > 0) load(base);
     int mm[KE], ee[KE];
 #pragma unroll
@@ -83,8 +78,11 @@ __device__ __forceinline__ void rmsnorm_to_x_g(const int16_t *__restrict__ hm, c
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
       const int i = base + tid + k * bs;
+      // elements i and i ^ 1 sit in lanes l and l ^ 1 (bs is even): the even
+      // lane writes the pair into the matvec's input form
+      const int odd = __builtin_amdgcn_mov_dpp(mm[k], 0xB1, 0xf, 0xf, false);   // quad_perm 1,0,3,2
       if (i < D) {
-        mq[i] = (short)mm[k];
+        if ((i & 1) == 0) put_x_pair(xs, i >> 4, (i >> 1) & 7, mm[k], odd);
         if ((i & 15) == 0) xes[i >> 4] = ee[k];
         if (dm) {
           dm[i] = (int16_t)mm[k];
@@ -93,14 +91,42 @@ __device__ __forceinline__ void rmsnorm_to_x_g(const int16_t *__restrict__ hm, c
       }
     }
   }
+}
+
+// The same RMSNorm with thread t on the adjacent elements 2t and 2t+1
+// (D <= 2*blockDim): its two divisions and quantisations are one
+// instruction stream, a tile's 16 elements sit in one 8-lane group, and the
+// pair goes into the matvec's input form as it is.  hm/he and the squares
+// (sq, D doubles) are LDS; g0/g1: this thread's gammas.  All threads call.
+__device__ __forceinline__ void rmsnorm_pairs_to_x(const int16_t *__restrict__ hm,
+                                                   const int8_t *__restrict__ he, double g0, double g1,
+                                                   int D, int *xs, int *xes, double *sq, double *leaf) {
+  const int i0 = 2 * (int)threadIdx.x;
+  const bool on = i0 < D;
+  const int j = on ? i0 : 0;
+  const int e_in = he[j >> 4];
+  const double x0 = bfp_val(hm[j], e_in), x1 = bfp_val(hm[j + 1], e_in);
+  if (on) {
+    sq[i0] = x0 * x0;
+    sq[i0 + 1] = x1 * x1;
+  }
   lds_barrier();
-  for (int p = tid; p < D / 2; p += bs) put_x_pair(xs, p >> 3, p & 7, mq[2 * p], mq[2 * p + 1]);
+  const double s = pairwise_sum_block(sq, D, leaf);
+  const double rt = sqrt(s / (double)D + 1e-5);
+  const double y0 = on ? (x0 * g0) / rt : 0.0;
+  const double y1 = on ? (x1 * g1) / rt : 0.0;
+  int m0, m1, e;
+  quantize16_pairs(y0, y1, m0, m1, e, true);   // tile_quantize(rmsnorm_fp(.)): canonical
+  if (on) {
+    put_x_pair(xs, i0 >> 4, (i0 >> 1) & 7, m0, m1);
+    if ((i0 & 15) == 0) xes[i0 >> 4] = e;
+  }
 }
 
 __device__ __forceinline__ void rmsnorm_to_x(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
                                              const double *__restrict__ g, int D, int *xs, int *xes,
                                              double *dbuf, double *leaf, int16_t *dm, int8_t *de) {
-  rmsnorm_to_x_g(hm, he, [g](int, int i) { return g[i]; }, D, xs, xes, dbuf, leaf, dm, de);
+  rmsnorm_to_x_g<4>(hm, he, [g](int, int i) { return g[i]; }, D, xs, xes, dbuf, leaf, dm, de);
 }
 
 // ------------------------------------------------------------- epilogues

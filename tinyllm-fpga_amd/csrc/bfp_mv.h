@@ -178,6 +178,113 @@ __device__ __forceinline__ void chunk_AM(const ChunkRegs<TPT> &R, const int *xs,
   M_out = M;
 }
 
+// chunk_AM of two chunks (R1, R2) over the same input vector in one pass:
+// the x reads and the cross-wave reductions (and their barriers) are shared.
+// Same results as two chunk_AM calls.
+template <int NW, int TPT>
+__device__ __forceinline__ void chunk_AM2(const ChunkRegs<TPT> &R1, const ChunkRegs<TPT> &R2,
+                                          const int *xs, const int *xes, int nT, int *redM,
+                                          long long *redA, long long &A1, int &M1, long long &A2,
+                                          int &M2) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+  typedef short s2 __attribute__((ext_vector_type(2)));
+#define BFP_DOT2(a, b, acc) \
+  __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, (a)), __builtin_bit_cast(s2, (b)), (acc), false)
+  long long S1[TPT], S2[TPT];
+  int E1[TPT], E2[TPT];
+  int m1 = -(1 << 29), m2 = -(1 << 29);
+  auto dot = [&](const uint4 &a, const uint4 &b, const int4 &h0, const int4 &h1, const int4 &l0,
+                 const int4 &l1) {
+    int ah = 0, al = 0;
+    ah = BFP_DOT2(a.x, h0.x, ah);
+    al = BFP_DOT2(a.x, l0.x, al);
+    ah = BFP_DOT2(a.y, h0.y, ah);
+    al = BFP_DOT2(a.y, l0.y, al);
+    ah = BFP_DOT2(a.z, h0.z, ah);
+    al = BFP_DOT2(a.z, l0.z, al);
+    ah = BFP_DOT2(a.w, h0.w, ah);
+    al = BFP_DOT2(a.w, l0.w, al);
+    ah = BFP_DOT2(b.x, h1.x, ah);
+    al = BFP_DOT2(b.x, l1.x, al);
+    ah = BFP_DOT2(b.y, h1.y, ah);
+    al = BFP_DOT2(b.y, l1.y, al);
+    ah = BFP_DOT2(b.z, h1.z, ah);
+    al = BFP_DOT2(b.z, l1.z, al);
+    ah = BFP_DOT2(b.w, h1.w, ah);
+    al = BFP_DOT2(b.w, l1.w, al);
+    return (long long)ah * 256 + al;
+  };
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    const int t = tq + 4 * (w + NW * j);
+    if (t < nT) {
+      const int4 *xp = reinterpret_cast<const int4 *>(xs + t * 16);
+      const int4 h0 = xp[0], h1 = xp[1], l0 = xp[2], l1 = xp[3];
+      S1[j] = dot(R1.a[j], R1.b[j], h0, h1, l0, l1);
+      S2[j] = dot(R2.a[j], R2.b[j], h0, h1, l0, l1);
+      E1[j] = xes[t] + R1.e[j];
+      E2[j] = xes[t] + R2.e[j];
+      m1 = E1[j] > m1 ? E1[j] : m1;
+      m2 = E2[j] > m2 ? E2[j] : m2;
+    } else {
+      S1[j] = S2[j] = 0;
+      E1[j] = E2[j] = -(1 << 29);
+    }
+  }
+#undef BFP_DOT2
+  m1 = pmax<16>(m1);
+  m1 = pmax<32>(m1);
+  m2 = pmax<16>(m2);
+  m2 = pmax<32>(m2);
+  if (NW > 1) {
+    if (tq == 0) {
+      redM[w * 16 + r] = m1;
+      redM[(NW + w) * 16 + r] = m2;
+    }
+    lds_barrier();
+    m1 = redM[r];
+    m2 = redM[NW * 16 + r];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) {
+      m1 = redM[i * 16 + r] > m1 ? redM[i * 16 + r] : m1;
+      m2 = redM[(NW + i) * 16 + r] > m2 ? redM[(NW + i) * 16 + r] : m2;
+    }
+  }
+  long long a1 = 0, a2 = 0;
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    const int sh1 = m1 - E1[j], sh2 = m2 - E2[j];
+    if (sh1 <= ALIGN_MAX) a1 += S1[j] >> sh1;
+    if (sh2 <= ALIGN_MAX) a2 += S2[j] >> sh2;
+  }
+  a1 = psum<16>(a1);
+  a1 = psum<32>(a1);
+  a2 = psum<16>(a2);
+  a2 = psum<32>(a2);
+  if (NW > 1) {
+    if (tq == 0) {
+      redA[w * 16 + r] = a1;
+      redA[(NW + w) * 16 + r] = a2;
+    }
+    lds_barrier();
+    if (w == 0) {
+      a1 = redA[r];
+      a2 = redA[NW * 16 + r];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) {
+        a1 += redA[i * 16 + r];
+        a2 += redA[(NW + i) * 16 + r];
+      }
+    }
+    lds_barrier();   // redM/redA may be reused by a following chunk
+  }
+  A1 = a1 < SAT_LO ? SAT_LO : (a1 > SAT_HI ? SAT_HI : a1);
+  A2 = a2 < SAT_LO ? SAT_LO : (a2 > SAT_HI ? SAT_HI : a2);
+  M1 = m1;
+  M2 = m2;
+}
+
 // chunk_AM for up to S sequences at once: x of sequence s in LDS at
 // xs + s*nT*16 / xes + s*nT (ns <= S valid).  One pass over the weight
 // registers forms every sequence's tile sums, so the chunk's weights are

@@ -61,6 +61,7 @@ constexpr int PT_THREADS = 512;   // 8 waves: the attention body's workgroup siz
 constexpr int PT_NW = PT_THREADS / 64;
 constexpr int PT_HEAD_D64 = 9;    // head rows of at most 576 elements
 constexpr unsigned long long PT_SPIN_TICKS = 200000000ull;   // 2 s at 100 MHz
+constexpr int PT_POLL_STAGGER = 12;   // s_sleep units (64 clocks): ~0.3 us between the first two polls
 
 // --------------------------------------------------------- memory access
 // The roles are separate functions (their register allocations stay apart),
@@ -81,6 +82,18 @@ template <class T>
 __device__ __forceinline__ T cload(const PT_CONST T *p) {
   return *(const T *)p;
 }
+// A role function receives its arguments in vector registers, so the
+// compiler treats them as varying across lanes (per-lane loads, and a loop
+// around every buffer access whose descriptor derives from them).  They are
+// the same in every lane: take lane 0's value into scalar registers.
+template <class T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+  const unsigned long long u = (unsigned long long)p;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+  return (T *)(((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ int uniform_int(int v) { return __builtin_amdgcn_readfirstlane(v); }
 constexpr int CPOL_SC1 = 16;   // buffer-instruction cache policy: SC1 (device scope)
 
 template <class T>
@@ -120,19 +133,15 @@ __device__ __forceinline__ void load_chunk_rs(ChunkRegs<TPT> &R, const void *wm,
   }
 }
 
-// This thread's gammas (elements tid and tid + blockDim; D <= 2 * PT_THREADS)
-// of one norm, prefetched with the layer's weights.
+// This thread's gammas (elements 2t and 2t + 1; D <= 2 * PT_THREADS) of one
+// norm, prefetched with the layer's weights (one 16-byte load).
 struct Gammas {
   double v[2];
 };
 __device__ __forceinline__ void load_gammas(Gammas &G, const double *g, int D) {
-  const rsrc_t r = rsrc(g, D * 8);
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    typedef unsigned v2u __attribute__((ext_vector_type(2)));
-    const v2u u = __builtin_amdgcn_raw_buffer_load_b64(r, (threadIdx.x + k * PT_THREADS) * 8, 0, 0);
-    G.v[k] = __longlong_as_double((long long)(((unsigned long long)u.y << 32) | u.x));
-  }
+  const uint4 u = ld_b128<0>(rsrc(g, D * 8), threadIdx.x * 16);   // past D: zeros
+  G.v[0] = __longlong_as_double((long long)(((unsigned long long)u.y << 32) | u.x));
+  G.v[1] = __longlong_as_double((long long)(((unsigned long long)u.w << 32) | u.z));
 }
 
 // Tagged activation word.
@@ -158,28 +167,37 @@ struct Wait {
     }
     return false;
   }
+  // Spin until the words carry `tag`: after the first miss two polls stay
+  // in flight, about half a round trip apart (the sleep staggers the first
+  // two; each later poll is issued before the oldest is checked), so a
+  // store is seen about half a round trip sooner than with one poll at a
+  // time.
   __device__ __forceinline__ unsigned word(rsrc_t r, int off, unsigned tag) {
     unsigned v = ld_coh(r, off);
     if ((v >> 24) == tag || aborted) return v;
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    unsigned prev = ld_coh(r, off);
+    __builtin_amdgcn_s_sleep(PT_POLL_STAGGER);
     for (unsigned it = 1;; ++it) {
-      __builtin_amdgcn_s_sleep(1);
-      v = ld_coh(r, off);
-      if ((v >> 24) == tag || give_up(it, t0)) return v;
+      const unsigned next = ld_coh(r, off);
+      if ((prev >> 24) == tag || give_up(it, t0)) return prev;
+      prev = next;
     }
   }
   // four consecutive words (16-byte aligned, byte offset off) in one load
+  __device__ __forceinline__ static bool ok4(const uint4 &v, unsigned tag) {
+    return (v.x >> 24) == tag && (v.y >> 24) == tag && (v.z >> 24) == tag && (v.w >> 24) == tag;
+  }
   __device__ __forceinline__ uint4 quad(rsrc_t r, int off, unsigned tag) {
-    auto ok = [&](const uint4 &v) {
-      return (v.x >> 24) == tag && (v.y >> 24) == tag && (v.z >> 24) == tag && (v.w >> 24) == tag;
-    };
     uint4 v = ld_b128<CPOL_SC1>(r, off);
-    if (ok(v) || aborted) return v;
+    if (ok4(v, tag) || aborted) return v;
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    uint4 prev = ld_b128<CPOL_SC1>(r, off);
+    __builtin_amdgcn_s_sleep(PT_POLL_STAGGER);
     for (unsigned it = 1;; ++it) {
-      __builtin_amdgcn_s_sleep(1);
-      v = ld_b128<CPOL_SC1>(r, off);
-      if (ok(v) || give_up(it, t0)) return v;
+      const uint4 next = ld_b128<CPOL_SC1>(r, off);
+      if (ok4(prev, tag) || give_up(it, t0)) return prev;
+      prev = next;
     }
   }
 };
@@ -307,6 +325,7 @@ struct AttnCohIO {
 // Role entry: the argument block (device memory) as scalars, the wait
 // state in registers, the dynamic LDS as LDS.
 #define PT_ENTER()                                  \
+  pp = uniform_ptr(pp);                             \
   const PersistArgs p = cload(pp);                  \
   Wait w{rsrc(p.abort_flag, 4), false};             \
   dsm = lds(dsm);                                   \
@@ -434,7 +453,12 @@ __device__ __forceinline__ int end_of_step(const PersistArgs &p, int s, double *
 template <int PPW, bool SHORT>
 __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
   PT_ENTER();
+  c = uniform_int(c);
   const int D = p.D, nT = D / 16, nq = D + 2 * p.KV;
+  // the step's RoPE row (HD/2 x (cos, sin)) for the attention, in LDS ahead
+  // of the norm and attention work space
+  double *rope_s = dsm;
+  dsm += 64;
   double *dbuf = dsm;
   double *leaf = dsm + 3 * D;
   int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);
@@ -452,15 +476,17 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
     if (c == 0 && threadIdx.x == 0 && p.clock) put_clock(p.clock, s);
     const rsrc_t rq = rsrc(p.t_qkv + (s & 1) * nq);
     for (int l = 0; l < p.NL; ++l) {
-      const LayerArgs a = cload(L + l);
+      LayerArgs a = cload(L + l);
       const unsigned tg = tag_of(s, l, p.NL);
+      double rope_v = 0.0;   // loaded now, stored to LDS before the attention
+      if (c < p.n_att && threadIdx.x < 64) rope_v = a.rope[(long long)s * 64 + threadIdx.x];
       if (l == 0)
         embed_vec(p, tok, hm, he);
       else
         wait_bfp(w, rsrc(p.t_h + (s & 1) * D), D, tag_of(s, l - 1, p.NL), hm, he);
       lds_barrier();
       stamp(p, c == 0, s, l, 0);
-      rmsnorm_to_x_g(hm, he, [&](int k, int) { return k < 2 ? G1.v[k] : 0.0; }, D, xs, xes, dbuf, leaf, nullptr, nullptr);
+      rmsnorm_pairs_to_x(hm, he, G1.v[0], G1.v[1], D, xs, xes, dbuf + D, leaf);
       lds_barrier();
       stamp(p, c == 0, s, l, 10);
       long long A;
@@ -474,6 +500,8 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
       }
       stamp(p, c == 0, s, l, 1);
       if (c < p.n_att) {
+        if (threadIdx.x < 64) rope_s[threadIdx.x] = rope_v;
+        a.rope_row = rope_s;
         lds_barrier();   // the attention reuses the LDS
         AttnCohIO io;
         io.rq = rq;
@@ -504,6 +532,7 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
 // O chunk c: h1 = q(h + Wo att).
 __device__ void role_o(const PT_CONST PersistArgs *pp, double *dsm, int c) {
   PT_ENTER();
+  c = uniform_int(c);
   const int D = p.D, nT = D / 16;
   int *xs = reinterpret_cast<int *>(dsm);
   int *xes = xs + nT * 16;
@@ -552,6 +581,7 @@ __device__ void role_o(const PT_CONST PersistArgs *pp, double *dsm, int c) {
 // G/U chunks (2c, 2c+1): mlp = q(q(silu(g)) * u) of n2 = rmsnorm(h1, g2).
 __device__ void role_gu(const PT_CONST PersistArgs *pp, double *dsm, int c) {
   PT_ENTER();
+  c = uniform_int(c);
   const int D = p.D, nT = D / 16;
   double *dbuf = dsm;
   double *leaf = dsm + 3 * D;
@@ -559,8 +589,8 @@ __device__ void role_gu(const PT_CONST PersistArgs *pp, double *dsm, int c) {
   int *xes = xs + nT * 16;
   int16_t *hm = reinterpret_cast<int16_t *>(xes + nT);
   int8_t *he = reinterpret_cast<int8_t *>(hm + D);
-  __shared__ int redM[PT_NW * 16];
-  __shared__ long long redA[PT_NW * 16];
+  __shared__ int redM[2 * PT_NW * 16];        // G and U
+  __shared__ long long redA[2 * PT_NW * 16];
   ChunkRegs<2> RG, RU;
   Gammas G2;
   auto load_w = [&](int l) {
@@ -577,13 +607,12 @@ __device__ void role_gu(const PT_CONST PersistArgs *pp, double *dsm, int c) {
       wait_bfp(w, r1, D, tg, hm, he);
       lds_barrier();
       stamp(p, c == 0, s, l, 6);
-      rmsnorm_to_x_g(hm, he, [&](int k, int) { return k < 2 ? G2.v[k] : 0.0; }, D, xs, xes, dbuf, leaf, nullptr, nullptr);
+      rmsnorm_pairs_to_x(hm, he, G2.v[0], G2.v[1], D, xs, xes, dbuf + D, leaf);
       lds_barrier();
       stamp(p, c == 0, s, l, 12);
       long long Ag, Au;
       int Mg, Mu;
-      chunk_AM<PT_NW, 2>(RG, xs, xes, nT, redM, redA, Ag, Mg);
-      chunk_AM<PT_NW, 2>(RU, xs, xes, nT, redM, redA, Au, Mu);
+      chunk_AM2<PT_NW, 2>(RG, RU, xs, xes, nT, redM, redA, Ag, Mg, Au, Mu);
       stamp(p, c == 0, s, l, 13);
       if (threadIdx.x < 64) {
         int gm, ge, um, ue, me;
@@ -603,6 +632,7 @@ __device__ void role_gu(const PT_CONST PersistArgs *pp, double *dsm, int c) {
 // D chunk c: h = q(h1 + Wd mlp), the layer's output (and its history row).
 __device__ void role_d(const PT_CONST PersistArgs *pp, double *dsm, int c) {
   PT_ENTER();
+  c = uniform_int(c);
   const int D = p.D, nT = p.FFN / 16;
   int *xs = reinterpret_cast<int *>(dsm);
   int *xes = xs + nT * 16;
@@ -696,8 +726,10 @@ static size_t persist_lds(const PersistArgs &p, int max_ctx) {
   const size_t norm = (size_t)(3 * D + PW_MAX_LEAVES) * 8 + (size_t)nT * 17 * 4 + (size_t)D * 2 + nT;
   const size_t dx = (size_t)nTF * 17 * 4;
   const size_t head = (size_t)(3 * D + PW_MAX_LEAVES) * 8 + (size_t)D * 2 + nT;
-  size_t lds = attn_lds_bytes(max_ctx, attn_ppw(max_ctx));
-  lds = lds > norm ? lds : norm;
+  // the Q|K|V role keeps the step's RoPE row (64 doubles) ahead of both its
+  // norm work space and the attention's
+  size_t lds = attn_lds_bytes(max_ctx, attn_ppw(max_ctx)) + 64 * 8;
+  lds = lds > norm + 64 * 8 ? lds : norm + 64 * 8;
   lds = lds > dx ? lds : dx;
   lds = lds > head ? lds : head;
   return (lds + 15) & ~(size_t)15;
