@@ -352,11 +352,9 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
 /* Batch 1 runs the whole decode as one persistent cooperative launch (one
  * workgroup per compute unit, stages handing over through device-coherent
  * memory) when the dimensions allow it (D <= 576, FFN <= 1536, NL >= 2, the
- * Q|K|V, O, G/U and D chunks of a layer within the compute units) and the
- * KV capacity is at most 512 (the environment variable BFP_PERSIST=1 takes
- * it for every capacity); else, or with this flag or BFP_PERSIST=0, each
- * step is a replayed graph of per-stage kernels.  Both give identical
- * outputs. */
+ * Q|K|V, O, G/U and D chunks of a layer within the compute units); else, or
+ * with this flag or the environment variable BFP_PERSIST=0, each step is a
+ * replayed graph of per-stage kernels.  Both give identical outputs. */
 #define BFP_DECODE_NO_PERSIST 8
 /* Persistent path only: record the device clock (100 MHz) as each stage's
  * input becomes ready and as its output is stored, in the first workgroup of

@@ -14,13 +14,6 @@ pytestmark = pytest.mark.gpu
 TINY = dict(D=128, H_Q=2, H_KV=1, HD=64, FFN=256, NL=2, MAX_CTX=32, VOCAB=512)
 
 
-@pytest.fixture(autouse=True)
-def _persist_every_form(monkeypatch):
-    # the long attention form (capacity > 512) takes the persistent kernel
-    # only when asked
-    monkeypatch.setenv("BFP_PERSIST", "1")
-
-
 def _setup(cfg, seed):
     from bfp import Dims, synth
     from bfp.model import BfpModel

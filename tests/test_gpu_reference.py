@@ -110,21 +110,20 @@ def _digests(hm, he, b, steps, nl):
     return out
 
 
-@pytest.mark.parametrize("path_env", ["default", "persist"])
+@pytest.mark.parametrize("path_env", ["persist", "graph"])
 def test_config4_decode_on_gpu(gpu, path_env, monkeypatch):
     """BASELINE config 4 on the 30-layer model: 48-token prompt decoded
     through position 2047 (the long-context attention form, 9 heads over 3
     KV groups, up to 2048 positions), every step's 30 layer outputs (as a
     digest) and every token against the reference's own run -- on the
-    default path (the per-stage graph at this capacity) and on the
-    persistent kernel."""
+    persistent kernel (the default) and on the per-stage graph."""
     from bfp import Dims, synth
     from bfp.model import BfpModel
     path = GOLDEN / "ref_decode_cfg4.npz"
     if not path.exists():
         pytest.skip("ref_decode_cfg4.npz not generated")
-    if path_env == "persist":
-        monkeypatch.setenv("BFP_PERSIST", "1")
+    if path_env == "graph":
+        monkeypatch.setenv("BFP_PERSIST", "0")
     f = np.load(path)
     prompt = f["prompt"]
     n_gen = len(f["tokens"])

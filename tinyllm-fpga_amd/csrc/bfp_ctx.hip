@@ -187,14 +187,10 @@ void stage_lens(const bfp_dims &d, int len[ST_COUNT]) {
   for (int i = 0; i < ST_COUNT; ++i) len[i] = L[i];
 }
 
-// BFP_PERSIST: unset -> the persistent kernel for the short attention forms
-// (capacity <= 512; above it the long form inside the persistent kernel is
-// slower than the graph's own launch); "1" -> every form; "0" -> never.
-bool persist_enabled(int max_ctx) {
+// BFP_PERSIST=0 keeps batch-1 decodes on the per-stage graph.
+bool persist_enabled() {
   const char *v = getenv("BFP_PERSIST");
-  if (v && v[0] == '0') return false;
-  if (v && v[0] == '1') return true;
-  return attn_ppw(max_ctx) != 8;
+  return !(v && v[0] == '0');
 }
 
 // The whole batch-1 decode as one persistent launch (bfp_persist.hip).
@@ -1030,7 +1026,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
 
   PersistArgs pa{};
   int grid = 0;
-  if (batch == 1 && !(flags & (BFP_DECODE_NO_GRAPH | BFP_DECODE_NO_PERSIST)) && persist_enabled(c->max_ctx) &&
+  if (batch == 1 && !(flags & (BFP_DECODE_NO_GRAPH | BFP_DECODE_NO_PERSIST)) && persist_enabled() &&
       persist_plan(d, c->max_ctx, c->device, pa, grid)) {
     BFP_TRY(decode_persist(c, pa, grid, dprompt, n_prompt, n_gen, dout, dhm, dhe, rtl_loop,
                            (flags & BFP_DECODE_TRACE) != 0));
