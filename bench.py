@@ -231,9 +231,15 @@ def kernel_config(n_in):
 
 
 def kernel_name(n_out, n_in, reps):
-    """The matvec kernel the library launches (one 16-row chunk of one
-    problem per workgroup, csrc/bfp_core.hip:launch_matvec)."""
+    """The matvec kernel the library launches (csrc/bfp_core.hip:
+    launch_matvec): two 16-row chunks of one problem per workgroup for
+    576-input shapes with an even chunk count, the buffer-load form for
+    1536-input ones, else one chunk per workgroup."""
     nw, tpt = kernel_config(n_in)
+    if nw == 3 and tpt == 3 and (n_out // 16) % 2 == 0:
+        return "matvec2_kernel<3,3>"
+    if nw == 8 and tpt == 3:
+        return "matvec_kernel<8,3,true>"
     return "matvec_kernel<%d,%d>" % (nw, tpt)
 
 
@@ -563,9 +569,9 @@ def cpu_decode_baselines():
 def stream_probe():
     """Practical HBM ceilings: a 1 GiB device-to-device copy (read + write
     bytes) and a 4 GiB streaming read with the library's bfp_probe_read_d
-    (16-byte loads, a contiguous range per workgroup, 4 workgroups per CU),
-    with ordinary and with non-temporal loads (the matvec's weight-stream
-    policy).  The best read is the ceiling the matvec is compared with."""
+    (16-byte loads, 16 KB per workgroup, 262144 workgroups), with ordinary
+    and with non-temporal loads (the matvec's weight-stream policy).  The
+    best read is the ceiling the matvec is compared with."""
     import torch
     from bfp import _dev
     from bfp._lib import call
@@ -573,7 +579,7 @@ def stream_probe():
     b = torch.empty_like(a)
     a.fill_(1)
     f = torch.ones(1 << 30, dtype=torch.float32, device="cuda")       # 4 GiB
-    n_wg = torch.cuda.get_device_properties(0).multi_processor_count * 4
+    n_wg = (4 << 30) // 16384
     fold = torch.empty(n_wg, dtype=torch.int32, device="cuda")
 
     def read(nt):

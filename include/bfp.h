@@ -153,9 +153,11 @@ int bfp_matvec_ring_d(const void *P_m, const void *P_e, int n_out, int n_in, int
 /* Measurement probe, no reference counterpart: reads [p, p + bytes) once
  * with 16-byte loads (non-temporal when nt != 0, the matvec's weight-stream
  * policy), each of n_wg workgroups of 256 threads streaming one contiguous
- * range, writing one fold word per workgroup to out (n_wg words).  Its
+ * range and folding it into one word, stored to out[w] (n_wg words) only
+ * when it equals a fixed sentinel, so out is normally left untouched.  Its
  * bytes / time is the practical HBM read ceiling the matvec is compared
- * with.  bytes % 16 == 0, and every workgroup gets at least one word. */
+ * with (fastest with 16 KB per workgroup).  bytes % 16 == 0, every
+ * workgroup gets at least one word and at most 1 GiB. */
 int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, int nt, void *stream);
 
 /* Host-buffer convenience form of matvec_hw_golden: W in the reference

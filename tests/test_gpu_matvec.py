@@ -152,6 +152,46 @@ def test_matvec_batched_ring(gpu):
         assert (ye[i] == want_e).all() and (ym[i] == want_m.reshape(-1)).all()
 
 
+@pytest.mark.parametrize("n_out,n_in", [(192, 576), (48, 1536), (16, 576)],
+                         ids=["chunk-pairs", "buffer-load", "one-chunk"])
+def test_matvec_output_alignment(gpu, n_out, n_in):
+    """Outputs at a 2-byte-aligned address (the dword store form needs 4)
+    give the same bits as at an aligned one, for each kernel form; the
+    bytes on both sides of the output are left alone."""
+    import torch
+    from bfp import _dev
+    from bfp._lib import call
+    rng = np.random.default_rng(n_out + n_in)
+    W = rng.standard_normal((n_out, n_in)).astype(np.float32) * np.float32(0.02)
+    n_mats = 3
+    X = rng.standard_normal((n_mats, n_in))
+    bm, be = n_out * n_in * 2, n_out * n_in // 16
+    Pm = torch.empty(bm, dtype=torch.uint8, device="cuda")
+    Pe = torch.empty(be, dtype=torch.uint8, device="cuda")
+    dW = _dev.to_dev(W)
+    call("bfp_quantize_pack_f32_d", dW.data_ptr(), n_out, n_in, Pm.data_ptr(), Pe.data_ptr(),
+         _dev.stream())
+    xq = [sim.tile_quantize(X[i]) for i in range(n_mats)]
+    dxm = _dev.to_dev(np.stack([q[0].reshape(-1) for q in xq]))
+    dxe = _dev.to_dev(np.stack([q[1] for q in xq]))
+    outs = []
+    for off in (0, 1):
+        ym = torch.full((n_mats * n_out + 2,), 0x5A5A, dtype=torch.int16, device="cuda")
+        ye = torch.empty(n_mats * n_out // 16, dtype=torch.int8, device="cuda")
+        call("bfp_matvec_ring_d", Pm.data_ptr(), Pe.data_ptr(), n_out, n_in, n_mats, 1, bm, be,
+             dxm.data_ptr(), dxe.data_ptr(), n_in, ym.data_ptr() + 2 * off, ye.data_ptr(), n_out,
+             0, _dev.stream())
+        h = ym.cpu().numpy()
+        assert h[0] == 0x5A5A or off == 0
+        assert h[off + n_mats * n_out] == 0x5A5A
+        outs.append((h[off:off + n_mats * n_out].reshape(n_mats, -1), ye.cpu().numpy()))
+    assert (outs[0][0] == outs[1][0]).all() and (outs[0][1] == outs[1][1]).all()
+    Wm, We = _oracle_quantize_W(W)
+    for i in range(n_mats):
+        want_m, _ = sim.matvec_bfp(xq[i][0], xq[i][1], Wm, We)
+        assert (outs[1][0][i] == want_m.reshape(-1)).all()
+
+
 def _neg_full_scale_case():
     """One output row with A = -(2^20 - 1) at M = 30: y = -1048575 rounds to
     mantissa -32768 at e = 20 (raw); re-quantised it is (-16384, 21)."""

@@ -233,10 +233,29 @@ __global__ void tile_decode_kernel(const int16_t *__restrict__ m, const int8_t *
 }
 
 // ------------------------------------------------------------------ matvec
+// Output stores of the standalone matvec.  A few scattered partial-line
+// writes per workgroup cost the streaming read several percent (a 64-byte
+// store per 36 KB one-shot workgroup read: 6.6-6.7 TB/s against 7.2 without
+// it); as dwords with the non-temporal policy the cost mostly goes (7.0).
+// 2-byte stores with that policy were slower than plain ones.
+// Lanes 0-15 hold rows 0-15 (m); the 16 mantissas go out as 8 dwords of row
+// pairs when yr is 4-byte aligned.
+__device__ __forceinline__ void store_rows16(int16_t *yr, int m, int lane) {
+  if ((reinterpret_cast<uintptr_t>(yr) & 3) == 0) {
+    const int src = (lane & 7) * 2;
+    const int a = __shfl(m, src, 64), b = __shfl(m, src + 1, 64);
+    const unsigned w = ((unsigned)a & 0xffffu) | ((unsigned)b << 16);
+    if (lane < 8) __builtin_nontemporal_store(w, reinterpret_cast<unsigned *>(yr) + lane);
+  } else if (lane < 16) {
+    yr[lane] = (int16_t)m;
+  }
+}
+
 // Standalone matvec: one 16-row chunk of one problem per workgroup (the
 // engine and its exactness argument are in bfp_mv.h).  Problem r reads
-// matrix (r mod ring) when ring > 0.
-template <int NW, int TPT>
+// matrix (r mod ring) when ring > 0.  BUF: the weights through buffer
+// loads (load_chunk_buf).
+template <int NW, int TPT, bool BUF = false>
 __global__ __launch_bounds__(64 * NW) void matvec_kernel(
     const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
     long long smat_e, int nT, int n_chunks, int ring, const int16_t *__restrict__ xm,
@@ -254,8 +273,12 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
 
   ChunkRegs<TPT> R;
   const long long cc = (long long)c * cstride;   // chunk c of this matrix in the layout
-  load_chunk<NW, TPT, true>(R, Pm + wmat * smat_m + cc * nT * 32, Pe + wmat * smat_e + cc * nT * 16,
+  if constexpr (BUF)
+    load_chunk_buf<NW, TPT>(R, Pm + wmat * smat_m + cc * nT * 32, Pe + wmat * smat_e + cc * nT * 16,
                             nT);
+  else
+    load_chunk<NW, TPT, true>(R, Pm + wmat * smat_m + cc * nT * 32, Pe + wmat * smat_e + cc * nT * 16,
+                              nT);
   stage_x_bfp(xs, xes, xm + mat * x_stride, xe + mat * (x_stride / 16), nT);
   __syncthreads();
   long long A;
@@ -265,37 +288,103 @@ __global__ __launch_bounds__(64 * NW) void matvec_kernel(
     int m, e;
     chunk_quant(A, M, m, e);
     const int lane = threadIdx.x;
-    if (lane < 16) ym[mat * y_stride + c * 16 + lane] = (int16_t)m;
+    store_rows16(ym + mat * y_stride + c * 16, m, lane);
     if (lane == 0) ye[mat * (y_stride / 16) + c] = (int8_t)e;
   }
 }
 
+// Two adjacent 16-row chunks of one problem per workgroup: both chunks'
+// weight loads are issued before any arithmetic, and one pass (chunk_AM2)
+// forms both chunks' rows, so a workgroup streams twice the bytes per
+// barrier round.  n_chunks is even.  On 576-input chunks (three waves) this
+// streamed 7.11 TB/s on the 49152 x 576 sweep against 6.80 for one chunk per
+// workgroup; on the 1536-input chunk (eight waves) it was slower (6.42
+// against 6.63), so that shape keeps one chunk per workgroup.
+template <int NW, int TPT>
+__global__ __launch_bounds__(64 * NW) void matvec2_kernel(
+    const uint4 *__restrict__ Pm, const int8_t *__restrict__ Pe, long long smat_m,
+    long long smat_e, int nT, int n_chunks, int ring, const int16_t *__restrict__ xm,
+    const int8_t *__restrict__ xe, long long x_stride, int16_t *__restrict__ ym,
+    int8_t *__restrict__ ye, long long y_stride, int cstride) {
+  extern __shared__ int smem[];
+  int *xs = smem;              // nT * 16
+  int *xes = smem + nT * 16;   // nT
+  __shared__ int redM[2 * NW * 16];
+  __shared__ long long redA[2 * NW * 16];
+  const int pairs = n_chunks / 2;
+  const int mat = blockIdx.x / pairs;
+  const int c = 2 * (blockIdx.x - mat * pairs);
+  const int wmat = ring > 0 ? mat % ring : mat;
+  ChunkRegs<TPT> R1, R2;
+  const long long c1 = (long long)c * cstride, c2 = (long long)(c + 1) * cstride;
+  load_chunk<NW, TPT, true>(R1, Pm + wmat * smat_m + c1 * nT * 32, Pe + wmat * smat_e + c1 * nT * 16, nT);
+  load_chunk<NW, TPT, true>(R2, Pm + wmat * smat_m + c2 * nT * 32, Pe + wmat * smat_e + c2 * nT * 16, nT);
+  stage_x_bfp(xs, xes, xm + mat * x_stride, xe + mat * (x_stride / 16), nT);
+  __syncthreads();
+  long long A1, A2;
+  int M1, M2;
+  chunk_AM2<NW, TPT>(R1, R2, xs, xes, nT, redM, redA, A1, M1, A2, M2);
+  if (threadIdx.x < 64) {
+    int m1, e1, m2, e2;
+    chunk_quant(A1, M1, m1, e1);
+    chunk_quant(A2, M2, m2, e2);
+    const int lane = threadIdx.x;
+    int16_t *yr = ym + mat * y_stride + c * 16;   // 32 contiguous mantissas
+    if ((reinterpret_cast<uintptr_t>(yr) & 3) == 0) {
+      // as 16 dwords of row pairs with non-temporal stores (store_rows16):
+      // lane L writes rows 2L, 2L + 1 of the pair (chunk c for L < 8, chunk
+      // c + 1 above)
+      const int src = (lane & 7) * 2;
+      const int a1 = __shfl(m1, src, 64), b1 = __shfl(m1, src + 1, 64);
+      const int a2 = __shfl(m2, src, 64), b2 = __shfl(m2, src + 1, 64);
+      const int lo = lane < 8 ? a1 : a2, hi = lane < 8 ? b1 : b2;
+      const unsigned w = ((unsigned)lo & 0xffffu) | ((unsigned)hi << 16);
+      if (lane < 16) __builtin_nontemporal_store(w, reinterpret_cast<unsigned *>(yr) + lane);
+    } else if (lane < 16) {
+      yr[lane] = (int16_t)m1;
+      yr[16 + lane] = (int16_t)m2;
+    }
+    if (lane == 0) {
+      ye[mat * (y_stride / 16) + c] = (int8_t)e1;
+      ye[mat * (y_stride / 16) + c + 1] = (int8_t)e2;
+    }
+  }
+}
+
 // Read-only streaming probe: workgroup w reads the contiguous range
-// [w*per, (w+1)*per) of 16-byte words, eight loads in flight per thread
-// (addresses clamped, so there is no branch around a load), folded into one
-// word per workgroup so the loads cannot be dropped.  NT: the loads carry
-// the non-temporal cache policy, as the matvec's weight stream does.
-// Measures the practical HBM read ceiling the matvec is compared with.
+// [w*per, (w+1)*per) of 16-byte words through a buffer resource over that
+// range (four loads in flight per thread; loads past its end read 0, so
+// there is no branch around a load), folded into one word per workgroup that
+// is stored only when it equals a fixed sentinel, so the loads cannot be
+// dropped.  NT: the loads carry the non-temporal cache
+// policy (bit 1 of the policy operand), as the matvec's weight stream does.
+// Measures the practical HBM read ceiling the matvec is compared with; with
+// per = 1024 (16 KB per workgroup, every workgroup resident at once on a
+// 4 GiB read) this measured 7.3-7.4 TB/s, against 7.1-7.2 for a few
+// workgroups per CU each streaming a long range.
 template <bool NT>
 __global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *__restrict__ p,
                                                          long long n16, long long per,
                                                          unsigned *__restrict__ out) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  constexpr int POL = NT ? 2 : 0;
   const long long i0 = blockIdx.x * per;
-  const long long i1 = i0 + per < n16 ? i0 + per : n16;
+  const int n = (int)(i0 + per < n16 ? per : n16 - i0);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4 *>(p + i0), (short)0, n * 16, 0x00020000);
   unsigned acc = 0;
-  for (long long b = i0; b < i1; b += 8 * 256) {
-    uint4 v[8];
+  for (int b = 0; b < n; b += 4 * 256) {
+    v4u v[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      long long i = b + k * 256 + threadIdx.x;
-      i = i < i1 ? i : i1 - 1;
-      v[k] = NT ? ld_nt(p + i) : p[i];
-    }
+    for (int k = 0; k < 4; ++k)
+      v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, (b + k * 256 + (int)threadIdx.x) * 16, 0, POL);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    for (int k = 0; k < 4; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
   }
-  acc = acc ^ (unsigned)peer<1>((int)acc);
-  if (threadIdx.x == 0) out[blockIdx.x] = acc;
+  // The compare keeps the loads live without a store per workgroup: one
+  // 4-byte store per 16 KB workgroup cost 4% of the read rate (the lines
+  // written are shared by workgroups on different XCDs).
+  if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
 }
 
 // Narrow embedding rows of n token ids, one workgroup per id: the mantissa
@@ -378,12 +467,18 @@ int launch_matvec(const void *P_m, const void *P_e, int n_out, int n_in, int n_m
                    n_in, nw, tpt);
   const int n_chunks = n_out / 16;
   long long blocks = (long long)n_chunks * n_mats;
+  if (nw == 3 && tpt == 3 && n_chunks % 2 == 0) {
+    fn = matvec2_kernel<3, 3>;
+    blocks /= 2;
+  } else if (nw == 8 && tpt == 3) {
+    fn = matvec_kernel<8, 3, true>;
+  }
   if (blocks > INT_MAX) return set_err(BFP_EINVAL, "matvec: grid too large");
   size_t shm = (size_t)nT * 17 * sizeof(int);
   if (shm > 60 * 1024) return set_err(BFP_EINVAL, "matvec: n_in=%d too large", n_in);
-  // One 16-row chunk of one problem per workgroup, for every batch length:
-  // the workgroups run in order, so a batch walks its problems (and a ring
-  // of weight copies) in sequence.  (A fixed grid in which each workgroup
+  // One 16-row chunk (two on 576-input shapes) of one problem per
+  // workgroup, for every batch length: the workgroups run in order, so a
+  // batch walks its problems (and a ring of weight copies) in sequence.  (A fixed grid in which each workgroup
   // streamed a contiguous range of chunks measured 5.5 TB/s on HBM-resident
   // weights against this form's 6.8.)
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * nw), shm, stream,
@@ -559,6 +654,8 @@ int bfp_probe_read_d(const void *p, size_t bytes, uint32_t *out, int n_wg, int n
   const long long per = (n16 + n_wg - 1) / n_wg;
   if ((long long)(n_wg - 1) * per >= n16)
     return set_err(BFP_EINVAL, "probe_read: %d workgroups leave some without words", n_wg);
+  if (per > (1LL << 26))
+    return set_err(BFP_EINVAL, "probe_read: more than 1 GiB per workgroup (n_wg=%d)", n_wg);
   hipLaunchKernelGGL(nt ? probe_read_kernel<true> : probe_read_kernel<false>, dim3(n_wg),
                      dim3(256), 0, (hipStream_t)stream, reinterpret_cast<const uint4 *>(p), n16,
                      per, reinterpret_cast<unsigned *>(out));

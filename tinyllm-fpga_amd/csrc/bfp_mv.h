@@ -48,6 +48,33 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<TPT> &R, const uint4 *__res
   }
 }
 
+// Same through buffer instructions with the nt cache policy (bit 1 of the
+// policy operand): every load is unconditional, tiles past nT fall outside
+// the buffer's range and read 0.  On the 1536-input chunk (eight waves) this
+// streamed 6.95 TB/s against 6.62 for load_chunk; on 576-input chunks
+// (three waves) it was slower (6.41 against 6.83).
+template <int NW, int TPT>
+__device__ __forceinline__ void load_chunk_buf(ChunkRegs<TPT> &R, const uint4 *pm, const int8_t *pe,
+                                               int nT) {
+  constexpr int POL = 2;
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t rm =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(pm), (short)0, nT * 512, 0x00020000);
+  const __amdgpu_buffer_rsrc_t re =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(pe), (short)0, nT * 16, 0x00020000);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, tq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    const int t = tq + 4 * (w + NW * j);
+    const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rm, (t * 32 + r) * 16, 0, POL);
+    const v4u b = __builtin_amdgcn_raw_buffer_load_b128(rm, (t * 32 + 16 + r) * 16, 0, POL);
+    R.a[j] = make_uint4(a.x, a.y, a.z, a.w);
+    R.b[j] = make_uint4(b.x, b.y, b.z, b.w);
+    R.e[j] = (int)(signed char)__builtin_amdgcn_raw_buffer_load_b8(re, t * 16 + r, 0, POL);
+  }
+}
+
 // Same, with every load unconditional (tiles past nT re-read tile nT-1; the
 // engine ignores those lanes), so the loads of several chunks can be kept in
 // flight without the compiler draining them at a branch.
