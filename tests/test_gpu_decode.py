@@ -74,6 +74,47 @@ def test_head_batched_equals_single_d576(gpu):
     gm.close()
 
 
+@pytest.mark.parametrize("D,vocab", [(576, 4176), (128, 512), (192, 1040)],
+                         ids=["d576-ragged", "d128", "d192"])
+def test_head_sequence_lanes_equal_single(gpu, D, vocab):
+    """The batched head with sequences on the lanes (k_head_seq, batches of
+    32 and more) over 70 sequences -- a full lane group of 64 and a partial
+    one -- equals the single-sequence head bit for bit, logits and argmax.
+    The vocabulary leaves a short last workgroup (4176 rows in 32-row
+    workgroups).  Tied logits: rows 5 and 9 (one workgroup) hold the same
+    vector V and rows 3 and 40 (two workgroups) hold -V, scaled so that for
+    most sequences one of the two ties holds the largest logit: the argmax is
+    then the tie's first row."""
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    H = D // 64
+    cfg = dict(D=D, H_Q=H, H_KV=1, HD=64, FFN=2 * D, NL=1, MAX_CTX=8, VOCAB=vocab)
+    d = Dims(**cfg)
+    fm = synth.make_model(d, seed=31)
+    V = fm.embed[7].copy() * np.float32(60.0)
+    fm.embed[5] = V
+    fm.embed[9] = V
+    fm.embed[3] = -V
+    fm.embed[40] = -V
+    gm = BfpModel(d, max_batch=70)
+    gm.load_fp32(fm)
+    rng = np.random.default_rng(31)
+    hs = [sim.fp_quantize_vec(rng.standard_normal(d.D) * (0.3 + 0.01 * b)) for b in range(70)]
+    q = [sim.tile_quantize(h) for h in hs]
+    am, lg = gm.head(np.stack([x[0].reshape(-1) for x in q]), np.stack([x[1] for x in q]),
+                     logits=True)
+    n_tie = 0
+    for b in range(70):
+        a1, l1 = gm.head(q[b][0].reshape(1, -1), q[b][1].reshape(1, -1), logits=True)
+        assert (lg[b].view(np.int64) == l1[0].view(np.int64)).all(), b
+        assert am[b] == a1[0] == int(np.argmax(lg[b])), b     # np.argmax: first index
+        if lg[b][am[b]] in (lg[b][5], lg[b][3]):
+            assert am[b] in (3, 5), (b, am[b])
+            n_tie += 1
+    assert n_tie >= 40, n_tie
+    gm.close()
+
+
 @pytest.mark.parametrize("graph", [True, False], ids=["graph", "direct"])
 def test_decode_tiny(gpu, graph):
     d, om, gm = _setup(TINY, seed=5)

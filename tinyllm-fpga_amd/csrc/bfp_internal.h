@@ -76,7 +76,7 @@ int prepare_head_kernels(int D);
 // Raise a kernel's dynamic-LDS limit on the current device to at least
 // `bytes` (never lowering it: the limit is process-wide per device).
 int raise_lds_limit(const void *f, int bytes);
-int head_workgroups(int vocab, int D, int rows_single, int batch);
+int head_workgroups(int vocab, int D, int rows_single, int batch, bool have64);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);
 int launch_ctl(const CtlArgs &a, hipStream_t s);

@@ -800,9 +800,136 @@ int launch_embed(const EmbedArgs &a, hipStream_t s) {
 
 // Head workgroups for `batch` sequences: the batch-1 kernel covers
 // rows_single rows per workgroup, the batch > 1 GEMV HEAD_ROWS_MULTI.
-int head_workgroups(int vocab, int D, int rows_single, int batch) {
+// Batched head on the float64 matrix cores (batch >= HEAD_SEQ_MIN).
+// v_mfma_f64_16x16x4f64 computes every output as four FMAs in k order, each
+// rounded (checked on the GPU against FMA chains over a million outputs:
+// bit-equal, while separate multiply-adds or other orders differ), so
+// partial l of a logit -- the FMA chain over k = 64i + 4l + c, i then c
+// ascending, of k_head_logits / k_head_gemv -- is one accumulator fed by
+// NB MFMAs (one per 64-column block i, c on the instruction's k axis).
+// A wave computes a tile of 16 rows x 16 sequences: accumulator l holds
+// partial l of all 256 logits; the 16 partials are then summed in the
+// butterfly order of those kernels (q and q + 8, then 4 apart, 2, 1) inside
+// each lane, so the logits are bit-identical to theirs.
+// Operands: A (lane L: row L % 16, c = L / 16) from the float64 embedding
+// copy permuted at load time so that a lane's 16 values of block i are
+// contiguous (e64p[row][(4i + c) * 16 + l] = embed[row][64i + 4l + c]); B
+// (lane L: c = L / 16, sequence L % 16) from the workgroup's 16 normed
+// hidden vectors in LDS, laid out [i][l][c][sequence].  Output (lane L,
+// element v) is row 4v + L / 16, sequence L % 16.
+// Workgroup: 4 waves, 16 sequences (blockIdx.y), rows [x * rpw, + rpw) in
+// 16-row tiles dealt to the waves in turn; its per-sequence first-index
+// argmax goes to part_v / part_i.
+typedef double head_d4 __attribute__((ext_vector_type(4)));
+constexpr int HEAD_MX_WAVES = 4;
+inline int head_mx_lds(int D) { return 16 * D * 8 + HEAD_MX_WAVES * 16 * 4 * 12; }
+
+template <int NB>
+__global__ __launch_bounds__(64 * HEAD_MX_WAVES) void k_head_mx(HeadArgs a, int rpw) {
+  extern __shared__ double hsx[];
+  double *hb = hsx;                                       // [i][l][c][16 sequences]
+  double *bvs = hsx + 16 * 64 * NB;                       // [wave][lane / 16 group][sequence]
+  int *bis = reinterpret_cast<int *>(bvs + HEAD_MX_WAVES * 64);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int s0 = blockIdx.y * 16;
+  const int ns = a.batch - s0 < 16 ? a.batch - s0 : 16;
+  // stage the 16 sequences' normed hidden: element (i, l, c, s) = hn[s][64i + 4l + c]
+  for (int q = threadIdx.x; q < 16 * 64 * NB; q += blockDim.x) {
+    const int s = q & 15, c = (q >> 4) & 3, l = (q >> 6) & 15, i = q >> 10;
+    const int sc = s < ns ? s : ns - 1;
+    hb[q] = a.hn[(long long)(s0 + sc) * a.D + 64 * i + 4 * l + c];
+  }
+  lds_barrier();
+  const int row_lo = blockIdx.x * rpw;
+  const int row_hi = row_lo + rpw < a.VOCAB ? row_lo + rpw : a.VOCAB;
+  double bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const double *bl = hb + lane;                           // + (16i + l) * 64
+  for (int r0 = row_lo + 16 * w; r0 < row_hi; r0 += 16 * HEAD_MX_WAVES) {
+    const double2 *ap = reinterpret_cast<const double2 *>(
+        a.embed64 + (long long)(r0 + (lane & 15)) * a.D + (lane >> 4) * 16);   // + 64 i doubles
+    head_d4 acc[16];
+#pragma unroll
+    for (int l = 0; l < 16; ++l) acc[l] = head_d4{0.0, 0.0, 0.0, 0.0};
+    double2 av[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) av[k] = ap[k];
+#pragma unroll 1
+    for (int i = 0; i < NB; ++i) {
+      double2 an[8];
+      if (i + 1 < NB) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) an[k] = ap[32 * (i + 1) + k];
+      }
+#pragma unroll
+      for (int l = 0; l < 16; ++l) {
+        const double av_l = (l & 1) ? av[l >> 1].y : av[l >> 1].x;
+        acc[l] = __builtin_amdgcn_mfma_f64_16x16x4f64(av_l, bl[(16 * i + l) * 64], acc[l], 0, 0, 0);
+      }
+      if (i + 1 < NB) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) av[k] = an[k];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      double q8[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) q8[q] = acc[q][v] + acc[q + 8][v];
+      const double q4[4] = {q8[0] + q8[4], q8[1] + q8[5], q8[2] + q8[6], q8[3] + q8[7]};
+      const double x = (q4[0] + q4[2]) + (q4[1] + q4[3]);
+      const int row = r0 + 4 * v + (lane >> 4);
+      const int s = lane & 15;
+      if (a.logits && s < ns) a.logits[(long long)(s0 + s) * a.VOCAB + row] = x;
+      if (x > bv || (x == bv && row < bi)) {
+        bv = x;
+        bi = row;
+      }
+    }
+  }
+  bvs[w * 64 + lane] = bv;
+  bis[w * 64 + lane] = bi;
+  lds_barrier();
+  if (threadIdx.x < 16 && (int)threadIdx.x < ns) {
+    const int s = threadIdx.x;
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    for (int q = 0; q < 4 * HEAD_MX_WAVES; ++q) {   // (wave, lane group) slots of sequence s
+      const double x = bvs[q * 16 + s];
+      const int i = bis[q * 16 + s];
+      if (x > bv || (x == bv && i < bi)) {
+        bv = x;
+        bi = i;
+      }
+    }
+    a.part_v[(long long)(s0 + s) * a.n_wg + blockIdx.x] = bv;
+    a.part_i[(long long)(s0 + s) * a.n_wg + blockIdx.x] = bi;
+  }
+}
+
+typedef void (*head_mx_fn)(HeadArgs, int);
+static head_mx_fn head_mx_kernel(int nb) {
+  switch (nb) {
+    case 1: return k_head_mx<1>;
+    case 2: return k_head_mx<2>;
+    case 3: return k_head_mx<3>;
+    case 4: return k_head_mx<4>;
+    case 5: return k_head_mx<5>;
+    case 6: return k_head_mx<6>;
+    case 7: return k_head_mx<7>;
+    case 8: return k_head_mx<8>;
+    default: return k_head_mx<9>;
+  }
+}
+
+int head_workgroups(int vocab, int D, int rows_single, int batch, bool have64) {
+  if (batch == 1) return vocab / rows_single;
+  if (head_seq_form(D, batch, have64)) {
+    const int r = head_seq_rows(vocab);
+    return (vocab + r - 1) / r;
+  }
   const int rm = head_rows_multi(D);
-  return batch == 1 ? vocab / rows_single : (vocab + rm - 1) / rm;
+  return (vocab + rm - 1) / rm;
 }
 
 int prepare_head_kernels(int D) {
@@ -810,6 +937,8 @@ int prepare_head_kernels(int D) {
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<9, 2, true>), sh));
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<9, 2, false>), sh));
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<27, 1, false>), sh));
+  if (D % 64 == 0 && D <= 576)
+    BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(head_mx_kernel(D / 64)), head_mx_lds(D)));
   return BFP_OK;
 }
 
@@ -825,9 +954,15 @@ int launch_head(const HeadArgs &a, hipStream_t s) {
     return launch_status("head");
   }
   if (!a.hn) return set_err(BFP_EINVAL, "head: no normed-hidden buffer for batch %d", a.batch);
-  if (a.n_wg != head_workgroups(a.VOCAB, a.D, a.rows_per_wg, a.batch))
+  const bool seqf = head_seq_form(a.D, a.batch, a.embed64 != nullptr);
+  if (a.n_wg != head_workgroups(a.VOCAB, a.D, a.rows_per_wg, a.batch, a.embed64 != nullptr))
     return set_err(BFP_EINVAL, "head: %d workgroups for batch %d", a.n_wg, a.batch);
   hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
+  if (seqf) {
+    hipLaunchKernelGGL(head_mx_kernel(a.D / 64), dim3(a.n_wg, (a.batch + 15) / 16),
+                       dim3(64 * HEAD_MX_WAVES), head_mx_lds(a.D), s, a, head_seq_rows(a.VOCAB));
+    return launch_status("head");
+  }
   const int sg = head_seq_group(a.D);
   const size_t shg = (size_t)sg * a.D * 8;
   if (a.D == 576)

@@ -16,10 +16,13 @@
 // term as Wh.xl' over the first copy plus Wl'.xh over the second, and the
 // weight sums against a constant 64 operand over both copies (= 128 sum).
 // sum x (one value per sequence) comes from the vector unit.  |Phh| <= 2^18
-// and the rest fits in 29 bits, so S is formed exactly in 64 bits.  One
-// more MFMA places E = W_e + x_e straight into the accumulator layout (A
-// holds [W_e, 1], B holds [1, x_e]), so every per-output quantity is in the
-// lane that owns the output: no lane exchange is needed.
+// and the rest fits in 29 bits, so S is formed exactly in 64 bits.  E =
+// W_e + x_e of the lane's four output rows comes from one LDS word (the four
+// rows' weight exponents, tile-major) and one byte, so every per-output
+// quantity is in the lane that owns the output: no lane exchange is needed.
+// (E through one more MFMA per tile and chunk, A = [W_e, 1], B = [1, x_e],
+// made the max-exponent pass a chain of dependent LDS reads and MFMAs: 1.9
+// against 1.0 us for the 576 x 3072 G/U block of 16 sequences.)
 //
 // A block is NC adjacent 16-row chunks of the device layout by 16
 // sequences.  Lane l supplies row / sequence l % 16 and k-group l / 16
@@ -121,12 +124,13 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
   }
   __syncthreads();
   const mx_v4 zero = {0, 0, 0, 0};
-  // E = W_e + x_e of chunk c, tile t in the accumulator layout (k-group 0)
-  auto tile_E = [&](int c, int t) {
-    const int we = wex[t * RW + c * 16 + i], xv = xex[t * 16 + i];
-    const long a = kg == 0 ? (long)((we & 0xff) | (1 << 8)) : 0;
-    const long b = kg == 0 ? (long)(1 | ((xv & 0xff) << 8)) : 0;
-    return mx_mfma(a, b, zero);
+  // E = W_e + x_e of chunk c, tile t for this lane's outputs (rows 4 kg + v,
+  // sequence i): the four rows' exponents are one 4-byte word of wex
+  auto tile_E = [&](int c, int t, int (&E)[4]) {
+    const int ww = *reinterpret_cast<const int *>(wex + t * RW + c * 16 + 4 * kg);
+    const int xv = xex[t * 16 + i];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) E[v] = ((ww << (24 - 8 * v)) >> 24) + xv;
   };
   const int tpw = (nT + nw - 1) / nw;
   const int t0 = w * tpw, t1 = t0 + tpw < nT ? t0 + tpw : nT;
@@ -136,8 +140,10 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
   for (int c = 0; c < NC; ++c) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) M[c][v] = -(1 << 29);
+#pragma unroll 4
     for (int t = t0; t < t1; ++t) {
-      const mx_v4 E = tile_E(c, t);
+      int E[4];
+      tile_E(c, t, E);
 #pragma unroll
       for (int v = 0; v < 4; ++v) M[c][v] = E[v] > M[c][v] ? E[v] : M[c][v];
     }
@@ -184,7 +190,8 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
         mx_v4 cr = mx_mfma(first ? wh : wl, first ? xl : xh, zero);
         cr = mx_mfma(wh, k64, cr);
         ll = mx_mfma(wl, k64, ll);
-        const mx_v4 E = tile_E(c, tb + k);
+        int E[4];
+        tile_E(c, tb + k, E);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int d = M[c][v] - E[v];
