@@ -15,17 +15,16 @@
 
 using namespace bfp;
 
-// The float64 copy of the embedding the batched head reads (every float32
-// is exact in float64), permuted within each row of D = 64 NB columns:
-// v64[row][(4i + c) * 16 + l] = v[row][64i + 4l + c].
-__global__ void widen_embed_kernel(const float *__restrict__ v, long long n, int D,
-                                   double *__restrict__ v64) {
+// The copy of the embedding the batched head reads, permuted within each
+// row of D = 64 NB columns: vp[row][(4i + c) * 16 + l] = v[row][64i + 4l + c].
+__global__ void permute_embed_kernel(const float *__restrict__ v, long long n, int D,
+                                     float *__restrict__ vp) {
   const long long q = blockIdx.x * (long long)blockDim.x + threadIdx.x;   // destination index
   if (q >= n) return;
   const long long row = q / D;
   const int j = (int)(q - row * D);
   const int l = j & 15, c = (j >> 4) & 3, i = j >> 6;
-  v64[q] = (double)v[row * D + 64 * i + 4 * l + c];
+  vp[q] = v[row * D + 64 * i + 4 * l + c];
 }
 
 struct bfp_ctx {
@@ -40,8 +39,8 @@ struct bfp_ctx {
   double *g1 = nullptr, *g2 = nullptr, *norm_w = nullptr, *rope = nullptr;
   double *rope_row = nullptr;   // one (cos, sin) row for a position past the table
   float *embed = nullptr;
-  double *embed64 = nullptr;   // the embedding as float64, permuted per row for the
-                               // batched head (made when max_batch >= HEAD_SEQ_MIN)
+  float *embedp = nullptr;     // the embedding permuted per row for the batched head
+                               // (made when max_batch >= HEAD_SEQ_MIN)
   // activations (max_batch sequences)
   int16_t *h_m = nullptr, *h1_m = nullptr, *qkv_am = nullptr, *att_m = nullptr, *mlp_m = nullptr;
   int8_t *h_e = nullptr, *h1_e = nullptr, *qkv_ae = nullptr, *att_e = nullptr, *mlp_e = nullptr;
@@ -137,7 +136,7 @@ void rope_table(std::vector<double> &t, int max_ctx, int HD) {
 
 // Workgroups of the head for `batch` sequences, and the most any batch uses.
 int head_nwg(const bfp_ctx *c, int batch) {
-  return head_workgroups(c->d.VOCAB, c->d.D, c->head_rows, batch, c->embed64 != nullptr);
+  return head_workgroups(c->d.VOCAB, c->d.D, c->head_rows, batch, c->embedp != nullptr);
 }
 int head_part_max(const bfp_ctx *c) {
   int m = 0;
@@ -148,7 +147,7 @@ int head_part_max(const bfp_ctx *c) {
 HeadArgs head_args(bfp_ctx *c, int batch, double *logits) {
   const bfp_dims &d = c->d;
   HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, head_nwg(c, batch), c->h_m, c->h_e, c->norm_w,
-              c->embed, c->part_v, c->part_i, logits, c->hn, c->embed64};
+              c->embed, c->part_v, c->part_i, logits, c->hn, c->embedp};
   return ha;
 }
 
@@ -378,7 +377,7 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->rope_row, sizeof(double) * d.HD)) ||
       (rc = c->alloc((void **)&c->embed, sizeof(float) * (size_t)d.VOCAB * d.D)) ||
       (max_batch >= HEAD_SEQ_MIN && d.D % 64 == 0 && d.D <= 576 &&
-       (rc = c->alloc((void **)&c->embed64, sizeof(double) * (size_t)d.VOCAB * d.D))) ||
+       (rc = c->alloc((void **)&c->embedp, sizeof(float) * (size_t)d.VOCAB * d.D))) ||
       (rc = c->alloc((void **)&c->h_m, 2 * B * d.D)) || (rc = c->alloc((void **)&c->h_e, B * d.D / 16)) ||
       (rc = c->alloc((void **)&c->h1_m, 2 * B * d.D)) ||
       (rc = c->alloc((void **)&c->h1_e, B * d.D / 16)) ||
@@ -550,11 +549,11 @@ int bfp_load_weights(bfp_ctx *c, int which, int layer, const float *fp32, const 
       if (!fp32) return set_err(BFP_EINVAL, "the embedding must be given as float32");
       HIP_TRY(hipMemcpy(c->embed, fp32, sizeof(float) * (size_t)d.VOCAB * d.D,
                         hipMemcpyHostToDevice));
-      if (c->embed64) {
+      if (c->embedp) {
         const long long n = (long long)d.VOCAB * d.D;
-        hipLaunchKernelGGL(widen_embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                           c->embed, n, d.D, c->embed64);
-        BFP_TRY(launch_status("embed widen"));
+        hipLaunchKernelGGL(permute_embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           s, c->embed, n, d.D, c->embedp);
+        BFP_TRY(launch_status("embed permute"));
         HIP_TRY(hipStreamSynchronize(s));
       }
       return BFP_OK;

@@ -98,23 +98,22 @@ struct HeadArgs {
   double *part_v; int *part_i;             // (batch, n_wg) per-workgroup argmax
   double *logits;                          // optional (batch, VOCAB)
   double *hn;                              // (batch, D) normed hidden, batch > 1 path
-  const double *embed64;                   // (VOCAB, D) float64 embedding, permuted per row:
+  const float *embedp;                     // (VOCAB, D) the embedding permuted per row, or null:
                                            // [row][(4i + c) * 16 + l] = embed[row][64i + 4l + c]
 };
 
 // Batches from HEAD_SEQ_MIN sequences on run the head on the float64 matrix
-// cores (k_head_mx), when the embedding's float64 copy exists and
+// cores (k_head_mx), when the embedding's permuted copy exists and
 // D % 64 == 0, D <= 576.
 constexpr int HEAD_SEQ_MIN = 32;
-inline bool head_seq_form(int D, int batch, bool have64) {
-  return have64 && batch >= HEAD_SEQ_MIN && D % 64 == 0 && D <= 576;
+inline bool head_seq_form(int D, int batch, bool havep) {
+  return havep && batch >= HEAD_SEQ_MIN && D % 64 == 0 && D <= 576;
 }
-// Rows per workgroup of k_head_mx: the vocabulary over about 128 row groups
-// (x 4 groups of 16 sequences at batch 64: two workgroups per CU), in whole
-// 64-row steps of its four waves.
+// Rows per workgroup of k_head_mx: the vocabulary over about 256 row groups
+// (one workgroup of 64 sequences per CU), in whole 16-row tiles.
 inline int head_seq_rows(int vocab) {
-  const int r = (vocab + 127) / 128;
-  return (r + 63) / 64 * 64;
+  const int r = (vocab + 255) / 256;
+  return (r + 15) / 16 * 16;
 }
 
 // Attention form by KV capacity: products per producer wave and AV block

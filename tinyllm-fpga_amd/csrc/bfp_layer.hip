@@ -807,103 +807,125 @@ int launch_embed(const EmbedArgs &a, hipStream_t s) {
 // partial l of a logit -- the FMA chain over k = 64i + 4l + c, i then c
 // ascending, of k_head_logits / k_head_gemv -- is one accumulator fed by
 // NB MFMAs (one per 64-column block i, c on the instruction's k axis).
-// A wave computes a tile of 16 rows x 16 sequences: accumulator l holds
-// partial l of all 256 logits; the 16 partials are then summed in the
-// butterfly order of those kernels (q and q + 8, then 4 apart, 2, 1) inside
-// each lane, so the logits are bit-identical to theirs.
-// Operands: A (lane L: row L % 16, c = L / 16) from the float64 embedding
-// copy permuted at load time so that a lane's 16 values of block i are
-// contiguous (e64p[row][(4i + c) * 16 + l] = embed[row][64i + 4l + c]); B
-// (lane L: c = L / 16, sequence L % 16) from the workgroup's 16 normed
-// hidden vectors in LDS, laid out [i][l][c][sequence].  Output (lane L,
-// element v) is row 4v + L / 16, sequence L % 16.
-// Workgroup: 4 waves, 16 sequences (blockIdx.y), rows [x * rpw, + rpw) in
-// 16-row tiles dealt to the waves in turn; its per-sequence first-index
-// argmax goes to part_v / part_i.
+// Tiles of 16 rows x 16 sequences: accumulator l holds partial l of all 256
+// logits; the 16 partials are then summed in the butterfly order of those
+// kernels (q and q + 8, then 4 apart, 2, 1), so the logits are bit-identical
+// to theirs.
+// Operands: B (lane L: c = L / 16, sequence L % 16) is a group of 16 normed
+// hidden vectors, held in registers for the whole kernel; A (lane L: row
+// L % 16, c = L / 16) comes from the 16-row tile of the embedding in LDS,
+// staged as float32 from a copy permuted at load time so that a lane's 16
+// values of block i are contiguous: ep[row][(4i + c) * 16 + l] =
+// embed[row][64i + 4l + c].  The next tile's loads are issued before a
+// tile's MFMAs and stored to the other LDS buffer after them.  Output (lane
+// L, element v) is row 4v + L / 16, sequence L % 16.
+// Workgroup: 8 waves, 64 sequences (blockIdx.y), rows [x * rpw, + rpw) in
+// 16-row tiles.  Waves 2g and 2g + 1 take sequence group g (16 sequences)
+// and partials 0-7 and 8-15 of it (NB x 8 doubles of B a lane each); the
+// odd wave hands its partials over through LDS and the even one sums the
+// tree and keeps the per-sequence first-index argmax, which goes to
+// part_v / part_i.
 typedef double head_d4 __attribute__((ext_vector_type(4)));
-constexpr int HEAD_MX_WAVES = 4;
-inline int head_mx_lds(int D) { return 16 * D * 8 + HEAD_MX_WAVES * 16 * 4 * 12; }
+constexpr int HEAD_ROW_PAD = 4;   // floats: rows 16 B apart in the LDS banks
+inline int head_mx_lds(int D) { return 2 * 16 * (D + HEAD_ROW_PAD) * 4 + 4 * 8 * 4 * 64 * 8; }
 
 template <int NB>
-__global__ __launch_bounds__(64 * HEAD_MX_WAVES) void k_head_mx(HeadArgs a, int rpw) {
-  extern __shared__ double hsx[];
-  double *hb = hsx;                                       // [i][l][c][16 sequences]
-  double *bvs = hsx + 16 * 64 * NB;                       // [wave][lane / 16 group][sequence]
-  int *bis = reinterpret_cast<int *>(bvs + HEAD_MX_WAVES * 64);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int s0 = blockIdx.y * 16;
-  const int ns = a.batch - s0 < 16 ? a.batch - s0 : 16;
-  // stage the 16 sequences' normed hidden: element (i, l, c, s) = hn[s][64i + 4l + c]
-  for (int q = threadIdx.x; q < 16 * 64 * NB; q += blockDim.x) {
-    const int s = q & 15, c = (q >> 4) & 3, l = (q >> 6) & 15, i = q >> 10;
-    const int sc = s < ns ? s : ns - 1;
-    hb[q] = a.hn[(long long)(s0 + sc) * a.D + 64 * i + 4 * l + c];
+__global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
+  constexpr int D = 64 * NB, RS = D + HEAD_ROW_PAD, F4 = D / 4;   // float4 per row
+  constexpr int TQ = 16 * F4, KQ = (TQ + 511) / 512;               // float4 per tile, per thread
+  extern __shared__ float esm[];          // 2 x 16 rows x RS floats, then the hand-over
+  double *xch = reinterpret_cast<double *>(esm + 2 * 16 * RS);     // [group][l'][v][lane]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = w >> 1, hf = w & 1;
+  const int sl = blockIdx.y * 64 + 16 * g + (lane & 15);
+  const bool live = sl < a.batch;
+  const int sc = live ? sl : a.batch - 1;
+  const int c = lane >> 4;
+  double bq[NB][8];
+  {
+    const double *hp = a.hn + (long long)sc * D + c + 32 * hf;   // partial 8 hf + l
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) bq[i][l] = hp[64 * i + 4 * l];
   }
-  lds_barrier();
   const int row_lo = blockIdx.x * rpw;
   const int row_hi = row_lo + rpw < a.VOCAB ? row_lo + rpw : a.VOCAB;
+  const int ntile = (row_hi - row_lo) / 16;
+  float4 st[KQ];
+  auto load_tile = [&](int t) {
+    const float4 *src = reinterpret_cast<const float4 *>(a.embedp + (long long)(row_lo + 16 * t) * D);
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+      const int q = k * 512 + tid;
+      st[k] = src[q < TQ ? q : TQ - 1];
+    }
+  };
+  auto store_tile = [&](int buf) {
+    float *dst = esm + buf * 16 * RS;
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+      const int q = k * 512 + tid, r = q / F4, j = q - r * F4;
+      if (q < TQ) *reinterpret_cast<float4 *>(dst + r * RS + 4 * j) = st[k];
+    }
+  };
   double bv = -INFINITY;
   int bi = 0x7fffffff;
-  const double *bl = hb + lane;                           // + (16i + l) * 64
-  for (int r0 = row_lo + 16 * w; r0 < row_hi; r0 += 16 * HEAD_MX_WAVES) {
-    const double2 *ap = reinterpret_cast<const double2 *>(
-        a.embed64 + (long long)(r0 + (lane & 15)) * a.D + (lane >> 4) * 16);   // + 64 i doubles
-    head_d4 acc[16];
-#pragma unroll
-    for (int l = 0; l < 16; ++l) acc[l] = head_d4{0.0, 0.0, 0.0, 0.0};
-    double2 av[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) av[k] = ap[k];
-#pragma unroll 1
-    for (int i = 0; i < NB; ++i) {
-      double2 an[8];
-      if (i + 1 < NB) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) an[k] = ap[32 * (i + 1) + k];
-      }
-#pragma unroll
-      for (int l = 0; l < 16; ++l) {
-        const double av_l = (l & 1) ? av[l >> 1].y : av[l >> 1].x;
-        acc[l] = __builtin_amdgcn_mfma_f64_16x16x4f64(av_l, bl[(16 * i + l) * 64], acc[l], 0, 0, 0);
-      }
-      if (i + 1 < NB) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) av[k] = an[k];
-      }
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      double q8[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) q8[q] = acc[q][v] + acc[q + 8][v];
-      const double q4[4] = {q8[0] + q8[4], q8[1] + q8[5], q8[2] + q8[6], q8[3] + q8[7]};
-      const double x = (q4[0] + q4[2]) + (q4[1] + q4[3]);
-      const int row = r0 + 4 * v + (lane >> 4);
-      const int s = lane & 15;
-      if (a.logits && s < ns) a.logits[(long long)(s0 + s) * a.VOCAB + row] = x;
-      if (x > bv || (x == bv && row < bi)) {
-        bv = x;
-        bi = row;
-      }
-    }
+  if (ntile > 0) {
+    load_tile(0);
+    store_tile(0);
   }
-  bvs[w * 64 + lane] = bv;
-  bis[w * 64 + lane] = bi;
   lds_barrier();
-  if (threadIdx.x < 16 && (int)threadIdx.x < ns) {
-    const int s = threadIdx.x;
-    bv = -INFINITY;
-    bi = 0x7fffffff;
-    for (int q = 0; q < 4 * HEAD_MX_WAVES; ++q) {   // (wave, lane group) slots of sequence s
-      const double x = bvs[q * 16 + s];
-      const int i = bis[q * 16 + s];
-      if (x > bv || (x == bv && i < bi)) {
-        bv = x;
-        bi = i;
+  double *xg = xch + g * (8 * 4 * 64) + lane;   // + (l' * 4 + v) * 64
+  for (int t = 0; t < ntile; ++t) {
+    if (t + 1 < ntile) load_tile(t + 1);
+    const float *ar = esm + (t & 1) * 16 * RS + (lane & 15) * RS + 16 * c + 8 * hf;
+    head_d4 acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = head_d4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const float4 f0 = *reinterpret_cast<const float4 *>(ar + 64 * i);
+      const float4 f1 = *reinterpret_cast<const float4 *>(ar + 64 * i + 4);
+      const float e[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+      for (int l = 0; l < 8; ++l)
+        acc[l] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)e[l], bq[i][l], acc[l], 0, 0, 0);
+    }
+    if (hf) {
+#pragma unroll
+      for (int l = 0; l < 8; ++l)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xg[(l * 4 + v) * 64] = acc[l][v];
+    }
+    if (t + 1 < ntile) store_tile((t + 1) & 1);
+    lds_barrier();
+    if (!hf) {
+      const int rbase = row_lo + 16 * t + (lane >> 4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        double q8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) q8[q] = acc[q][v] + xg[(q * 4 + v) * 64];
+        const double q4[4] = {q8[0] + q8[4], q8[1] + q8[5], q8[2] + q8[6], q8[3] + q8[7]};
+        const double x = (q4[0] + q4[2]) + (q4[1] + q4[3]);
+        const int row = rbase + 4 * v;
+        if (a.logits && live) a.logits[(long long)sl * a.VOCAB + row] = x;
+        if (x > bv || (x == bv && row < bi)) {
+          bv = x;
+          bi = row;
+        }
       }
     }
-    a.part_v[(long long)(s0 + s) * a.n_wg + blockIdx.x] = bv;
-    a.part_i[(long long)(s0 + s) * a.n_wg + blockIdx.x] = bi;
+    lds_barrier();   // the hand-over is read before the odd wave writes the next tile's
+  }
+  if (!hf) {
+    argmax_step<16>(bv, bi);   // the four lanes of a sequence (lane / 16)
+    argmax_step<32>(bv, bi);
+    if (lane < 16 && live) {
+      a.part_v[(long long)sl * a.n_wg + blockIdx.x] = bv;
+      a.part_i[(long long)sl * a.n_wg + blockIdx.x] = bi;
+    }
   }
 }
 
@@ -954,13 +976,13 @@ int launch_head(const HeadArgs &a, hipStream_t s) {
     return launch_status("head");
   }
   if (!a.hn) return set_err(BFP_EINVAL, "head: no normed-hidden buffer for batch %d", a.batch);
-  const bool seqf = head_seq_form(a.D, a.batch, a.embed64 != nullptr);
-  if (a.n_wg != head_workgroups(a.VOCAB, a.D, a.rows_per_wg, a.batch, a.embed64 != nullptr))
+  const bool seqf = head_seq_form(a.D, a.batch, a.embedp != nullptr);
+  if (a.n_wg != head_workgroups(a.VOCAB, a.D, a.rows_per_wg, a.batch, a.embedp != nullptr))
     return set_err(BFP_EINVAL, "head: %d workgroups for batch %d", a.n_wg, a.batch);
   hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
   if (seqf) {
-    hipLaunchKernelGGL(head_mx_kernel(a.D / 64), dim3(a.n_wg, (a.batch + 15) / 16),
-                       dim3(64 * HEAD_MX_WAVES), head_mx_lds(a.D), s, a, head_seq_rows(a.VOCAB));
+    hipLaunchKernelGGL(head_mx_kernel(a.D / 64), dim3(a.n_wg, (a.batch + 63) / 64), dim3(512),
+                       head_mx_lds(a.D), s, a, head_seq_rows(a.VOCAB));
     return launch_status("head");
   }
   const int sg = head_seq_group(a.D);
