@@ -184,6 +184,48 @@ __global__ __launch_bounds__(256) void k_norm_seq(LayerArgs a, int which) {
   }
 }
 
+// The same with thread t on elements 2t, 2t + 1 (rmsnorm_pairs; blockDim
+// >= D / 2): one division pair and one tile quantisation per thread, the
+// squares' pairwise sum over LDS.  dsm: D + PW_MAX_LEAVES doubles.
+__global__ __launch_bounds__(512) void k_norm_pairs(LayerArgs a, int which) {
+  extern __shared__ double dsm[];
+  const int b = blockIdx.x, nT = a.D / 16;
+  const int16_t *hm = (which == 1 ? a.h_m : a.h1_m) + (long long)b * a.D;
+  const int8_t *he = (which == 1 ? a.h_e : a.h1_e) + (long long)b * nT;
+  const double *g = which == 1 ? a.g1 : a.g2;
+  const int i0 = 2 * (int)threadIdx.x;
+  const bool on = i0 < a.D;
+  const double2 gg = *reinterpret_cast<const double2 *>(g + (on ? i0 : 0));
+  int m0, m1, e;
+  rmsnorm_pairs(hm, he, gg.x, gg.y, a.D, dsm, dsm + a.D, m0, m1, e);
+  if (on) {
+    int16_t *om = a.xn_m + (long long)b * a.D;
+    int8_t *oe = a.xn_e + (long long)b * nT;
+    *reinterpret_cast<int *>(om + i0) = (m0 & 0xffff) | (m1 << 16);
+    if ((i0 & 15) == 0) oe[i0 >> 4] = (int8_t)e;
+    if (a.dump) {
+      const int st = which == 1 ? ST_N1 : ST_N2;
+      const StageDump *d = a.dump;
+      d->m[st][b * d->mstride[st] + i0] = (int16_t)m0;
+      d->m[st][b * d->mstride[st] + i0 + 1] = (int16_t)m1;
+      if ((i0 & 15) == 0) d->e[st][b * (d->mstride[st] / 16) + (i0 >> 4)] = (int8_t)e;
+    }
+  }
+}
+
+// The RMSNorm launch of the multi-sequence paths: the pair form up to
+// D = 1024, else one thread per 4 elements (k_norm_seq).
+static void launch_norm_seq(const LayerArgs &a, int which, hipStream_t s) {
+  if (a.D <= 1024) {
+    const int nt = (a.D / 2 + 63) / 64 * 64;
+    hipLaunchKernelGGL(k_norm_pairs, dim3(a.batch), dim3(nt), (size_t)(a.D + PW_MAX_LEAVES) * 8, s,
+                       a, which);
+  } else {
+    const size_t sh = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8 + (size_t)(a.D / 16) * 17 * 4;
+    hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh, s, a, which);
+  }
+}
+
 constexpr int MSEQ = 8;   // sequences per workgroup of the multi-sequence matvecs
 
 // The epilogue of a multi-sequence chunk: wave 0, four sequences per pass
@@ -731,16 +773,15 @@ static int mx_waves(int nT, int n_blocks) {
 
 static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
   const int nTD = a.D / 16, nTF = a.FFN / 16;
-  const size_t sh_norm = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
   const int G = (a.batch + MX_SEQ - 1) / MX_SEQ;
   const int bq = (a.D + 2 * a.KV) / 32, bo = a.D / 16, bg = a.FFN / 16;
-  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 1);
+  launch_norm_seq(a, 1, s);
   hipLaunchKernelGGL(k_qkv_mx, dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
                      mx_lds_bytes(2, nTD), s, a);
   BFP_TRY(launch_attn(a, s));
   hipLaunchKernelGGL(k_o_res_mx, dim3(bo, G), dim3(64 * mx_waves(nTD, bo * G)),
                      mx_lds_bytes(1, nTD), s, a);
-  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 2);
+  launch_norm_seq(a, 2, s);
   hipLaunchKernelGGL(k_gu_mx, dim3(bg, G), dim3(64 * mx_waves(nTD, bg * G)),
                      mx_lds_bytes(2, nTD), s, a);
   hipLaunchKernelGGL(k_d_res_mx, dim3(bo, G), dim3(64 * mx_waves(nTF, bo * G)),
@@ -758,14 +799,13 @@ static int launch_layer_multi(const LayerArgs &a, hipStream_t s) {
   lkm_fn fd = pick_dres_m(nwf, tptf);
   if (!fq || !fo || !fg || !fd) return set_err(BFP_EINVAL, "no layer kernel for D=%d FFN=%d", a.D, a.FFN);
   const int nq = a.D + 2 * a.KV;
-  const size_t sh_norm = (size_t)(3 * a.D + PW_MAX_LEAVES) * 8 + (size_t)nTD * 17 * 4;
   const int G = (a.batch + MSEQ - 1) / MSEQ;
   const size_t shD = (size_t)MSEQ * nTD * 17 * 4, shF = (size_t)MSEQ * nTF * 17 * 4;
-  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 1);
+  launch_norm_seq(a, 1, s);
   hipLaunchKernelGGL(fq, dim3(nq / 16, G), dim3(64 * nw), shD, s, a);
   BFP_TRY(launch_attn(a, s));
   hipLaunchKernelGGL(fo, dim3(a.D / 16, G), dim3(64 * nw), shD, s, a);
-  hipLaunchKernelGGL(k_norm_seq, dim3(a.batch), dim3(256), sh_norm, s, a, 2);
+  launch_norm_seq(a, 2, s);
   hipLaunchKernelGGL(fg, dim3(a.FFN / 16, G), dim3(64 * nw), shD, s, a);
   hipLaunchKernelGGL(fd, dim3(a.D / 16, G), dim3(64 * nwf), shF, s, a);
   return launch_status("layer");

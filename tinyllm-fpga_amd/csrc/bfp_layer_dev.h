@@ -98,9 +98,11 @@ __device__ __forceinline__ void rmsnorm_to_x_g(const int16_t *__restrict__ hm, c
 // instruction stream, a tile's 16 elements sit in one 8-lane group, and the
 // pair goes into the matvec's input form as it is.  hm/he and the squares
 // (sq, D doubles) are LDS; g0/g1: this thread's gammas.  All threads call.
-__device__ __forceinline__ void rmsnorm_pairs_to_x(const int16_t *__restrict__ hm,
-                                                   const int8_t *__restrict__ he, double g0, double g1,
-                                                   int D, int *xs, int *xes, double *sq, double *leaf) {
+// Core of it: returns this thread's quantised pair (m0, m1) and its tile's
+// exponent e (every thread; meaningful where 2 * tid < D).
+__device__ __forceinline__ void rmsnorm_pairs(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
+                                              double g0, double g1, int D, double *sq, double *leaf,
+                                              int &m0, int &m1, int &e) {
   const int i0 = 2 * (int)threadIdx.x;
   const bool on = i0 < D;
   const int j = on ? i0 : 0;
@@ -115,8 +117,16 @@ __device__ __forceinline__ void rmsnorm_pairs_to_x(const int16_t *__restrict__ h
   const double rt = sqrt(s / (double)D + 1e-5);
   const double y0 = on ? (x0 * g0) / rt : 0.0;
   const double y1 = on ? (x1 * g1) / rt : 0.0;
-  int m0, m1, e;
   quantize16_pairs(y0, y1, m0, m1, e, true);   // tile_quantize(rmsnorm_fp(.)): canonical
+}
+
+__device__ __forceinline__ void rmsnorm_pairs_to_x(const int16_t *__restrict__ hm,
+                                                   const int8_t *__restrict__ he, double g0, double g1,
+                                                   int D, int *xs, int *xes, double *sq, double *leaf) {
+  const int i0 = 2 * (int)threadIdx.x;
+  const bool on = i0 < D;
+  int m0, m1, e;
+  rmsnorm_pairs(hm, he, g0, g1, D, sq, leaf, m0, m1, e);
   if (on) {
     put_x_pair(xs, i0 >> 4, (i0 >> 1) & 7, m0, m1);
     if ((i0 & 15) == 0) xes[i0 >> 4] = e;
