@@ -62,3 +62,70 @@ def test_block_scheme_equals_numpy():
         a = [float(v) for v in a]
         want = float(np.add.reduce(np.array(a)))
         assert _block_scheme(a) == want, n
+
+
+def _equal_leaves(n):
+    """(nl, L) when numpy's splits of n give nl <= 8 equal leaves of L
+    elements, L % 8 == 0 (csrc/bfp_f64.h pw_equal_leaves), else None."""
+    nl, L = 1, n
+    while L > 128:
+        n2 = L // 2
+        n2 -= n2 % 8
+        if 2 * n2 != L:
+            return None
+        L, nl = n2, nl * 2
+    return (nl, L) if nl <= 8 and L % 8 == 0 and L >= 8 else None
+
+
+def _wave_scheme(a, nl, L):
+    """csrc/bfp_f64.h sum_sq_wave on 64 lanes: lane 8f + j runs accumulator
+    j of leaf f; quad swaps i^1, i^2, the 8-lane half-mirror (i <-> 7-i),
+    then the 16-lane mirror (i <-> 15-i) and the 16- and 32-lane swaps;
+    lane 0's value, plus numpy's initial 0.0."""
+    lanes = []
+    for lane in range(64):
+        f, j = lane >> 3, lane & 7
+        base = (f if f < nl else 0) * L + j
+        r = a[base]
+        for k in range(1, L // 8):
+            r = r + a[base + 8 * k]
+        lanes.append(r)
+
+    def step(partner):
+        return [lanes[i] + lanes[partner(i)] for i in range(64)]
+    lanes = step(lambda i: i ^ 1)
+    lanes = step(lambda i: i ^ 2)
+    lanes = step(lambda i: (i & ~7) | (7 - (i & 7)))
+    if nl >= 2:
+        lanes = step(lambda i: (i & ~15) | (15 - (i & 15)))
+    if nl >= 4:
+        lanes = step(lambda i: i ^ 16)
+    if nl >= 8:
+        lanes = step(lambda i: i ^ 32)
+    return 0.0 + lanes[0]
+
+
+def test_wave_scheme_equals_numpy():
+    """Every D % 64 == 0 up to 1024 has numpy leaves of the wave form, and the
+    wave's accumulators and butterfly give np.add.reduce's bits; 1536 (FFN)
+    does not (it keeps the block-wide sum).  Squares of BFP values like the
+    RMSNorm's, plus wide-range and cancelling inputs."""
+    rng = np.random.default_rng(11)
+    for D in range(64, 1025, 64):
+        nl_L = _equal_leaves(D)
+        assert nl_L is not None, D
+        nl, L = nl_L
+        assert nl * L == D
+        for trial in range(20):
+            if trial % 3 == 0:
+                x = rng.integers(-32768, 32768, D) * 2.0 ** rng.integers(-40, 10, D // 16).repeat(16)
+                a = x * x
+            elif trial % 3 == 1:
+                a = rng.standard_normal(D) * 10.0 ** rng.integers(-8, 8, D)
+            else:
+                a = rng.standard_normal(D)
+            want = np.add.reduce(a)
+            got = _wave_scheme(a, nl, L)
+            assert np.float64(got).view(np.int64) == np.float64(want).view(np.int64), (D, trial)
+    assert _equal_leaves(576) == (8, 72)
+    assert _equal_leaves(1536) is None

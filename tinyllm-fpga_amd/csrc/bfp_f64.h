@@ -292,6 +292,77 @@ __device__ __forceinline__ double group8_max(double v) {
   return fmax(v, dpp(v, 0x4E));
 }
 
+// numpy's pairwise sum of the squares of D BFP values (hm, he) by one wave
+// alone, when numpy's splits give nl <= 8 equal leaves of L <= 128 elements
+// with L % 8 == 0 (every D % 64 == 0 up to 1024: 576 = 8 x 72): lane 8f + j
+// runs accumulator r_j of leaf f (elements fL + j, fL + j + 8, ... in
+// order); the leaf's ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) comes from quad
+// swaps i ^ 1, i ^ 2 and the 8-lane half-mirror (after the swaps a quad's
+// lanes hold one value, so the mirror partner is the other quad), the
+// leaves' ((L0+L1)+(L2+L3))+... from the 16-lane mirror and the 16- and
+// 32-lane swaps.  Every lane returns 0.0 + the sum (numpy's initial 0.0).
+__device__ __forceinline__ double dpp_f64(double x, int ctrl) {
+  const long long b = __double_as_longlong(x);
+  int lo = (int)(b & 0xffffffffLL), hi = (int)(b >> 32);
+  switch (ctrl) {
+    case 0xB1:
+      lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xf, 0xf, false);
+      hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xf, 0xf, false);
+      break;
+    case 0x4E:
+      lo = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xf, 0xf, false);
+      hi = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xf, 0xf, false);
+      break;
+    case 0x141:
+      lo = __builtin_amdgcn_mov_dpp(lo, 0x141, 0xf, 0xf, false);
+      hi = __builtin_amdgcn_mov_dpp(hi, 0x141, 0xf, 0xf, false);
+      break;
+    default:   // 0x140 row_mirror
+      lo = __builtin_amdgcn_mov_dpp(lo, 0x140, 0xf, 0xf, false);
+      hi = __builtin_amdgcn_mov_dpp(hi, 0x140, 0xf, 0xf, false);
+      break;
+  }
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+__device__ __forceinline__ double sum_sq_wave(const int16_t *hm, const int8_t *he, int nl, int L) {
+  const int lane = threadIdx.x & 63;
+  const int f = lane >> 3, j = lane & 7;
+  const int base = (f < nl ? f : 0) * L + j;
+  double r = 0.0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if (8 * k < L) {
+      const int i = base + 8 * k;
+      const double x = bfp_val(hm[i], he[i >> 4]);
+      r = k == 0 ? x * x : r + x * x;
+    }
+  }
+  r = r + dpp_f64(r, 0xB1);
+  r = r + dpp_f64(r, 0x4E);
+  r = r + dpp_f64(r, 0x141);
+  if (nl >= 2) r = r + dpp_f64(r, 0x140);
+  if (nl >= 4) r = r + peer<16>(r);
+  if (nl >= 8) r = r + peer<32>(r);
+  const long long b = __double_as_longlong(r);
+  const int lo32 = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), 0);
+  const int hi32 = __builtin_amdgcn_readlane((int)(b >> 32), 0);
+  return 0.0 + __longlong_as_double((long long)(((unsigned long long)(unsigned)hi32 << 32) | (unsigned)lo32));
+}
+// The leaves of numpy's pairwise sum over n elements when they are nl <= 8
+// equal leaves of L elements, L % 8 == 0 (sum_sq_wave's form); false if not.
+__host__ __device__ inline bool pw_equal_leaves(int n, int &nl, int &L) {
+  nl = 1;
+  L = n;
+  while (L > 128) {
+    int n2 = L / 2;
+    n2 -= n2 % 8;
+    if (2 * n2 != L) return false;
+    L = n2;
+    nl *= 2;
+  }
+  return nl <= 8 && L % 8 == 0 && L >= 8;
+}
+
 // tile_quantize of the 16 values held two per lane by an 8-lane group
 // (elements 2j and 2j+1 in lane j of the group): the tile exponent in e and
 // this lane's two mantissas, canonical when `canonical` (the same values as

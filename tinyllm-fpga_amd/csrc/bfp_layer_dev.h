@@ -96,8 +96,11 @@ __device__ __forceinline__ void rmsnorm_to_x_g(const int16_t *__restrict__ hm, c
 // The same RMSNorm with thread t on the adjacent elements 2t and 2t+1
 // (D <= 2*blockDim): its two divisions and quantisations are one
 // instruction stream, a tile's 16 elements sit in one 8-lane group, and the
-// pair goes into the matvec's input form as it is.  hm/he and the squares
-// (sq, D doubles) are LDS; g0/g1: this thread's gammas.  All threads call.
+// pair goes into the matvec's input form as it is.  The squares' pairwise
+// sum: where numpy's leaves are at most 8 equal ones (every D % 64 == 0 up
+// to 1024) each wave forms it alone from hm/he (sum_sq_wave: no barrier, no
+// leaf buffer), else through sq (D doubles of LDS) and the block-wide sum.
+// g0/g1: this thread's gammas.  All threads call.
 // Core of it: returns this thread's quantised pair (m0, m1) and its tile's
 // exponent e (every thread; meaningful where 2 * tid < D).
 __device__ __forceinline__ void rmsnorm_pairs(const int16_t *__restrict__ hm, const int8_t *__restrict__ he,
@@ -108,12 +111,18 @@ __device__ __forceinline__ void rmsnorm_pairs(const int16_t *__restrict__ hm, co
   const int j = on ? i0 : 0;
   const int e_in = he[j >> 4];
   const double x0 = bfp_val(hm[j], e_in), x1 = bfp_val(hm[j + 1], e_in);
-  if (on) {
-    sq[i0] = x0 * x0;
-    sq[i0 + 1] = x1 * x1;
+  int nl, L;
+  double s;
+  if (pw_equal_leaves(D, nl, L)) {   // uniform: every wave forms the sum itself
+    s = sum_sq_wave(hm, he, nl, L);
+  } else {
+    if (on) {
+      sq[i0] = x0 * x0;
+      sq[i0 + 1] = x1 * x1;
+    }
+    lds_barrier();
+    s = pairwise_sum_block(sq, D, leaf);
   }
-  lds_barrier();
-  const double s = pairwise_sum_block(sq, D, leaf);
   const double rt = sqrt(s / (double)D + 1e-5);
   const double y0 = on ? (x0 * g0) / rt : 0.0;
   const double y1 = on ? (x1 * g1) / rt : 0.0;
