@@ -630,24 +630,73 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   }
   lds_barrier();
   // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
-  double mx = -INFINITY;
-  for (int t = tid; t < n; t += NT) mx = fmax(mx, sc[t]);
-  mx = fmax(mx, peer<32>(mx));
-  mx = fmax(mx, peer<16>(mx));
-  mx = fmax(mx, peer<8>(mx));
-  mx = fmax(mx, peer<4>(mx));
-  mx = fmax(mx, peer<2>(mx));
-  mx = fmax(mx, peer<1>(mx));
-  if (l == 0) red[w] = mx;
-  lds_barrier();
-  mx = red[0];
+  if (SHORT && n <= 128) {
+    // wave 0 alone (only it reads p in the short forms' AV chain): lane l
+    // holds positions l and l + 64; numpy's sum of n <= 128 is one block --
+    // n < 8 added in order from 0.0, else accumulators r_j (lanes 0-7,
+    // positions j, j + 8, ... in order) combined
+    // ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the last n % 8 in order --
+    // plus the reduction's initial 0.0.  No barrier: the wave reads back
+    // only its own LDS writes.
+    if (w == 0) {
+      const double s0 = l < n ? sc[l] : -INFINITY, s1 = l + 64 < n ? sc[l + 64] : -INFINITY;
+      double mx = fmax(s0, s1);
+      mx = fmax(mx, peer<32>(mx));
+      mx = fmax(mx, peer<16>(mx));
+      mx = fmax(mx, peer<8>(mx));
+      mx = fmax(mx, peer<4>(mx));
+      mx = fmax(mx, peer<2>(mx));
+      mx = fmax(mx, peer<1>(mx));
+      const double e0 = exp_f64(s0 - mx), e1 = exp_f64(s1 - mx);
+      if (l < n) sc[l] = e0;
+      if (l + 64 < n) sc[l + 64] = e1;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      double res;
+      if (n < 8) {
+        res = 0.0;
+        for (int t = 0; t < n; ++t) res += sc[t];
+      } else {
+        const int top = n - n % 8, j = l & 7;
+        double r = sc[j];
+        for (int t = 8 + j; t < top; t += 8) r = r + sc[t];
+        r = r + dpp_f64(r, 0xB1);
+        r = r + dpp_f64(r, 0x4E);
+        r = r + dpp_f64(r, 0x141);
+        const long long rb = __double_as_longlong(r);
+        res = __longlong_as_double(
+            (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(rb >> 32), 0) << 32) |
+                        (unsigned)__builtin_amdgcn_readlane((int)(rb & 0xffffffffLL), 0)));
+        for (int t = top; t < n; ++t) res += sc[t];
+      }
+      const double sum = 0.0 + res;
+      if (l < n) sc[l] = e0 / sum;
+      if (l + 64 < n) sc[l + 64] = e1 / sum;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    }
+  } else {
+    double mx = -INFINITY;
+    for (int t = tid; t < n; t += NT) mx = fmax(mx, sc[t]);
+    mx = fmax(mx, peer<32>(mx));
+    mx = fmax(mx, peer<16>(mx));
+    mx = fmax(mx, peer<8>(mx));
+    mx = fmax(mx, peer<4>(mx));
+    mx = fmax(mx, peer<2>(mx));
+    mx = fmax(mx, peer<1>(mx));
+    if (l == 0) red[w] = mx;
+    lds_barrier();
+    mx = red[0];
 #pragma unroll
-  for (int i = 1; i < ATT_WAVES; ++i) mx = fmax(mx, red[i]);
-  for (int t = tid; t < n; t += NT) sc[t] = exp_f64(sc[t] - mx);
-  lds_barrier();
-  const double sum = pairwise_sum_block(sc, n, leaf);
-  for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
-  lds_barrier();
+    for (int i = 1; i < ATT_WAVES; ++i) mx = fmax(mx, red[i]);
+    for (int t = tid; t < n; t += NT) sc[t] = exp_f64(sc[t] - mx);
+    lds_barrier();
+    const double sum = pairwise_sum_block(sc, n, leaf);
+    for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
+    lds_barrier();
+  }
 
   double acc = 0.0;
   if constexpr (SHORT) {
