@@ -16,15 +16,17 @@
 using namespace bfp;
 
 // The copy of the embedding the batched head reads, permuted within each
-// row of D = 64 NB columns: vp[row][(4i + c) * 16 + l] = v[row][64i + 4l + c].
+// row of D = 64 NB columns: vp[row][(4i + c) * 16 + 4h + j] =
+// v[row][64i + 4(h + 4j) + c] (partials h, h + 4, h + 8, h + 12 of block i,
+// k-index c, contiguous).
 __global__ void permute_embed_kernel(const float *__restrict__ v, long long n, int D,
                                      float *__restrict__ vp) {
   const long long q = blockIdx.x * (long long)blockDim.x + threadIdx.x;   // destination index
   if (q >= n) return;
   const long long row = q / D;
-  const int j = (int)(q - row * D);
-  const int l = j & 15, c = (j >> 4) & 3, i = j >> 6;
-  vp[q] = v[row * D + 64 * i + 4 * l + c];
+  const int jj = (int)(q - row * D);
+  const int j = jj & 3, h = (jj >> 2) & 3, c = (jj >> 4) & 3, i = jj >> 6;
+  vp[q] = v[row * D + 64 * i + 4 * (h + 4 * j) + c];
 }
 
 struct bfp_ctx {

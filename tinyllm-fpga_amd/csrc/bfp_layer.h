@@ -99,7 +99,7 @@ struct HeadArgs {
   double *logits;                          // optional (batch, VOCAB)
   double *hn;                              // (batch, D) normed hidden, batch > 1 path
   const float *embedp;                     // (VOCAB, D) the embedding permuted per row, or null:
-                                           // [row][(4i + c) * 16 + l] = embed[row][64i + 4l + c]
+                                           // [row][(4i + c) * 16 + 4h + j] = embed[row][64i + 4(h + 4j) + c]
 };
 
 // Batches from HEAD_SEQ_MIN sequences on run the head on the float64 matrix
@@ -109,10 +109,11 @@ constexpr int HEAD_SEQ_MIN = 32;
 inline bool head_seq_form(int D, int batch, bool havep) {
   return havep && batch >= HEAD_SEQ_MIN && D % 64 == 0 && D <= 576;
 }
-// Rows per workgroup of k_head_mx: the vocabulary over about 256 row groups
-// (one workgroup of 64 sequences per CU), in whole 16-row tiles.
+// Rows per workgroup of k_head_mx: the vocabulary over about 128 row groups
+// (x 2 workgroups of 32 sequences at batch 64: one per CU), in whole 16-row
+// tiles.
 inline int head_seq_rows(int vocab) {
-  const int r = (vocab + 255) / 256;
+  const int r = (vocab + 127) / 128;
   return (r + 15) / 16 * 16;
 }
 

@@ -854,60 +854,73 @@ int launch_embed(const EmbedArgs &a, hipStream_t s) {
 // Operands: B (lane L: c = L / 16, sequence L % 16) is a group of 16 normed
 // hidden vectors, held in registers for the whole kernel; A (lane L: row
 // L % 16, c = L / 16) comes from the 16-row tile of the embedding in LDS,
-// staged as float32 from a copy permuted at load time so that a lane's 16
-// values of block i are contiguous: ep[row][(4i + c) * 16 + l] =
-// embed[row][64i + 4l + c].  The next tile's loads are issued before a
-// tile's MFMAs and stored to the other LDS buffer after them.  Output (lane
-// L, element v) is row 4v + L / 16, sequence L % 16.
-// Workgroup: 8 waves, 64 sequences (blockIdx.y), rows [x * rpw, + rpw) in
-// 16-row tiles.  Waves 2g and 2g + 1 take sequence group g (16 sequences)
-// and partials 0-7 and 8-15 of it (NB x 8 doubles of B a lane each); the
-// odd wave hands its partials over through LDS and the even one sums the
-// tree and keeps the per-sequence first-index argmax, which goes to
-// part_v / part_i.
+// staged as float32 from a copy permuted at load time (ep, below).  The
+// next tile's loads are issued before a tile's MFMAs and stored to the
+// other LDS buffer after them.  Output (lane L, element v) is row
+// 4v + L / 16, sequence L % 16.
+// Workgroup: 8 waves, 32 sequences (blockIdx.y), rows [x * rpw, + rpw) in
+// 16-row tiles.  Waves 4g .. 4g + 3 take sequence group g (16 sequences);
+// wave h of them holds partials h, h + 4, h + 8, h + 12 (NB x 4 doubles of B
+// a lane), so the butterfly's first two levels stay in the wave: a_h =
+// p_h + p_(h+8), a_(h+4) = p_(h+4) + p_(h+12), b_h = a_h + a_(h+4).  Waves
+// h = 1..3 hand b_h over through LDS and wave h = 0 forms (b0 + b2) +
+// (b1 + b3) and keeps the per-sequence first-index argmax, which goes to
+// part_v / part_i.  ep holds a wave's four partials contiguously:
+// ep[row][(4i + c) * 16 + 4h + j] = embed[row][64i + 4(h + 4j) + c].
 typedef double head_d4 __attribute__((ext_vector_type(4)));
 constexpr int HEAD_ROW_PAD = 4;   // floats: rows 16 B apart in the LDS banks
-inline int head_mx_lds(int D) { return 2 * 16 * (D + HEAD_ROW_PAD) * 4 + 4 * 8 * 4 * 64 * 8; }
+inline int head_mx_lds(int D) { return 2 * 16 * (D + HEAD_ROW_PAD) * 4 + 2 * 3 * 4 * 64 * 8; }
 
 template <int NB>
 __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
   constexpr int D = 64 * NB, RS = D + HEAD_ROW_PAD, F4 = D / 4;   // float4 per row
   constexpr int TQ = 16 * F4, KQ = (TQ + 511) / 512;               // float4 per tile, per thread
   extern __shared__ float esm[];          // 2 x 16 rows x RS floats, then the hand-over
-  double *xch = reinterpret_cast<double *>(esm + 2 * 16 * RS);     // [group][l'][v][lane]
+  double *xch = reinterpret_cast<double *>(esm + 2 * 16 * RS);     // [group][h - 1][v][lane]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = w >> 1, hf = w & 1;
-  const int sl = blockIdx.y * 64 + 16 * g + (lane & 15);
+  const int g = w >> 2, h = w & 3;
+  const int sl = blockIdx.y * 32 + 16 * g + (lane & 15);
   const bool live = sl < a.batch;
   const int sc = live ? sl : a.batch - 1;
   const int c = lane >> 4;
-  double bq[NB][8];
+  double bq[NB][4];
   {
-    const double *hp = a.hn + (long long)sc * D + c + 32 * hf;   // partial 8 hf + l
+    const double *hp = a.hn + (long long)sc * D + c + 4 * h;   // partial h + 4j
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int l = 0; l < 8; ++l) bq[i][l] = hp[64 * i + 4 * l];
+      for (int j = 0; j < 4; ++j) bq[i][j] = hp[64 * i + 16 * j];
   }
   const int row_lo = blockIdx.x * rpw;
   const int row_hi = row_lo + rpw < a.VOCAB ? row_lo + rpw : a.VOCAB;
   const int ntile = (row_hi - row_lo) / 16;
-  float4 st[KQ];
+  // staging registers by name (an array of them, indexed in the lambdas,
+  // stayed in scratch memory)
+  static_assert(KQ <= 5, "at most 5 staging registers");
+  float4 st0, st1, st2, st3, st4;
   auto load_tile = [&](int t) {
     const float4 *src = reinterpret_cast<const float4 *>(a.embedp + (long long)(row_lo + 16 * t) * D);
-#pragma unroll
-    for (int k = 0; k < KQ; ++k) {
+    auto ld = [&](int k) {
       const int q = k * 512 + tid;
-      st[k] = src[q < TQ ? q : TQ - 1];
-    }
+      return src[q < TQ ? q : TQ - 1];
+    };
+    st0 = ld(0);
+    if constexpr (KQ > 1) st1 = ld(1);
+    if constexpr (KQ > 2) st2 = ld(2);
+    if constexpr (KQ > 3) st3 = ld(3);
+    if constexpr (KQ > 4) st4 = ld(4);
   };
   auto store_tile = [&](int buf) {
     float *dst = esm + buf * 16 * RS;
-#pragma unroll
-    for (int k = 0; k < KQ; ++k) {
+    auto stq = [&](int k, float4 v) {
       const int q = k * 512 + tid, r = q / F4, j = q - r * F4;
-      if (q < TQ) *reinterpret_cast<float4 *>(dst + r * RS + 4 * j) = st[k];
-    }
+      if (q < TQ) *reinterpret_cast<float4 *>(dst + r * RS + 4 * j) = v;
+    };
+    stq(0, st0);
+    if constexpr (KQ > 1) stq(1, st1);
+    if constexpr (KQ > 2) stq(2, st2);
+    if constexpr (KQ > 3) stq(3, st3);
+    if constexpr (KQ > 4) stq(4, st4);
   };
   double bv = -INFINITY;
   int bi = 0x7fffffff;
@@ -916,39 +929,35 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
     store_tile(0);
   }
   lds_barrier();
-  double *xg = xch + g * (8 * 4 * 64) + lane;   // + (l' * 4 + v) * 64
+  double *xg = xch + g * (3 * 4 * 64) + lane;   // + ((h - 1) * 4 + v) * 64
   for (int t = 0; t < ntile; ++t) {
     if (t + 1 < ntile) load_tile(t + 1);
-    const float *ar = esm + (t & 1) * 16 * RS + (lane & 15) * RS + 16 * c + 8 * hf;
-    head_d4 acc[8];
+    const float *ar = esm + (t & 1) * 16 * RS + (lane & 15) * RS + 16 * c + 4 * h;
+    head_d4 acc[4];
 #pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = head_d4{0.0, 0.0, 0.0, 0.0};
+    for (int j = 0; j < 4; ++j) acc[j] = head_d4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const float4 f0 = *reinterpret_cast<const float4 *>(ar + 64 * i);
-      const float4 f1 = *reinterpret_cast<const float4 *>(ar + 64 * i + 4);
-      const float e[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-#pragma unroll
-      for (int l = 0; l < 8; ++l)
-        acc[l] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)e[l], bq[i][l], acc[l], 0, 0, 0);
+      const float4 f = *reinterpret_cast<const float4 *>(ar + 64 * i);
+      acc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)f.x, bq[i][0], acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)f.y, bq[i][1], acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)f.z, bq[i][2], acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)f.w, bq[i][3], acc[3], 0, 0, 0);
     }
-    if (hf) {
+    double b4[4];
 #pragma unroll
-      for (int l = 0; l < 8; ++l)
+    for (int v = 0; v < 4; ++v) b4[v] = (acc[0][v] + acc[2][v]) + (acc[1][v] + acc[3][v]);
+    if (h) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) xg[(l * 4 + v) * 64] = acc[l][v];
+      for (int v = 0; v < 4; ++v) xg[((h - 1) * 4 + v) * 64] = b4[v];
     }
     if (t + 1 < ntile) store_tile((t + 1) & 1);
     lds_barrier();
-    if (!hf) {
+    if (!h) {
       const int rbase = row_lo + 16 * t + (lane >> 4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        double q8[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) q8[q] = acc[q][v] + xg[(q * 4 + v) * 64];
-        const double q4[4] = {q8[0] + q8[4], q8[1] + q8[5], q8[2] + q8[6], q8[3] + q8[7]};
-        const double x = (q4[0] + q4[2]) + (q4[1] + q4[3]);
+        const double x = (b4[v] + xg[(4 + v) * 64]) + (xg[v * 64] + xg[(8 + v) * 64]);
         const int row = rbase + 4 * v;
         if (a.logits && live) a.logits[(long long)sl * a.VOCAB + row] = x;
         if (x > bv || (x == bv && row < bi)) {
@@ -957,9 +966,9 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
         }
       }
     }
-    lds_barrier();   // the hand-over is read before the odd wave writes the next tile's
+    lds_barrier();   // the hand-over is read before it is written for the next tile
   }
-  if (!hf) {
+  if (!h) {
     argmax_step<16>(bv, bi);   // the four lanes of a sequence (lane / 16)
     argmax_step<32>(bv, bi);
     if (lane < 16 && live) {
@@ -1021,7 +1030,7 @@ int launch_head(const HeadArgs &a, hipStream_t s) {
     return set_err(BFP_EINVAL, "head: %d workgroups for batch %d", a.n_wg, a.batch);
   hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
   if (seqf) {
-    hipLaunchKernelGGL(head_mx_kernel(a.D / 64), dim3(a.n_wg, (a.batch + 63) / 64), dim3(512),
+    hipLaunchKernelGGL(head_mx_kernel(a.D / 64), dim3(a.n_wg, (a.batch + 31) / 32), dim3(512),
                        head_mx_lds(a.D), s, a, head_seq_rows(a.VOCAB));
     return launch_status("head");
   }
