@@ -74,6 +74,7 @@ struct bfp_ctx {
   LayerArgs *pt_layers = nullptr;
   PersistArgs *pt_args = nullptr;
   unsigned long long *pt_clock = nullptr;
+  double *pt_scores = nullptr;   // the long attention form's score exchange
   std::vector<void *> allocs;
   int last_path = -1;   // BFP_PATH_* of the last decode
   float last_decode_ms = 0.f, last_gen_ms = 0.f;
@@ -231,6 +232,7 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
     BFP_TRY(c->alloc((void **)&c->pt_layers, sizeof(LayerArgs) * d.NL));
     BFP_TRY(c->alloc((void **)&c->pt_args, sizeof(PersistArgs)));
     BFP_TRY(c->alloc((void **)&c->pt_clock, sizeof(unsigned long long) * (c->max_ctx + 1)));
+    BFP_TRY(c->alloc_fine((void **)&c->pt_scores, sizeof(double) * (size_t)d.H_Q * c->max_ctx));
     std::vector<LayerArgs> la(d.NL);
     for (int l = 0; l < d.NL; ++l) la[l] = layer_args(c, l, 1);
     HIP_TRY(hipMemcpy(c->pt_layers, la.data(), sizeof(LayerArgs) * d.NL, hipMemcpyHostToDevice));
@@ -244,7 +246,9 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
   pa.t_qkv = (w += 2 * D);
   pa.t_mlp = (w += 2 * nq);
   pa.t_part = (w += 2 * F);
-  pa.abort_flag = (w += 2 * 4 * (size_t)grid);
+  pa.t_sflag = (w += 2 * 4 * (size_t)grid);
+  pa.sc_buf = c->pt_scores;
+  pa.abort_flag = (w += PT_SFLAGS_PER_HEAD * (size_t)d.H_Q);
   pa.L = c->pt_layers;
   pa.steps = steps;
   pa.n_prompt = n_prompt;

@@ -298,6 +298,8 @@ __device__ __forceinline__ void epi_dres(const LayerArgs &a, int b, int c, long 
 // Attention access through ordinary loads and stores: this sequence's q|k|v
 // (D + 2KV, raw BFP) in, its attention output (D) out.
 struct AttnPlainIO {
+  // long form: every workgroup of a head scores all positions itself
+  static constexpr bool kSplitScores = false;
   const int16_t *qm;
   const int8_t *qe;
   int16_t *om;
@@ -513,10 +515,17 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
       lse[ps_][1] = io.ke1(Ke + ((o + 32) >> 4));
     }
   };
+  // long form with IO::kSplitScores: the head's ATT_DSPLIT workgroups split
+  // the scores, workgroup dg taking rows t = ATT_DSPLIT u + dg (u < nu),
+  // and exchange them (see below); else every workgroup takes every row
+  constexpr int RS = (!SHORT && IO::kSplitScores) ? ATT_DSPLIT : 1;
+  const int r0 = RS > 1 ? dg : 0;
+  const int nu = (n - r0 + RS - 1) / RS;
   if constexpr (LANE_SPLIT) {
     ls_load(0);
   } else {
-    load_krow(io, kr[0], Km, Ke, ((long long)(tid < n ? tid : n - 1) * a.H_KV + g) * HD);
+    const int t = RS * tid + r0;
+    load_krow(io, kr[0], Km, Ke, ((long long)(t < n ? t : n - 1) * a.H_KV + g) * HD);
   }
 
   if (w == 0) {            // q head hq
@@ -600,27 +609,39 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     if (tid < n) sc[tid] = ddot64_skx_bfp(q, kr[0].m, kr[0].e4) / a.inv_sqrt_hd_div;
     if (tid == pos) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
   } else {
-    // passes of KR rows per thread: rows t0 + tid + j*NT; kr[0] of the next
-    // pass is loaded as soon as this pass's kr[0] is consumed
+    // passes of KR rows per thread: rows t = RS u + r0, u = u0 + tid + j*NT;
+    // kr[0] of the next pass is loaded as soon as this pass's kr[0] is
+    // consumed
     const int last = n - 1;
-    for (int t0 = 0; t0 < n; t0 += KR * NT) {
+    for (int u0 = 0; u0 < nu; u0 += KR * NT) {
 #pragma unroll
       for (int j = 1; j < KR; ++j) {
-        const int t = t0 + tid + j * NT;
+        const int t = RS * (u0 + tid + j * NT) + r0;
         load_krow(io, kr[j], Km, Ke, ((long long)(t < n ? t : last) * a.H_KV + g) * HD);
       }
 #pragma unroll
       for (int j = 0; j < KR; ++j) {
-        const int t = t0 + tid + j * NT;
+        const int t = RS * (u0 + tid + j * NT) + r0;
         const double sj = ddot64_skx_bfp(q, kr[j].m, kr[j].e4) / a.inv_sqrt_hd_div;
         if (j == 0) {
-          const int tn = t + KR * NT;
+          const int tn = t + RS * KR * NT;
           load_krow(io, kr[0], Km, Ke, ((long long)(tn < n ? tn : last) * a.H_KV + g) * HD);
         }
         if (t < n) sc[t] = sj;
       }
     }
-    if (tid == pos % NT) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
+    // row pos from LDS, by the thread that scored it from the cache
+    if ((pos - r0) % RS == 0 && tid == ((pos - r0) / RS) % NT) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
+    if constexpr (RS > 1) {
+      // exchange: publish this workgroup's rows, then read the other
+      // workgroups' (the same q, K rows and ddot order, so the same bits)
+      lds_barrier();
+      for (int u = tid; u < nu; u += NT) io.score_put(hq, RS * u + r0, sc[RS * u + r0]);
+      io.scores_publish(hq, dg);
+      io.scores_wait(hq, dg);
+      for (int t = tid; t < n; t += NT)
+        if (t % RS != r0) sc[t] = io.score_get(hq, t);
+    }
   }
   if constexpr (SHORT) {
     BFP_ATT_STORE_V(0)

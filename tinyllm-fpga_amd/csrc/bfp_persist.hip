@@ -58,6 +58,7 @@
 namespace bfp {
 
 constexpr int PT_THREADS = 512;   // 8 waves: the attention body's workgroup size
+static_assert(PT_SFLAGS_PER_HEAD == ATT_DSPLIT, "one score flag per long-form workgroup of a head");
 constexpr int PT_NW = PT_THREADS / 64;
 constexpr int PT_HEAD_D64 = 9;    // head rows of at most 576 elements
 constexpr unsigned long long PT_SPIN_TICKS = 200000000ull;   // 2 s at 100 MHz
@@ -275,9 +276,15 @@ __device__ __forceinline__ int clamp_tok(const PersistArgs &p, int t) {
 // Attention access at the device-coherent level: q|k|v and the output as
 // tagged words, the KV cache through SC1 buffer loads and stores.
 struct AttnCohIO {
+  // long form: the head's ATT_DSPLIT workgroups split the scores and
+  // exchange them through sc_buf (rsc: hq * max_ctx + t doubles) and one
+  // tagged flag word per (head, workgroup) (rfl)
+  static constexpr bool kSplitScores = true;
   rsrc_t rq, ro;                  // this step's q|k|v and attention output words
   unsigned tag;
   Wait *w;
+  rsrc_t rsc, rfl;
+  int sc_stride;
   rsrc_t rkm, rke, rvm, rve;      // this layer's KV cache
   const int16_t *km0, *vm0;
   const int8_t *ke0, *ve0;
@@ -320,6 +327,32 @@ struct AttnCohIO {
     lds_barrier();
   }
   __device__ __forceinline__ void out(int idx, int m, int e, bool) const { st_coh(ro, 4 * idx, tagged(m, e, tag)); }
+  __device__ __forceinline__ void score_put(int hq, int t, double v) const {
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    v2u x;
+    x.x = (unsigned)b;
+    x.y = (unsigned)(b >> 32);
+    __builtin_amdgcn_raw_buffer_store_b64(x, rsc, 8 * (hq * sc_stride + t), 0, CPOL_SC1);
+  }
+  __device__ __forceinline__ double score_get(int hq, int t) const {
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    const v2u x = __builtin_amdgcn_raw_buffer_load_b64(rsc, 8 * (hq * sc_stride + t), 0, CPOL_SC1);
+    return __longlong_as_double((long long)(((unsigned long long)x.y << 32) | x.x));
+  }
+  // every wave's score stores complete (vmcnt 0), then one flag word
+  __device__ __forceinline__ void scores_publish(int hq, int dg) const {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    lds_barrier();
+    if (threadIdx.x == 0) st_coh(rfl, 4 * (hq * ATT_DSPLIT + dg), tag << 24);
+  }
+  // lanes 0..ATT_DSPLIT-1 of wave 0 wait for the other workgroups' flags
+  __device__ __forceinline__ void scores_wait(int hq, int dg) const {
+    if (threadIdx.x < ATT_DSPLIT && (int)threadIdx.x != dg) w->word(rfl, 4 * (hq * ATT_DSPLIT + threadIdx.x), tag);
+    lds_barrier();
+  }
 };
 
 // Role entry: the argument block (device memory) as scalars, the wait
@@ -516,6 +549,9 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
         io.rke = rsrc(a.k_e);
         io.rvm = rsrc(a.v_m);
         io.rve = rsrc(a.v_e);
+        io.rsc = rsrc(p.sc_buf);
+        io.rfl = rsrc(p.t_sflag);
+        io.sc_stride = a.max_ctx;
         attn_body<PPW, SHORT>(a, io, c, 0, s, s, dsm);
         stamp(p, c == 0, s, l, 3);
       }
