@@ -71,7 +71,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (SHORT ? (PPW == 3 ? 6 : 4) : 2)) v
   const int b = blockIdx.y, nq = a.D + 2 * a.KV;
   AttnPlainIO io{a.qkv_m + b * nq, a.qkv_e + b * (nq / 16), a.att_m + b * a.D,
                  a.att_e + b * (a.D / 16)};
-  attn_body<PPW, SHORT>(a, io, blockIdx.x, b, cur_kv_pos(a), cur_pos(a), dsm);
+  attn_body<PPW, SHORT>(a, io, blockIdx.x, b, [&] { return make_int2(cur_kv_pos(a), cur_pos(a)); }, dsm);
 }
 
 // ----------------------------------------------------------------- o_res

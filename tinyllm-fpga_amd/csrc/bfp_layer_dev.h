@@ -398,8 +398,8 @@ __device__ __forceinline__ void load_krow(const IO &io, KRow &r, const int16_t *
 // input, the KV cache and the output (AttnPlainIO: ordinary loads and
 // stores; the persistent decode kernel's form reads and writes at the
 // device-coherent level).  dsm: attn_lds_bytes(a.max_ctx, PPW) of LDS.
-template <int PPW, bool SHORT, class IO>
-__device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, int b, int pos, int rpos,
+template <int PPW, bool SHORT, class IO, class PosF>
+__device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, int b, PosF posf,
                                           double *dsm) {
   constexpr int NT = 64 * ATT_WAVES;
   constexpr int AVC = ATT_AVC;                 // V rows per staged chunk (short)
@@ -423,16 +423,53 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   const bool lead = dg == 0;                             // stores the cache row and the dumps
   const int grp = a.H_Q / a.H_KV, g = hq / grp;
   const int HD = 64;
-  const int n = pos + 1;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const double *cs = a.rope_row ? a.rope_row                 // (HD/2) x (cos, sin)
-                                : a.rope + (long long)rpos * HD;
   const long long kv_tok = (long long)a.H_KV * HD;     // elements per position
   int16_t *Km = a.k_m + (long long)b * a.max_ctx * kv_tok;
   int8_t *Ke = a.k_e + (long long)b * a.max_ctx * (kv_tok / 16);
   int16_t *Vm = a.v_m + (long long)b * a.max_ctx * kv_tok;
   int8_t *Ve = a.v_e + (long long)b * a.max_ctx * (kv_tok / 16);
   const bool writer = (hq % grp) == 0 && lead;
+
+  // contexts of at most 128 (PPW 2) or 256 (PPW 3) positions: each 32-lane
+  // half-wave scores one position, lane j (of 32) holding elements j and
+  // 32 + j of its K row, in passes of 2*ATT_WAVES positions.  The elements
+  // of LS_PRE passes (128 positions) are in registers at once: the first
+  // group's are loaded before the position is read (rows clamped to the
+  // cache's last slot: their values past n - 1 are never used), a second
+  // group's (PPW 3, more than 128 positions) after the first is scored.
+  // (Eight passes keep the PPW 3 form within 80 registers: three workgroups
+  // per CU.  Staging the rows through LDS with 16-byte loads instead, and
+  // reading the lanes' elements from there, measured slower: config 5
+  // 33.1k -> 32.8k tokens/s.)
+  constexpr bool LANE_SPLIT = SHORT && (PPW == 2 || PPW == 3);
+  constexpr int LS_PASS = LANE_SPLIT ? (PPW == 2 ? 128 : 256) / (2 * ATT_WAVES) : 1;
+  constexpr int LS_PRE = LS_PASS < 8 ? LS_PASS : 8;
+  int lsm[LS_PRE][2], lse[LS_PRE][2];
+  auto ls_load = [&](int g0, int last) {   // passes g0 .. g0 + LS_PRE - 1, rows up to `last`
+#pragma unroll
+    for (int ps_ = 0; ps_ < LS_PRE; ++ps_) {
+      int t = 2 * ATT_WAVES * (g0 + ps_) + 2 * w + (l >> 5);
+      t = t < last ? t : last;
+      const long long o = ((long long)t * a.H_KV + g) * HD + (l & 31);
+      lsm[ps_][0] = io.km1(Km + o);
+      lsm[ps_][1] = io.km1(Km + o + 32);
+      lse[ps_][0] = io.ke1(Ke + (o >> 4));
+      lse[ps_][1] = io.ke1(Ke + ((o + 32) >> 4));
+    }
+  };
+  if constexpr (LANE_SPLIT) ls_load(0, a.max_ctx - 1);
+  // this wave's q|k|v input: q head hq (wave 0), k head g (1), v head g (2
+  // and the rest, which do not use it)
+  int in_m, in_e;
+  io.qkv(w == 0 ? hq * HD + l : (w == 1 ? a.D + g * HD + l : a.D + a.KV + g * HD + l), in_m, in_e);
+  // the position is read after the loads that do not depend on it are issued
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const int2 pp = posf();   // (KV slot, RoPE position)
+  const int pos = pp.x, rpos = pp.y;
+  const int n = pos + 1;
+  const double *cs = a.rope_row ? a.rope_row                 // (HD/2) x (cos, sin)
+                                : a.rope + (long long)rpos * HD;
 
   // AV staging: chunk c holds rows c*AVC .. c*AVC+AVC-1 (clamped to n-1, so
   // no load sits in a branch); thread tid loads 16-byte part tid%8 of rows
@@ -492,38 +529,13 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   // phase, so a pass over 64 * ATT_WAVES * KR positions waits for memory once)
   constexpr int KR = SHORT ? 1 : 2;
   KRow kr[KR];
-  // contexts of at most 128 (PPW 2) or 256 (PPW 3) positions: each 32-lane
-  // half-wave scores one position, lane j (of 32) holding elements j and
-  // 32 + j of its K row, in passes of 2*ATT_WAVES positions.  The elements
-  // of LS_PRE passes (128 positions) are in registers at once: the first
-  // group's are in flight during the RoPE phase, a second group's (PPW 3,
-  // more than 128 positions) are loaded after the first is scored.  (Eight
-  // passes keep the PPW 3 form within 80 registers: three workgroups per CU.)
-  constexpr bool LANE_SPLIT = SHORT && (PPW == 2 || PPW == 3);
-  constexpr int LS_PASS = LANE_SPLIT ? (PPW == 2 ? 128 : 256) / (2 * ATT_WAVES) : 1;
-  constexpr int LS_PRE = LS_PASS < 8 ? LS_PASS : 8;
-  int lsm[LS_PRE][2], lse[LS_PRE][2];
-  auto ls_load = [&](int g0) {   // passes g0 .. g0 + LS_PRE - 1
-#pragma unroll
-    for (int ps_ = 0; ps_ < LS_PRE; ++ps_) {
-      int t = 2 * ATT_WAVES * (g0 + ps_) + 2 * w + (l >> 5);
-      t = t < n ? t : n - 1;
-      const long long o = ((long long)t * a.H_KV + g) * HD + (l & 31);
-      lsm[ps_][0] = io.km1(Km + o);
-      lsm[ps_][1] = io.km1(Km + o + 32);
-      lse[ps_][0] = io.ke1(Ke + (o >> 4));
-      lse[ps_][1] = io.ke1(Ke + ((o + 32) >> 4));
-    }
-  };
   // long form with IO::kSplitScores: the head's ATT_DSPLIT workgroups split
   // the scores, workgroup dg taking rows t = ATT_DSPLIT u + dg (u < nu),
   // and exchange them (see below); else every workgroup takes every row
   constexpr int RS = (!SHORT && IO::kSplitScores) ? ATT_DSPLIT : 1;
   const int r0 = RS > 1 ? dg : 0;
   const int nu = (n - r0 + RS - 1) / RS;
-  if constexpr (LANE_SPLIT) {
-    ls_load(0);
-  } else {
+  if constexpr (!LANE_SPLIT) {
     const int t = RS * tid + r0;
     load_krow(io, kr[0], Km, Ke, ((long long)(t < n ? t : n - 1) * a.H_KV + g) * HD);
   }
@@ -531,9 +543,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   if (w == 0) {            // q head hq
     int idx = hq * HD + l;
     int e;
-    int xm, xe;
-    io.qkv(idx, xm, xe);
-    int m = rope_lane(bfp_val(xm, xe), cs, e);
+    int m = rope_lane(bfp_val(in_m, in_e), cs, e);
     q[l] = bfp_val(m, e);
     if (a.dump && lead) {
       int cm, ce;
@@ -542,11 +552,8 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
       if ((l & 15) == 0) a.dump->e[ST_Q][b * (a.dump->mstride[ST_Q] / 16) + (idx >> 4)] = (int8_t)ce;
     }
   } else if (w == 1) {     // k head g
-    int idx = a.D + g * HD + l;
     int e;
-    int xm, xe;
-    io.qkv(idx, xm, xe);
-    int m = rope_lane(bfp_val(xm, xe), cs, e);
+    int m = rope_lane(bfp_val(in_m, in_e), cs, e);
     kc[l] = bfp_val(m, e);
     long long o = ((long long)pos * a.H_KV + g) * HD + l;
     if (writer) {
@@ -560,9 +567,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
       if ((l & 15) == 0) a.dump->e[ST_K][b * (a.dump->mstride[ST_K] / 16) + (r >> 4)] = (int8_t)ce;
     }
   } else if (w == 2) {     // v head g (not rotated)
-    int idx = a.D + a.KV + g * HD + l;
-    int m, e;
-    io.qkv(idx, m, e);
+    const int m = in_m, e = in_e;
     vc[l] = bfp_val(m, e);
     long long o = ((long long)pos * a.H_KV + g) * HD + l;
     if (writer) {
@@ -587,7 +592,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     const double q0 = q[j], q1 = q[32 + j];
     const double k0 = kc[j], k1 = kc[32 + j];
     for (int g0 = 0; g0 < LS_PASS && 2 * ATT_WAVES * g0 < n; g0 += LS_PRE) {   // uniform
-      if (g0 > 0) ls_load(g0);
+      if (g0 > 0) ls_load(g0, n - 1);
 #pragma unroll
       for (int ps_ = 0; ps_ < LS_PRE; ++ps_) {
         if (2 * ATT_WAVES * (g0 + ps_) >= n) break;   // uniform

@@ -552,7 +552,7 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
         io.rsc = rsrc(p.sc_buf);
         io.rfl = rsrc(p.t_sflag);
         io.sc_stride = a.max_ctx;
-        attn_body<PPW, SHORT>(a, io, c, 0, s, s, dsm);
+        attn_body<PPW, SHORT>(a, io, c, 0, [s] { return make_int2(s, s); }, dsm);
         stamp(p, c == 0, s, l, 3);
       }
       const int ln = l + 1 < p.NL ? l + 1 : 0;
