@@ -126,6 +126,9 @@ def parse():
     ap.add_argument("--decode-probe", action="store_true",
                     help="with --decode-only: also run the HBM ceiling probe (its fixed read "
                          "and copy sizes calibrate rocprof's FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--decode-trace", action="store_true",
+                    help="with --decode-only: also run config 3 once with the persistent "
+                         "kernel's stage stamps and report the per-stage times")
     return ap.parse_args()
 
 
@@ -352,6 +355,75 @@ def decode_leg(reps, n_gen=64):
             "roofline": hbm_roofline(nbytes, g * 1e-3,
                                      "per generated step: 30 layers' BFP weights + the fp32 "
                                      "embedding the head reads + KV rows 0..pos")}
+
+
+# Stage stamps of the persistent batch-1 decode (csrc/bfp_persist.hip:
+# stamp k of (step, layer), taken by thread 0 of each role's first workgroup
+# on the 100 MHz device clock): Q|K|V 0 (h in), 10 (RMSNorm done), 11
+# (matvec done), 1 (q|k|v stored), 3 (attention job 0 done); O 4 (attention
+# output in), 15, 5; G/U 6 (h1 in), 12, 13, 7; D 8 (mlp in), 14, 9 (h
+# stored).  Head stamps per step: 0 (start), 1 (vocabulary slices done),
+# 2 (token chosen).
+TRACE_INTERVALS = [
+    ("h in -> Q|K|V start (hand-off)", (-1, 9), (0, 0)),
+    ("Q|K|V RMSNorm", (0, 0), (0, 10)),
+    ("Q|K|V matvec", (0, 10), (0, 11)),
+    ("Q|K|V epilogue + store", (0, 11), (0, 1)),
+    ("attention (incl. q|k|v hand-off)", (0, 1), (0, 3)),
+    ("attention -> O start (hand-off)", (0, 3), (0, 4)),
+    ("O matvec", (0, 4), (0, 15)),
+    ("O epilogue + store", (0, 15), (0, 5)),
+    ("h1 -> G/U start (hand-off)", (0, 5), (0, 6)),
+    ("G/U RMSNorm", (0, 6), (0, 12)),
+    ("G/U matvec", (0, 12), (0, 13)),
+    ("G/U epilogue + store", (0, 13), (0, 7)),
+    ("mlp -> D start (hand-off)", (0, 7), (0, 8)),
+    ("D matvec", (0, 8), (0, 14)),
+    ("D epilogue + store", (0, 14), (0, 9)),
+    ("layer (D store to D store)", (-1, 9), (0, 9)),
+]
+
+
+def decode_trace_leg():
+    """Config 3 once on the persistent path with stage stamps: the median
+    over generated steps and layers 1..NL-1 of each stage interval (us),
+    and of the head's."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    n_prompt, n_gen = 8, 64
+    d = Dims(MAX_CTX=n_prompt + n_gen)
+    gm = BfpModel(d)
+    gm.load_fp32(synth.make_model(d, seed=0))
+    prompt = synth.make_prompt(d, n_prompt, seed=0)
+    gm.decode(prompt[None, :], n_gen)
+    gm.decode(prompt[None, :], n_gen, trace=True)
+    path = gm.decode_path()
+    tr = gm.decode_trace()
+    gm.close()
+    if tr is None:
+        return {"path": path, "stages_us": None}
+    lay, head = tr
+    lay = lay.astype(np.int64)
+    head = head.astype(np.int64)
+    steps = range(n_prompt, n_prompt + n_gen)
+    out = {}
+    for name, (dl0, k0), (dl1, k1) in TRACE_INTERVALS:
+        v = [(lay[s, l + dl1, k1] - lay[s, l + dl0, k0]) / 100.0
+             for s in steps for l in range(1, d.NL)]
+        out[name] = round(float(np.median(v)), 2)
+    out["last D store -> head start"] = round(float(np.median(
+        [(head[s, 0] - lay[s, d.NL - 1, 9]) / 100.0 for s in steps])), 2)
+    out["head: vocabulary slices"] = round(float(np.median(
+        [(head[s, 1] - head[s, 0]) / 100.0 for s in steps])), 2)
+    out["head: argmax gather"] = round(float(np.median(
+        [(head[s, 2] - head[s, 1]) / 100.0 for s in steps])), 2)
+    out["head end -> next step's Q|K|V start"] = round(float(np.median(
+        [(lay[s + 1, 0, 0] - head[s, 2]) / 100.0 for s in list(steps)[:-1]])), 2)
+    out["step"] = round(float(np.median(
+        [(lay[s + 1, 0, 0] - lay[s, 0, 0]) / 100.0 for s in list(steps)[:-1]])), 2)
+    return {"path": path, "steps": f"{n_prompt}..{n_prompt + n_gen - 1}",
+            "stages_us": out}
 
 
 def long_context_leg():
@@ -641,6 +713,9 @@ def main():
         if args.decode_probe:
             note("HBM ceiling probe")
             res["stream_ceiling"] = stream_probe()
+        if args.decode_trace:
+            note("config 3 persistent-decode stage trace")
+            res["decode_trace"] = decode_trace_leg()
         print(json.dumps(res), flush=True)
         return
     print(f"[bench] building device rings for {len(SHAPES)} shapes x {args.reps} reps",
