@@ -741,7 +741,7 @@ int raise_lds_limit(const void *f, int bytes) {
 int prepare_layer_kernels(int max_ctx, int D, int FFN) {
   const int ppw = attn_ppw(max_ctx);
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(attn_kernel(ppw)),
-                          (int)attn_lds_bytes(max_ctx, ppw)));
+                          (int)attn_lds_bytes(max_ctx, ppw, AttnPlainIO::kAvBlock)));
   int nw, tpt, nwf, tptf;
   shape_for(D / 16, nw, tpt);
   shape_for(FFN / 16, nwf, tptf);
@@ -761,7 +761,7 @@ static int launch_attn(const LayerArgs &a, hipStream_t s) {
   // long contexts: ATT_DSPLIT workgroups per head, one 16-dimension tile each
   const int split = ppw == 8 ? ATT_DSPLIT : 1;
   hipLaunchKernelGGL(attn_kernel(ppw), dim3(a.H_Q * split, a.batch), dim3(64 * ATT_WAVES),
-                     attn_lds_bytes(a.max_ctx, ppw), s, a);
+                     attn_lds_bytes(a.max_ctx, ppw, AttnPlainIO::kAvBlock), s, a);
   return launch_status("attn");
 }
 

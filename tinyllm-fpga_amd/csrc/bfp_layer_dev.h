@@ -300,6 +300,7 @@ __device__ __forceinline__ void epi_dres(const LayerArgs &a, int b, int c, long 
 struct AttnPlainIO {
   // long form: every workgroup of a head scores all positions itself
   static constexpr bool kSplitScores = false;
+  static constexpr int kAvBlock = 32;   // AV products: 16 KB of LDS, three workgroups a CU
   const int16_t *qm;
   const int8_t *qe;
   int16_t *om;
@@ -372,10 +373,13 @@ constexpr int AVL_TBP = AVL_TB + 2;
 constexpr int AVL_DEPTH = 4;
 constexpr int AVL_G = 8;        // chain: positions per group of LDS reads
 constexpr int AVL_AHEAD = 3;    // chain: groups of reads in flight ahead of the adds
-inline size_t attn_lds_bytes(int max_ctx, int ppw) {
+// av_block: rows of the short forms' AV products held in LDS at once
+// (IO::kAvBlock)
+inline size_t attn_lds_bytes(int max_ctx, int ppw, int av_block) {
   const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
   const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4) : (size_t)2 * 16 * AVL_TBP * 8;
-  return (256 + sc_len) * 8 + av;
+  const size_t pr = ppw <= 4 ? (size_t)av_block * 64 * 8 : 0;
+  return (256 + sc_len) * 8 + av + pr;
 }
 
 // One K row of the cache (64 mantissas, 4 tile exponents) in registers.
@@ -397,7 +401,7 @@ __device__ __forceinline__ void load_krow(const IO &io, KRow &r, const int16_t *
 // 0..pos with RoPE position rpos.  `io` carries every access to the q|k|v
 // input, the KV cache and the output (AttnPlainIO: ordinary loads and
 // stores; the persistent decode kernel's form reads and writes at the
-// device-coherent level).  dsm: attn_lds_bytes(a.max_ctx, PPW) of LDS.
+// device-coherent level).  dsm: attn_lds_bytes(a.max_ctx, PPW, IO::kAvBlock) of LDS.
 template <int PPW, bool SHORT, class IO, class PosF>
 __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, int b, PosF posf,
                                           double *dsm) {
@@ -416,6 +420,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   // long: product double buffer, 2 x 16 dimensions x AVL_TBP doubles
   int16_t *vsm = reinterpret_cast<int16_t *>(sc + ((a.max_ctx + 1) & ~1));
   int8_t *vse = reinterpret_cast<int8_t *>(vsm + 2 * AVC * 64);
+  double *prod = reinterpret_cast<double *>(vse + 2 * AVC * 4);   // IO::kAvBlock x 64
   double *buf = sc + ((a.max_ctx + 1) & ~1);
   __shared__ double red[ATT_WAVES];
   const int hq = SHORT ? bx : bx / ATT_DSPLIT;
@@ -727,36 +732,46 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   double acc = 0.0;
   if constexpr (SHORT) {
     // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281):
-    // every product rounded, then added, in t order.  Chunk c+1 is loaded
-    // while wave 0 adds chunk c.  Row pos is this launch's V (vc): its writer
-    // workgroup may not have stored it yet.
+    // every product rounded, then added, in t order.  Every thread forms a
+    // block of IO::kAvBlock rows' products p[t] * (m * 2^(e-15)) into LDS,
+    // one per position and dimension; wave 0 then only reads and adds them,
+    // one dimension per lane.  (Wave 0 forming each product itself cost
+    // about 70 cycles per position.)  Chunk c+1 of V is loaded while chunk c
+    // is used.  Row pos is this launch's V (vc): its writer workgroup may not
+    // have stored it yet; it is added last.
+    constexpr int PB = IO::kAvBlock;
+    static_assert(PB >= 16 && PB % 16 == 0 && PB <= AVC, "AV product block");
     const int nch = (n + AVC - 1) / AVC;
+    if (n <= 128) lds_barrier();   // wave 0's softmax wrote p without a barrier
     for (int c = 0; c < nch; ++c) {
       BFP_ATT_LOAD_V(c + 1 < nch ? c + 1 : c)
-      if (w == 0) {
-        // 16 positions at a time: their LDS reads and products are independent
-        // and issued together; only the adds form the chain
-        // pos = n - 1 is the last position: it is added after the loop
-        const int t0 = c * AVC, t1 = min(pos, t0 + AVC);
-        const int16_t *vm = vsm + (c & 1) * AVC * 64 + l;
-        const int8_t *ve = vse + (c & 1) * AVC * 4 + (l >> 4);
-        int t = t0;
-        for (; t + 16 <= t1; t += 16) {
-          double pv[16];
+      const int t0 = c * AVC, t1 = min(pos, t0 + AVC);   // rows t0 .. t1-1
+      const int16_t *vmc = vsm + (c & 1) * AVC * 64;
+      const int8_t *vec = vse + (c & 1) * AVC * 4;
+      for (int r0 = 0; r0 < t1 - t0; r0 += PB) {         // uniform
+        const int nr = min(PB, t1 - t0 - r0);
+        for (int q = tid; q < nr * 64; q += NT) {
+          const int r = r0 + (q >> 6), dd = q & 63;
+          prod[q] = sc[t0 + r] * ldexp((double)vmc[r * 64 + dd], (int)vec[r * 4 + (dd >> 4)] - 15);
+        }
+        lds_barrier();
+        if (w == 0) {
+          // 16 positions at a time: their LDS reads are issued together;
+          // only the adds form the chain
+          const double *pl = prod + l;
+          int r = 0;
+          for (; r + 16 <= nr; r += 16) {
+            double pv[16];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int r = t + i - t0;
-            pv[i] = sc[t + i] * ldexp((double)vm[r * 64], (int)ve[r * 4] - 15);
+            for (int i = 0; i < 16; ++i) pv[i] = pl[(r + i) * 64];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc = acc + pv[i];
           }
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc = acc + pv[i];
+          for (; r < nr; ++r) acc = acc + pl[r * 64];
         }
-        for (; t < t1; ++t) {
-          const int r = t - t0;
-          acc = acc + sc[t] * ldexp((double)vm[r * 64], (int)ve[r * 4] - 15);
-        }
-        if (c == nch - 1) acc = acc + sc[pos] * vc[l];
+        lds_barrier();   // the block's LDS is refilled
       }
+      if (w == 0 && c == nch - 1) acc = acc + sc[pos] * vc[l];
       if (c + 1 < nch) BFP_ATT_STORE_V(c + 1)
       lds_barrier();
     }

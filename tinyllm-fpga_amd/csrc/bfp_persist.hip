@@ -280,6 +280,7 @@ struct AttnCohIO {
   // exchange them through sc_buf (rsc: hq * max_ctx + t doubles) and one
   // tagged flag word per (head, workgroup) (rfl)
   static constexpr bool kSplitScores = true;
+  static constexpr int kAvBlock = ATT_AVC;   // a whole staged chunk's products (one workgroup a CU)
   rsrc_t rq, ro;                  // this step's q|k|v and attention output words
   unsigned tag;
   Wait *w;
@@ -764,7 +765,7 @@ static size_t persist_lds(const PersistArgs &p, int max_ctx) {
   const size_t head = (size_t)(3 * D + PW_MAX_LEAVES) * 8 + (size_t)D * 2 + nT;
   // the Q|K|V role keeps the step's RoPE row (64 doubles) ahead of both its
   // norm work space and the attention's
-  size_t lds = attn_lds_bytes(max_ctx, attn_ppw(max_ctx)) + 64 * 8;
+  size_t lds = attn_lds_bytes(max_ctx, attn_ppw(max_ctx), AttnCohIO::kAvBlock) + 64 * 8;
   lds = lds > norm + 64 * 8 ? lds : norm + 64 * 8;
   lds = lds > dx ? lds : dx;
   lds = lds > head ? lds : head;
