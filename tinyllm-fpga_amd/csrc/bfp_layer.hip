@@ -860,31 +860,43 @@ int launch_embed(const EmbedArgs &a, hipStream_t s) {
 // Operands: B (lane L: c = L / 16, sequence L % 16) is a group of 16 normed
 // hidden vectors, held in registers for the whole kernel; A (lane L: row
 // L % 16, c = L / 16) comes from the 16-row tile of the embedding in LDS,
-// staged as float32 from a copy permuted at load time (ep, below).  The
-// next tile's loads are issued before a tile's MFMAs and stored to the
-// other LDS buffer after them.  Output (lane L, element v) is row
+// staged as float32 from a copy permuted at load time (ep, below) into two
+// LDS buffers by tile parity.  Output (lane L, element v) is row
 // 4v + L / 16, sequence L % 16.
 // Workgroup: 8 waves, 32 sequences (blockIdx.y), rows [x * rpw, + rpw) in
-// 16-row tiles.  Waves 4g .. 4g + 3 take sequence group g (16 sequences);
-// wave h of them holds partials h, h + 4, h + 8, h + 12 (NB x 4 doubles of B
-// a lane), so the butterfly's first two levels stay in the wave: a_h =
+// 16-row tiles.  Wave w takes sequence group g = w & 1 (16 sequences) and
+// partials h, h + 4, h + 8, h + 12 with h = w >> 1 (NB x 4 doubles of B a
+// lane), so the butterfly's first two levels stay in the wave: a_h =
 // p_h + p_(h+8), a_(h+4) = p_(h+4) + p_(h+12), b_h = a_h + a_(h+4).  Waves
 // h = 1..3 hand b_h over through LDS and wave h = 0 forms (b0 + b2) +
 // (b1 + b3) and keeps the per-sequence first-index argmax, which goes to
-// part_v / part_i.  ep holds a wave's four partials contiguously:
-// ep[row][(4i + c) * 16 + 4h + j] = embed[row][64i + 4(h + 4j) + c].
+// part_v / part_i.  The two h = 0 waves (w = 0, 1) run on different SIMDs
+// (waves go to the four SIMDs in turn).
+// The hand-over is double-buffered by tile parity, so one barrier a tile
+// orders both it and the embedding buffers.  A tile's embedding loads are
+// issued two tiles ahead (two register sets) and stored to LDS after the
+// MFMAs of the tile before it.  ep holds a wave's four partials
+// contiguously: ep[row][(4i + c) * 16 + 4h + j] = embed[row][64i + 4(h + 4j) + c].
 typedef double head_d4 __attribute__((ext_vector_type(4)));
 constexpr int HEAD_ROW_PAD = 4;   // floats: rows 16 B apart in the LDS banks
-inline int head_mx_lds(int D) { return 2 * 16 * (D + HEAD_ROW_PAD) * 4 + 2 * 3 * 4 * 64 * 8; }
+constexpr int HEAD_XCH = 2 * 3 * 4 * 64;   // doubles of one hand-over buffer
+inline int head_mx_lds(int D) { return 2 * 16 * (D + HEAD_ROW_PAD) * 4 + 2 * HEAD_XCH * 8; }
+
+// one tile's staging registers, by name (an array of them, indexed in the
+// lambdas, stayed in scratch memory)
+struct HeadStage {
+  float4 v0, v1, v2, v3, v4;
+};
 
 template <int NB>
 __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
   constexpr int D = 64 * NB, RS = D + HEAD_ROW_PAD, F4 = D / 4;   // float4 per row
   constexpr int TQ = 16 * F4, KQ = (TQ + 511) / 512;               // float4 per tile, per thread
+  static_assert(KQ <= 5, "at most 5 staging registers");
   extern __shared__ float esm[];          // 2 x 16 rows x RS floats, then the hand-over
-  double *xch = reinterpret_cast<double *>(esm + 2 * 16 * RS);     // [group][h - 1][v][lane]
+  double *xch = reinterpret_cast<double *>(esm + 2 * 16 * RS);     // [parity][group][h - 1][v][lane]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = w >> 2, h = w & 3;
+  const int g = w & 1, h = w >> 1;
   const int sl = blockIdx.y * 32 + 16 * g + (lane & 15);
   const bool live = sl < a.batch;
   const int sc = live ? sl : a.batch - 1;
@@ -900,44 +912,43 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
   const int row_lo = blockIdx.x * rpw;
   const int row_hi = row_lo + rpw < a.VOCAB ? row_lo + rpw : a.VOCAB;
   const int ntile = (row_hi - row_lo) / 16;
-  // staging registers by name (an array of them, indexed in the lambdas,
-  // stayed in scratch memory)
-  static_assert(KQ <= 5, "at most 5 staging registers");
-  float4 st0, st1, st2, st3, st4;
-  auto load_tile = [&](int t) {
+  auto load_tile = [&](HeadStage &st, int t) {
     const float4 *src = reinterpret_cast<const float4 *>(a.embedp + (long long)(row_lo + 16 * t) * D);
     auto ld = [&](int k) {
       const int q = k * 512 + tid;
       return src[q < TQ ? q : TQ - 1];
     };
-    st0 = ld(0);
-    if constexpr (KQ > 1) st1 = ld(1);
-    if constexpr (KQ > 2) st2 = ld(2);
-    if constexpr (KQ > 3) st3 = ld(3);
-    if constexpr (KQ > 4) st4 = ld(4);
+    st.v0 = ld(0);
+    if constexpr (KQ > 1) st.v1 = ld(1);
+    if constexpr (KQ > 2) st.v2 = ld(2);
+    if constexpr (KQ > 3) st.v3 = ld(3);
+    if constexpr (KQ > 4) st.v4 = ld(4);
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const HeadStage &st, int buf) {
     float *dst = esm + buf * 16 * RS;
     auto stq = [&](int k, float4 v) {
       const int q = k * 512 + tid, r = q / F4, j = q - r * F4;
       if (q < TQ) *reinterpret_cast<float4 *>(dst + r * RS + 4 * j) = v;
     };
-    stq(0, st0);
-    if constexpr (KQ > 1) stq(1, st1);
-    if constexpr (KQ > 2) stq(2, st2);
-    if constexpr (KQ > 3) stq(3, st3);
-    if constexpr (KQ > 4) stq(4, st4);
+    stq(0, st.v0);
+    if constexpr (KQ > 1) stq(1, st.v1);
+    if constexpr (KQ > 2) stq(2, st.v2);
+    if constexpr (KQ > 3) stq(3, st.v3);
+    if constexpr (KQ > 4) stq(4, st.v4);
   };
   double bv = -INFINITY;
   int bi = 0x7fffffff;
+  HeadStage s0, s1;
   if (ntile > 0) {
-    load_tile(0);
-    store_tile(0);
+    load_tile(s0, 0);
+    store_tile(s0, 0);
   }
+  if (ntile > 1) load_tile(s1, 1);
   lds_barrier();
-  double *xg = xch + g * (3 * 4 * 64) + lane;   // + ((h - 1) * 4 + v) * 64
-  for (int t = 0; t < ntile; ++t) {
-    if (t + 1 < ntile) load_tile(t + 1);
+  double *xg = xch + g * (3 * 4 * 64) + lane;   // + parity * HEAD_XCH + ((h - 1) * 4 + v) * 64
+  // tile t: `nxt` holds tile t + 1 (loaded a tile ago), `fut` takes t + 2
+  auto tile = [&](int t, HeadStage &nxt, HeadStage &fut) {
+    if (t + 2 < ntile) load_tile(fut, t + 2);
     const float *ar = esm + (t & 1) * 16 * RS + (lane & 15) * RS + 16 * c + 4 * h;
     head_d4 acc[4];
 #pragma unroll
@@ -953,17 +964,21 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
     double b4[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) b4[v] = (acc[0][v] + acc[2][v]) + (acc[1][v] + acc[3][v]);
+    double *xb = xg + (t & 1) * HEAD_XCH;
     if (h) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) xg[((h - 1) * 4 + v) * 64] = b4[v];
+      for (int v = 0; v < 4; ++v) xb[((h - 1) * 4 + v) * 64] = b4[v];
     }
-    if (t + 1 < ntile) store_tile((t + 1) & 1);
+    if (t + 1 < ntile) store_tile(nxt, (t + 1) & 1);
+    // Orders this tile's hand-over before wave h = 0 reads it, the store of
+    // tile t + 1 before its MFMAs, and every read of buffer t & 1 (embedding
+    // and hand-over) before tile t + 2 writes it.
     lds_barrier();
     if (!h) {
       const int rbase = row_lo + 16 * t + (lane >> 4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const double x = (b4[v] + xg[(4 + v) * 64]) + (xg[v * 64] + xg[(8 + v) * 64]);
+        const double x = (b4[v] + xb[(4 + v) * 64]) + (xb[v * 64] + xb[(8 + v) * 64]);
         const int row = rbase + 4 * v;
         if (a.logits && live) a.logits[(long long)sl * a.VOCAB + row] = x;
         if (x > bv || (x == bv && row < bi)) {
@@ -972,7 +987,10 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
         }
       }
     }
-    lds_barrier();   // the hand-over is read before it is written for the next tile
+  };
+  for (int t = 0; t < ntile; t += 2) {
+    tile(t, s1, s0);
+    if (t + 1 < ntile) tile(t + 1, s0, s1);
   }
   if (!h) {
     argmax_step<16>(bv, bi);   // the four lanes of a sequence (lane / 16)
