@@ -402,7 +402,7 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->hn, sizeof(double) * B * d.D)) ||
       (rc = c->alloc((void **)&c->part_v, sizeof(double) * B * head_part_max(c))) ||
       (rc = c->alloc((void **)&c->part_i, sizeof(int) * B * head_part_max(c))) ||
-      (rc = c->alloc((void **)&c->state, sizeof(int) * (B + 1))) ||
+      (rc = c->alloc((void **)&c->state, sizeof(int) * (B + 2))) ||   // + k_ctl_embed's count
       (rc = c->alloc((void **)&c->last, sizeof(int) * B)) ||
       (rc = c->alloc((void **)&c->dump_dev, sizeof(StageDump)))) {
     delete c;
@@ -1050,10 +1050,9 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     BFP_TRY(tmp.alloc((void **)&dhe, (size_t)batch * steps * d.NL * d.D / 16));
   }
   HIP_TRY(hipMemcpyAsync(dprompt, prompt, sizeof(int) * batch * n_prompt, hipMemcpyHostToDevice, s));
-  std::vector<int> st(batch + 1);
-  st[0] = 0;
+  std::vector<int> st(batch + 2, 0);   // step, next inputs, k_ctl_embed's arrival count
   for (int b = 0; b < batch; ++b) st[1 + b] = prompt[b * n_prompt];
-  HIP_TRY(hipMemcpyAsync(c->state, st.data(), sizeof(int) * (batch + 1), hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(c->state, st.data(), sizeof(int) * (batch + 2), hipMemcpyHostToDevice, s));
 
   PersistArgs pa{};
   int grid = 0;
@@ -1069,8 +1068,9 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   HeadArgs ha = head_args(c, batch, nullptr);
   CtlArgs ca{batch, n_prompt, n_gen, ha.n_wg, 0, c->state, dprompt, dout, c->part_v,
              c->part_i, c->last, rtl_loop ? 1 : 0};
+  // A step: the layers, the head, then k_ctl_embed (the token loop, the step
+  // increment and the next step's embedding); step 0's embedding goes first.
   auto enqueue_step = [&](bool head) -> int {
-    BFP_TRY(launch_embed(ea, s));
     for (int l = 0; l < d.NL; ++l) {
       LayerArgs a = layer_args(c, l, batch);
       a.pos_ptr = c->state;
@@ -1082,7 +1082,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     CtlArgs cc = ca;
     cc.head = head ? 1 : 0;
     if (head) BFP_TRY(launch_head(ha, s));
-    BFP_TRY(launch_ctl(cc, s));
+    BFP_TRY(launch_ctl_embed(cc, ea, s));
     return BFP_OK;
   };
   const bool use_graph = !(flags & BFP_DECODE_NO_GRAPH);
@@ -1113,6 +1113,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     (void)hipEventCreate(&ev1);
     (void)hipEventCreate(&evg);
     (void)hipEventRecord(ev0, s);
+    if (steps > 0) rc = launch_embed(ea, s);
     for (int step = 0; step < steps && !rc; ++step) {
       const bool head = rtl_loop || step >= n_prompt - 1;
       if (step == n_prompt) (void)hipEventRecord(evg, s);

@@ -80,6 +80,9 @@ int head_workgroups(int vocab, int D, int rows_single, int batch, bool have64);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);
 int launch_ctl(const CtlArgs &a, hipStream_t s);
+// k_ctl + step increment + the next step's k_embed in one launch; the step
+// counter's arrival count lives at state[1 + batch] and must be 0 at entry.
+int launch_ctl_embed(const CtlArgs &a, const EmbedArgs &e, hipStream_t s);
 struct RtlArgs;
 // The composed RTL-exact layer step (bfp_rtl.hip).
 int launch_rtl_layer(const RtlArgs &a, hipStream_t s);

@@ -622,9 +622,10 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
 // With rtl_loop, the policy of the FPGA driver (autoregress_bfp_top.sv
 // :357-386): every step's argmax is recorded (result_buf[step]) and the
 // next input is prompt[s+1] while s+1 < n_prompt, else this step's argmax.
-__global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
-  const int b = blockIdx.x, l = threadIdx.x;
-  const int s = a.state[0];
+// Argmax over the head's per-workgroup maxima of sequence b, the token
+// record and the next input (wave 0; returns the next input in every lane).
+__device__ __forceinline__ int ctl_body(const CtlArgs &a, int b, int s) {
+  const int l = threadIdx.x & 63;
   int nid = -1;
   if (a.head) {
     double best = -INFINITY;
@@ -645,12 +646,18 @@ __global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
     argmax_step<32>(best, besti);
     nid = besti;
   }
+  const int next = ctl_next(s, nid, a.n_prompt, a.prompt + b * a.n_prompt, a.rtl_loop);
   if (l == 0) {
     if (a.head) a.last[b] = nid;
     const int k = ctl_out_slot(s, a.n_prompt, a.n_gen, a.rtl_loop);
     if (a.head && k >= 0) a.out[b * ctl_out_len(a.n_prompt, a.n_gen, a.rtl_loop) + k] = nid;
-    a.state[1 + b] = ctl_next(s, nid, a.n_prompt, a.prompt + b * a.n_prompt, a.rtl_loop);
+    a.state[1 + b] = next;
   }
+  return next;
+}
+
+__global__ __launch_bounds__(64) void k_ctl(CtlArgs a) {
+  ctl_body(a, blockIdx.x, a.state[0]);
 }
 
 __global__ __launch_bounds__(64) void k_step_inc(int *state) {
@@ -658,10 +665,9 @@ __global__ __launch_bounds__(64) void k_step_inc(int *state) {
 }
 
 // Embedding lookup of the BFP table: embed_q[tid] = fp_quantize_vec(embed[tid])
-// (full.py:411-412), quantised on the fly from the float32 table.
-__global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
-  const int b = blockIdx.x;
-  int tok = a.state[1 + b];
+// (full.py:411-412), quantised on the fly from the float32 table, into h of
+// sequence b.
+__device__ __forceinline__ void embed_body(const EmbedArgs &a, int b, int tok) {
   tok = tok < 0 ? 0 : (tok >= a.VOCAB ? a.VOCAB - 1 : tok);
   const float *row = a.embed + (long long)tok * a.D;
   for (int base = 0; base < a.D; base += blockDim.x) {
@@ -673,6 +679,35 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
     if (ok) {
       a.h_m[b * a.D + i] = (int16_t)m;
       if ((i & 15) == 0) a.h_e[b * (a.D / 16) + (i >> 4)] = (int8_t)e;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
+  embed_body(a, blockIdx.x, a.state[1 + blockIdx.x]);
+}
+
+// The end of a batched decode step in one launch: k_ctl, the step increment
+// and the next step's k_embed.  Sequence b's workgroup picks its next input
+// and embeds it into h (the head has read h already).  The step counter
+// moves once every workgroup has read it: each counts itself in at
+// state[1 + batch] (device-scope, after its read), and the last one resets
+// that count and advances state[0].
+__global__ __launch_bounds__(256) void k_ctl_embed(CtlArgs a, EmbedArgs e) {
+  __shared__ int tok_s;
+  const int b = blockIdx.x;
+  const int s = a.state[0];
+  if (threadIdx.x < 64) {
+    const int next = ctl_body(a, b, s);
+    if (threadIdx.x == 0) tok_s = next;
+  }
+  __syncthreads();
+  embed_body(e, b, tok_s);
+  if (threadIdx.x == 0) {
+    const int n = __hip_atomic_fetch_add(a.state + 1 + a.batch, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (n == a.batch - 1) {
+      a.state[1 + a.batch] = 0;
+      a.state[0] = s + 1;
     }
   }
 }
@@ -1073,6 +1108,13 @@ int launch_ctl(const CtlArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(k_ctl, dim3(a.batch), dim3(64), 0, s, a);
   hipLaunchKernelGGL(k_step_inc, dim3(1), dim3(64), 0, s, a.state);
   return launch_status("ctl");
+}
+
+int launch_ctl_embed(const CtlArgs &a, const EmbedArgs &e, hipStream_t s) {
+  if (e.batch != a.batch || e.state != a.state)
+    return set_err(BFP_EINVAL, "ctl_embed: batch %d / %d or state differ", a.batch, e.batch);
+  hipLaunchKernelGGL(k_ctl_embed, dim3(a.batch), dim3(256), 0, s, a, e);
+  return launch_status("ctl_embed");
 }
 
 }  // namespace bfp
