@@ -57,6 +57,8 @@ struct bfp_ctx {
   int head_wg = 0, head_rows = 0;
   double *part_v = nullptr;
   int *part_i = nullptr, *state = nullptr, *last = nullptr;
+  unsigned *t_h1 = nullptr, *t_h = nullptr;   // batched decode: h1, h as tagged words (max_batch x D)
+  int *t_abort = nullptr;    // set by a tagged wait that gave up
   StageDump *dump_dev = nullptr;
   // engine tables of the composed RTL layer, made on its first use
   uint16_t *rtl_exp = nullptr;
@@ -404,6 +406,9 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->part_i, sizeof(int) * B * head_part_max(c))) ||
       (rc = c->alloc((void **)&c->state, sizeof(int) * (B + 2))) ||   // + k_ctl_embed's count
       (rc = c->alloc((void **)&c->last, sizeof(int) * B)) ||
+      (rc = c->alloc((void **)&c->t_h1, sizeof(unsigned) * B * d.D)) ||
+      (rc = c->alloc((void **)&c->t_h, sizeof(unsigned) * B * d.D)) ||
+      (rc = c->alloc((void **)&c->t_abort, sizeof(int))) ||
       (rc = c->alloc((void **)&c->dump_dev, sizeof(StageDump)))) {
     delete c;
     return nullptr;
@@ -1063,6 +1068,10 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     return decode_copy_out(c, batch, steps, n_out, dout, tokens_out, dhm, dhe, hist_m, hist_e);
   }
   c->last_path = (flags & BFP_DECODE_NO_GRAPH) ? BFP_PATH_EAGER : BFP_PATH_GRAPH;
+  // no tagged word of an earlier decode may carry a tag of this one
+  HIP_TRY(hipMemsetAsync(c->t_h1, 0, sizeof(unsigned) * batch * d.D, s));
+  HIP_TRY(hipMemsetAsync(c->t_h, 0, sizeof(unsigned) * batch * d.D, s));
+  HIP_TRY(hipMemsetAsync(c->t_abort, 0, sizeof(int), s));
 
   EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
   HeadArgs ha = head_args(c, batch, nullptr);
@@ -1077,6 +1086,10 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
       a.hist_m = dhm;
       a.hist_e = dhe;
       a.hist_steps = steps;
+      a.t_h1 = c->t_h1;   // tags are unique per (step, layer) within a decode
+      a.t_h = c->t_h;
+      a.g1_next = l + 1 < d.NL ? c->g1 + (size_t)(l + 1) * d.D : nullptr;
+      a.t_abort = c->t_abort;
       BFP_TRY(launch_layer(a, s));
     }
     CtlArgs cc = ca;
@@ -1132,6 +1145,12 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   if (!rc) {
     hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) rc = set_err(BFP_EIO, "decode: %s", hipGetErrorString(e));
+  }
+  if (!rc) {
+    int ab = 0;
+    hipError_t e = hipMemcpy(&ab, c->t_abort, sizeof ab, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) rc = set_err(BFP_EIO, "decode: %s", hipGetErrorString(e));
+    else if (ab) rc = set_err(BFP_EIO, "decode: a wait for tagged words gave up");
   }
   if (!rc) {
     float ms = 0.f, gms = 0.f;

@@ -52,6 +52,13 @@ struct LayerArgs {
   // h_out history for per-(step, layer) checks: ((b*hist_steps + pos)*NL + layer)*D
   int16_t *hist_m; int8_t *hist_e;
   int hist_steps, layer, NL;
+  // batched decode: h1 and h also as tagged words (batch x D each), read by
+  // the RMSNorm workgroups of the O and D launches (k_o_res_norm_mx: norm 2;
+  // k_d_res_norm_mx: the next layer's norm 1, with its gamma g1_next), or
+  // null; t_abort is set when one of their bounded waits gives up
+  unsigned *t_h1, *t_h;
+  const double *g1_next;
+  int *t_abort;
 };
 
 // The composed RTL-exact layer (smollm_layer_bfp.sv) on one sequence: the

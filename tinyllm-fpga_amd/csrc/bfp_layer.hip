@@ -184,20 +184,11 @@ __global__ __launch_bounds__(256) void k_norm_seq(LayerArgs a, int which) {
   }
 }
 
-// The same with thread t on elements 2t, 2t + 1 (rmsnorm_pairs; blockDim
-// >= D / 2): one division pair and one tile quantisation per thread, the
-// squares' pairwise sum over LDS.  dsm: D + PW_MAX_LEAVES doubles.
-__global__ __launch_bounds__(512) void k_norm_pairs(LayerArgs a, int which) {
-  extern __shared__ double dsm[];
-  const int b = blockIdx.x, nT = a.D / 16;
-  const int16_t *hm = (which == 1 ? a.h_m : a.h1_m) + (long long)b * a.D;
-  const int8_t *he = (which == 1 ? a.h_e : a.h1_e) + (long long)b * nT;
-  const double *g = which == 1 ? a.g1 : a.g2;
-  const int i0 = 2 * (int)threadIdx.x;
+// xn (and the stage dump) of sequence b from rmsnorm_pairs' (m0, m1, e).
+__device__ __forceinline__ void norm_pairs_out(const LayerArgs &a, int b, int which, int m0, int m1,
+                                               int e) {
+  const int i0 = 2 * (int)threadIdx.x, nT = a.D / 16;
   const bool on = i0 < a.D;
-  const double2 gg = *reinterpret_cast<const double2 *>(g + (on ? i0 : 0));
-  int m0, m1, e;
-  rmsnorm_pairs(hm, he, gg.x, gg.y, a.D, dsm, dsm + a.D, m0, m1, e);
   if (on) {
     int16_t *om = a.xn_m + (long long)b * a.D;
     int8_t *oe = a.xn_e + (long long)b * nT;
@@ -211,6 +202,22 @@ __global__ __launch_bounds__(512) void k_norm_pairs(LayerArgs a, int which) {
       if ((i0 & 15) == 0) d->e[st][b * (d->mstride[st] / 16) + (i0 >> 4)] = (int8_t)e;
     }
   }
+}
+
+// The same with thread t on elements 2t, 2t + 1 (rmsnorm_pairs; blockDim
+// >= D / 2): one division pair and one tile quantisation per thread, the
+// squares' pairwise sum over LDS.  dsm: D + PW_MAX_LEAVES doubles.
+__global__ __launch_bounds__(512) void k_norm_pairs(LayerArgs a, int which) {
+  extern __shared__ double dsm[];
+  const int b = blockIdx.x, nT = a.D / 16;
+  const int16_t *hm = (which == 1 ? a.h_m : a.h1_m) + (long long)b * a.D;
+  const int8_t *he = (which == 1 ? a.h_e : a.h1_e) + (long long)b * nT;
+  const double *g = which == 1 ? a.g1 : a.g2;
+  const int i0 = 2 * (int)threadIdx.x;
+  const double2 gg = *reinterpret_cast<const double2 *>(g + (i0 < a.D ? i0 : 0));
+  int m0, m1, e;
+  rmsnorm_pairs(hm, he, gg.x, gg.y, a.D, dsm, dsm + a.D, m0, m1, e);
+  norm_pairs_out(a, b, which, m0, m1, e);
 }
 
 // The RMSNorm launch of the multi-sequence paths: the pair form up to
@@ -379,6 +386,77 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_mx(LayerArgs a) {
   })
 }
 
+// An RMSNorm of sequence b (k_norm_pairs' arithmetic and output; which = 1:
+// norm 1 with gamma g, 2: norm 2) from tagged words that the blocks of the
+// same launch store (words: the sequence's D words): each thread polls whole
+// quads until all four carry this (step, layer)'s tag.  The wait is
+// bounded: after TW_SPIN_TICKS, or once another wait has given up, it sets
+// *t_abort and goes on (the host then reports the decode as failed).
+constexpr unsigned long long TW_SPIN_TICKS = 200000000ull;   // 2 s at 100 MHz
+__device__ __forceinline__ void norm_tagged(const LayerArgs &a, int b, int which, const unsigned *words,
+                                            const double *g, double *dsm) {
+  const int D = a.D;
+  int16_t *hm = reinterpret_cast<int16_t *>(dsm + D + PW_MAX_LEAVES);
+  int8_t *he = reinterpret_cast<int8_t *>(hm + D);
+  const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
+  const tw_rsrc r = tw_make(words + (long long)b * D, D * 4), rf = tw_make(a.t_abort, 4);
+  const int i0 = 2 * (int)threadIdx.x;
+  const double2 gg = *reinterpret_cast<const double2 *>(g + (i0 < D ? i0 : 0));
+  for (int q = threadIdx.x; q < D / 4; q += blockDim.x) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    uint4 v;
+    for (unsigned it = 0;; ++it) {
+      typedef unsigned v4u __attribute__((ext_vector_type(4)));
+      const v4u u = __builtin_amdgcn_raw_buffer_load_b128(r, 16 * q, 0, TW_SC1);
+      v = make_uint4(u.x, u.y, u.z, u.w);
+      if ((v.x >> 24) == tag && (v.y >> 24) == tag && (v.z >> 24) == tag && (v.w >> 24) == tag) break;
+      if ((it & 63u) == 63u &&
+          (__builtin_amdgcn_raw_buffer_load_b32(rf, 0, 0, TW_SC1) != 0u ||
+           __builtin_amdgcn_s_memrealtime() - t0 > TW_SPIN_TICKS)) {
+        __builtin_amdgcn_raw_buffer_store_b32(1u, rf, 0, 0, TW_SC1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    hm[4 * q] = (int16_t)(v.x & 0xffffu);
+    hm[4 * q + 1] = (int16_t)(v.y & 0xffffu);
+    hm[4 * q + 2] = (int16_t)(v.z & 0xffffu);
+    hm[4 * q + 3] = (int16_t)(v.w & 0xffffu);
+    if ((q & 3) == 0) he[q >> 2] = (int8_t)((v.x >> 16) & 0xffu);
+  }
+  __syncthreads();
+  int m0, m1, e;
+  rmsnorm_pairs(hm, he, gg.x, gg.y, D, dsm, dsm + D, m0, m1, e);
+  norm_pairs_out(a, b, which, m0, m1, e);
+}
+
+// k_o_res_mx's blocks (ids below nblk: chunk id % (D/16), sequence group
+// id / (D/16)) and RMSNorm 2 (one workgroup per sequence, ids from nblk) in
+// one launch.  The blocks also store h1 as tagged words, which the norm
+// workgroups poll.  Workgroups are dispatched in id order and the blocks
+// never wait, so every block a norm workgroup waits for has been dispatched
+// before it.  blockDim >= D / 2.
+__global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_norm_mx(LayerArgs a, int nblk) {
+  __shared__ long long Ao[16 * MX_SEQ];
+  __shared__ int Mo[16 * MX_SEQ];
+  extern __shared__ int8_t mx_ex[];
+  if ((int)blockIdx.x >= nblk) {
+    norm_tagged(a, blockIdx.x - nblk, 2, a.t_h1, a.g2, reinterpret_cast<double *>(mx_ex));
+    return;
+  }
+  const int nT = a.D / 16, c = blockIdx.x % nT, b0 = blockIdx.x / nT * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
+  mx_block<1>(a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT,
+              a.att_m + (long long)b0 * a.D, a.att_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(MX_SEQ, {
+    const int q_ = r_ * MX_SEQ + j_;
+    (void)cc_;
+    epi_ores(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h_m[b * a.D + c * 16 + r_],
+             a.h_e[b * (a.D / 16) + c], tag);
+  })
+}
+
 // G and U: the G chunk (2x) and U chunk (2x+1) of FFN chunk x per block.
 __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_gu_mx(LayerArgs a) {
   __shared__ long long Ao[2 * 16 * MX_SEQ];
@@ -411,6 +489,31 @@ __global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_mx(LayerArgs a) {
     (void)cc_;
     epi_dres(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h1_m[b * a.D + c * 16 + r_],
              a.h1_e[b * (a.D / 16) + c]);
+  })
+}
+
+
+// k_d_res_mx's blocks (ids below nblk) and the next layer's RMSNorm 1 (one
+// workgroup per sequence, ids from nblk, gamma g1_next) in one launch, as
+// k_o_res_norm_mx: the blocks also store h as tagged words.
+__global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_norm_mx(LayerArgs a, int nblk) {
+  __shared__ long long Ao[16 * MX_SEQ];
+  __shared__ int Mo[16 * MX_SEQ];
+  extern __shared__ int8_t mx_ex[];
+  if ((int)blockIdx.x >= nblk) {
+    norm_tagged(a, blockIdx.x - nblk, 1, a.t_h, a.g1_next, reinterpret_cast<double *>(mx_ex));
+    return;
+  }
+  const int nT = a.FFN / 16, nc = a.D / 16, c = blockIdx.x % nc, b0 = blockIdx.x / nc * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
+  mx_block<1>(a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT,
+              a.mlp_m + (long long)b0 * a.FFN, a.mlp_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(MX_SEQ, {
+    const int q_ = r_ * MX_SEQ + j_;
+    (void)cc_;
+    epi_dres(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h1_m[b * a.D + c * 16 + r_],
+             a.h1_e[b * (a.D / 16) + c], tag);
   })
 }
 
@@ -810,23 +913,57 @@ static int mx_waves(int nT, int n_blocks) {
   return w < 1 ? 1 : w;
 }
 
+// Waves per workgroup of k_d_res_mx (up to MX_WAVES_D).
+static int mx_waves_d(const LayerArgs &a) {
+  const int nTF = a.FFN / 16, n_blocks = a.D / 16 * ((a.batch + MX_SEQ - 1) / MX_SEQ);
+  int wd = 2048 / n_blocks;
+  wd = wd < (nTF + 1) / 2 ? wd : (nTF + 1) / 2;
+  return wd < MX_WAVES_D ? (wd < 1 ? 1 : wd) : MX_WAVES_D;
+}
+
+// The batched decode's RMSNorms in the O and D launches: when the tagged
+// buffers are given, no stage dump is asked for, and both launches' blocks
+// have at least D / 2 threads (rmsnorm_pairs).  The same for every layer
+// of a decode, so a layer skips its norm 1 exactly when the layer before
+// ran it.
+static bool mx_fused_norms(const LayerArgs &a) {
+  const int G = (a.batch + MX_SEQ - 1) / MX_SEQ, bo = a.D / 16;
+  return a.t_h1 && a.t_h && a.t_abort && !a.dump && 128 * mx_waves(a.D / 16, bo * G) >= a.D &&
+         128 * mx_waves_d(a) >= a.D;
+}
+
 static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   const int G = (a.batch + MX_SEQ - 1) / MX_SEQ;
   const int bq = (a.D + 2 * a.KV) / 16, bo = a.D / 16, bg = a.FFN / 16;
-  launch_norm_seq(a, 1, s);
+  const bool fused = mx_fused_norms(a);
+  if (!(fused && a.layer > 0)) launch_norm_seq(a, 1, s);   // else the last layer's D launch ran it
   hipLaunchKernelGGL(k_qkv_mx, dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
                      mx_lds_bytes(1, nTD), s, a);
   BFP_TRY(launch_attn(a, s));
-  hipLaunchKernelGGL(k_o_res_mx, dim3(bo, G), dim3(64 * mx_waves(nTD, bo * G)),
-                     mx_lds_bytes(1, nTD), s, a);
-  launch_norm_seq(a, 2, s);
+  const int wo = mx_waves(nTD, bo * G);
+  if (fused) {
+    // O + RMSNorm 2 in one launch (batched decode)
+    const size_t shn = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)a.D * 3;
+    const size_t sho = mx_lds_bytes(1, nTD);
+    hipLaunchKernelGGL(k_o_res_norm_mx, dim3(bo * G + a.batch), dim3(64 * wo), sho > shn ? sho : shn, s,
+                       a, bo * G);
+  } else {
+    hipLaunchKernelGGL(k_o_res_mx, dim3(bo, G), dim3(64 * wo), mx_lds_bytes(1, nTD), s, a);
+    launch_norm_seq(a, 2, s);
+  }
   hipLaunchKernelGGL(k_gu_mx, dim3(bg, G), dim3(64 * mx_waves(nTD, bg * G)),
                      mx_lds_bytes(2, nTD), s, a);
-  int wd = 2048 / (bo * G);
-  wd = wd < (nTF + 1) / 2 ? wd : (nTF + 1) / 2;
-  wd = wd < MX_WAVES_D ? (wd < 1 ? 1 : wd) : MX_WAVES_D;
-  hipLaunchKernelGGL(k_d_res_mx, dim3(bo, G), dim3(64 * wd), mx_lds_bytes(1, nTF), s, a);
+  const int wd = mx_waves_d(a);
+  if (fused && a.g1_next) {
+    // D + the next layer's RMSNorm 1 in one launch (batched decode)
+    const size_t shn = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)a.D * 3;
+    const size_t shd = mx_lds_bytes(1, nTF);
+    hipLaunchKernelGGL(k_d_res_norm_mx, dim3(bo * G + a.batch), dim3(64 * wd), shd > shn ? shd : shn, s,
+                       a, bo * G);
+  } else {
+    hipLaunchKernelGGL(k_d_res_mx, dim3(bo, G), dim3(64 * wd), mx_lds_bytes(1, nTF), s, a);
+  }
   return launch_status("layer");
 }
 

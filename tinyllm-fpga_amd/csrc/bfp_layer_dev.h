@@ -181,10 +181,26 @@ __device__ __forceinline__ int residual_lane(int om, int oe, int rm, int re, int
   return quantize16_lanes(s, e);
 }
 
+// Tagged words between the workgroups of one launch: a BFP value with an
+// 8-bit tag (1..255) of the (step, layer) that wrote it, stored and polled
+// with device-scope (SC1) buffer accesses, which bypass the XCD's L2.
+typedef __amdgpu_buffer_rsrc_t tw_rsrc;
+constexpr int TW_SC1 = 16;
+__device__ __forceinline__ tw_rsrc tw_make(const void *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ unsigned tw_tag(int step, int layer, int NL) {
+  return (unsigned)(((long long)step * NL + layer) % 255) + 1u;
+}
+__device__ __forceinline__ unsigned tw_word(int m, int e, unsigned tag) {
+  return ((unsigned)m & 0xffffu) | (((unsigned)e & 0xffu) << 16) | (tag << 24);
+}
+
 // o = Wo attn; h1 = q(h + o)   (full.py:284-285)
 // rm, re: this lane's row of h (the residual), loaded by the caller.
+// tag != 0: h1 also goes to a.t_h1 as a tagged word.
 __device__ __forceinline__ void epi_ores(const LayerArgs &a, int b, int c, long long A, int M,
-                                         bool wr, int rm, int re) {
+                                         bool wr, int rm, int re, unsigned tag = 0) {
   const int r = threadIdx.x & 15;
   int om, oe;
   chunk_quant(A, M, om, oe);
@@ -200,6 +216,9 @@ __device__ __forceinline__ void epi_ores(const LayerArgs &a, int b, int c, long 
   if (wr) {
     a.h1_m[row] = (int16_t)m;
     if (r == 0) a.h1_e[tile] = (int8_t)e;
+    if (tag)
+      __builtin_amdgcn_raw_buffer_store_b32(tw_word(m, e, tag), tw_make(a.t_h1, 0x7fffffff), 4 * row, 0,
+                                            TW_SC1);
     if (a.dump) {
       const StageDump *d = a.dump;
       d->m[ST_O][b * d->mstride[ST_O] + c * 16 + r] = (int16_t)com;
@@ -257,8 +276,9 @@ __device__ __forceinline__ void epi_gu(const LayerArgs &a, int b, int c, long lo
 
 // d = Wd mlp; h_out = q(h1 + d)   (full.py:291-293)
 // rm, re: this lane's row of h1 (the residual), loaded by the caller.
+// tag != 0: h also goes to a.t_h as a tagged word.
 __device__ __forceinline__ void epi_dres(const LayerArgs &a, int b, int c, long long A, int M,
-                                         bool wr, int rm, int re) {
+                                         bool wr, int rm, int re, unsigned tag = 0) {
   const int r = threadIdx.x & 15;
   int dmv, dev;
   chunk_quant(A, M, dmv, dev);
@@ -274,6 +294,9 @@ __device__ __forceinline__ void epi_dres(const LayerArgs &a, int b, int c, long 
   if (wr) {
     a.h_m[row] = (int16_t)m;
     if (r == 0) a.h_e[tile] = (int8_t)e;
+    if (tag)
+      __builtin_amdgcn_raw_buffer_store_b32(tw_word(m, e, tag), tw_make(a.t_h, 0x7fffffff), 4 * row, 0,
+                                            TW_SC1);
     if (a.dump) {
       const StageDump *d = a.dump;
       d->m[ST_D][b * d->mstride[ST_D] + c * 16 + r] = (int16_t)cdm;
