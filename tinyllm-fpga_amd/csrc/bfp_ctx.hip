@@ -58,6 +58,7 @@ struct bfp_ctx {
   double *part_v = nullptr;
   int *part_i = nullptr, *state = nullptr, *last = nullptr;
   unsigned *t_h1 = nullptr, *t_h = nullptr;   // batched decode: h1, h as tagged words (max_batch x D)
+  unsigned *t_qkv = nullptr;   // batched decode: q|k|v as tagged words (max_batch x (D + 2KV))
   int *t_abort = nullptr;    // set by a tagged wait that gave up
   StageDump *dump_dev = nullptr;
   // engine tables of the composed RTL layer, made on its first use
@@ -408,6 +409,7 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->last, sizeof(int) * B)) ||
       (rc = c->alloc((void **)&c->t_h1, sizeof(unsigned) * B * d.D)) ||
       (rc = c->alloc((void **)&c->t_h, sizeof(unsigned) * B * d.D)) ||
+      (rc = c->alloc((void **)&c->t_qkv, sizeof(unsigned) * B * (d.D + 2 * d.H_KV * d.HD))) ||
       (rc = c->alloc((void **)&c->t_abort, sizeof(int))) ||
       (rc = c->alloc((void **)&c->dump_dev, sizeof(StageDump)))) {
     delete c;
@@ -1071,6 +1073,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   // no tagged word of an earlier decode may carry a tag of this one
   HIP_TRY(hipMemsetAsync(c->t_h1, 0, sizeof(unsigned) * batch * d.D, s));
   HIP_TRY(hipMemsetAsync(c->t_h, 0, sizeof(unsigned) * batch * d.D, s));
+  HIP_TRY(hipMemsetAsync(c->t_qkv, 0, sizeof(unsigned) * batch * (d.D + 2 * d.H_KV * d.HD), s));
   HIP_TRY(hipMemsetAsync(c->t_abort, 0, sizeof(int), s));
 
   EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
@@ -1088,6 +1091,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
       a.hist_steps = steps;
       a.t_h1 = c->t_h1;   // tags are unique per (step, layer) within a decode
       a.t_h = c->t_h;
+      a.t_qkv = c->t_qkv;
       a.g1_next = l + 1 < d.NL ? c->g1 + (size_t)(l + 1) * d.D : nullptr;
       a.t_abort = c->t_abort;
       BFP_TRY(launch_layer(a, s));

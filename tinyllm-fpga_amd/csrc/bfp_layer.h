@@ -58,6 +58,9 @@ struct LayerArgs {
   // null; t_abort is set when one of their bounded waits gives up
   unsigned *t_h1, *t_h;
   const double *g1_next;
+  // batched decode: q|k|v also as tagged words (batch x (D + 2KV)), read by
+  // the attention workgroups of the Q|K|V launch (k_qkv_attn_mx), or null
+  unsigned *t_qkv;
   int *t_abort;
 };
 

@@ -369,6 +369,70 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_qkv_mx(LayerArgs a) {
   })
 }
 
+// The attention's q|k|v input from tagged words that the Q|K|V blocks of the
+// same launch store, polled with a bounded wait (tw_give_up); everything
+// else as AttnPlainIO.
+struct AttnTagIO : AttnPlainIO {
+  tw_rsrc rq, rf;   // this sequence's q|k|v words, the abort flag
+  unsigned tag;
+  __device__ __forceinline__ void qkv(int idx, int &m, int &e) const {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    unsigned v;
+    for (unsigned it = 0;; ++it) {
+      v = __builtin_amdgcn_raw_buffer_load_b32(rq, 4 * idx, 0, TW_SC1);
+      if ((v >> 24) == tag || tw_give_up(rf, it, t0)) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    m = (int)(short)(v & 0xffffu);
+    e = (int)(signed char)((v >> 16) & 0xffu);
+  }
+};
+
+// k_qkv_mx's blocks (ids below nblk: chunk id % ((D + 2KV) / 16), sequence
+// group id / that) and a short attention form's k_attn (H_Q x batch
+// workgroups from nblk: head id % H_Q, sequence id / H_Q) in one launch.
+// The blocks also store q|k|v as tagged words, which the attention
+// workgroups poll (AttnTagIO).  Workgroups are dispatched in id order and
+// the blocks never wait, so every block an attention workgroup waits for
+// has been dispatched before it.  blockDim = 64 * ATT_WAVES; the blocks'
+// Ao / Mo sit in the dynamic LDS after their exponents, so the attention
+// keeps k_attn's LDS and occupancy.
+template <int PPW>
+__global__ __launch_bounds__(64 * ATT_WAVES, (PPW == 3 ? 6 : 4)) void k_qkv_attn_mx(LayerArgs a, int nblk) {
+  extern __shared__ double dsm[];
+  const int nq = a.D + 2 * a.KV;
+  const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
+  if ((int)blockIdx.x >= nblk) {
+    const int L = blockIdx.x - nblk, hq = L % a.H_Q, b = L / a.H_Q;
+    AttnTagIO io{{a.qkv_m + b * nq, a.qkv_e + b * (nq / 16), a.att_m + b * a.D, a.att_e + b * (a.D / 16)},
+                 tw_make(a.t_qkv + (long long)b * nq, nq * 4), tw_make(a.t_abort, 4), tag};
+    attn_body<PPW, true>(a, io, hq, b, [&] { return make_int2(cur_kv_pos(a), cur_pos(a)); }, dsm);
+    return;
+  }
+  const int nT = a.D / 16, bq = nq / 16, c = blockIdx.x % bq, b0 = blockIdx.x / bq * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  int8_t *mx_ex = reinterpret_cast<int8_t *>(dsm);
+  long long *Ao = reinterpret_cast<long long *>(mx_ex + mx_lds_bytes(1, nT));   // 32 nT bytes
+  int *Mo = reinterpret_cast<int *>(Ao + 16 * MX_SEQ);
+  mx_block<1>(a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT,
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+  BFP_MX_EPI(MX_SEQ, {
+    const int q_ = r_ * MX_SEQ + j_;
+    (void)cc_;
+    epi_qkv(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, tag);
+  })
+}
+
+typedef void (*qa_fn)(LayerArgs, int);
+static qa_fn qkv_attn_kernel(int ppw) {
+  return ppw == 2 ? k_qkv_attn_mx<2> : (ppw == 3 ? k_qkv_attn_mx<3> : k_qkv_attn_mx<4>);
+}
+inline size_t qkv_attn_lds(const LayerArgs &a) {
+  const size_t sha = attn_lds_bytes(a.max_ctx, attn_ppw(a.max_ctx), AttnPlainIO::kAvBlock);
+  const size_t shq = (size_t)mx_lds_bytes(1, a.D / 16) + 16 * MX_SEQ * 12;
+  return sha > shq ? sha : shq;
+}
+
 // O and residual 1: one chunk per block.
 __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_mx(LayerArgs a) {
   __shared__ long long Ao[16 * MX_SEQ];
@@ -390,9 +454,8 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_mx(LayerArgs a) {
 // norm 1 with gamma g, 2: norm 2) from tagged words that the blocks of the
 // same launch store (words: the sequence's D words): each thread polls whole
 // quads until all four carry this (step, layer)'s tag.  The wait is
-// bounded: after TW_SPIN_TICKS, or once another wait has given up, it sets
-// *t_abort and goes on (the host then reports the decode as failed).
-constexpr unsigned long long TW_SPIN_TICKS = 200000000ull;   // 2 s at 100 MHz
+// bounded (tw_give_up): one that gives up sets *t_abort and goes on (the
+// host then reports the decode as failed).
 __device__ __forceinline__ void norm_tagged(const LayerArgs &a, int b, int which, const unsigned *words,
                                             const double *g, double *dsm) {
   const int D = a.D;
@@ -410,12 +473,7 @@ __device__ __forceinline__ void norm_tagged(const LayerArgs &a, int b, int which
       const v4u u = __builtin_amdgcn_raw_buffer_load_b128(r, 16 * q, 0, TW_SC1);
       v = make_uint4(u.x, u.y, u.z, u.w);
       if ((v.x >> 24) == tag && (v.y >> 24) == tag && (v.z >> 24) == tag && (v.w >> 24) == tag) break;
-      if ((it & 63u) == 63u &&
-          (__builtin_amdgcn_raw_buffer_load_b32(rf, 0, 0, TW_SC1) != 0u ||
-           __builtin_amdgcn_s_memrealtime() - t0 > TW_SPIN_TICKS)) {
-        __builtin_amdgcn_raw_buffer_store_b32(1u, rf, 0, 0, TW_SC1);
-        break;
-      }
+      if (tw_give_up(rf, it, t0)) break;
       __builtin_amdgcn_s_sleep(2);
     }
     hm[4 * q] = (int16_t)(v.x & 0xffffu);
@@ -880,6 +938,12 @@ int prepare_layer_kernels(int max_ctx, int D, int FFN) {
   const int ppw = attn_ppw(max_ctx);
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(attn_kernel(ppw)),
                           (int)attn_lds_bytes(max_ctx, ppw, AttnPlainIO::kAvBlock)));
+  if (ppw <= 4) {
+    LayerArgs la{};
+    la.max_ctx = max_ctx;
+    la.D = D;
+    BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(qkv_attn_kernel(ppw)), (int)qkv_attn_lds(la)));
+  }
   int nw, tpt, nwf, tptf;
   shape_for(D / 16, nw, tpt);
   shape_for(FFN / 16, nwf, tptf);
@@ -938,9 +1002,15 @@ static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
   const int bq = (a.D + 2 * a.KV) / 16, bo = a.D / 16, bg = a.FFN / 16;
   const bool fused = mx_fused_norms(a);
   if (!(fused && a.layer > 0)) launch_norm_seq(a, 1, s);   // else the last layer's D launch ran it
-  hipLaunchKernelGGL(k_qkv_mx, dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
-                     mx_lds_bytes(1, nTD), s, a);
-  BFP_TRY(launch_attn(a, s));
+  if (a.t_qkv && a.t_abort && !a.dump && attn_ppw(a.max_ctx) <= 4 && mx_waves(nTD, bq * G) == ATT_WAVES) {
+    // Q|K|V + attention in one launch (batched decode, short forms)
+    hipLaunchKernelGGL(qkv_attn_kernel(attn_ppw(a.max_ctx)), dim3(bq * G + a.H_Q * a.batch),
+                       dim3(64 * ATT_WAVES), qkv_attn_lds(a), s, a, bq * G);
+  } else {
+    hipLaunchKernelGGL(k_qkv_mx, dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
+                       mx_lds_bytes(1, nTD), s, a);
+    BFP_TRY(launch_attn(a, s));
+  }
   const int wo = mx_waves(nTD, bo * G);
   if (fused) {
     // O + RMSNorm 2 in one launch (batched decode)

@@ -153,15 +153,46 @@ __device__ __forceinline__ void rmsnorm_to_x(const int16_t *__restrict__ hm, con
 // r + 16k holds row r of chunk c of sequence b (b may differ between the
 // four 16-lane groups); only groups with wr set store.
 
+// Tagged words between the workgroups of one launch: a BFP value with an
+// 8-bit tag (1..255) of the (step, layer) that wrote it, stored and polled
+// with device-scope (SC1) buffer accesses, which bypass the XCD's L2.
+typedef __amdgpu_buffer_rsrc_t tw_rsrc;
+constexpr int TW_SC1 = 16;
+__device__ __forceinline__ tw_rsrc tw_make(const void *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ unsigned tw_tag(int step, int layer, int NL) {
+  return (unsigned)(((long long)step * NL + layer) % 255) + 1u;
+}
+__device__ __forceinline__ unsigned tw_word(int m, int e, unsigned tag) {
+  return ((unsigned)m & 0xffffu) | (((unsigned)e & 0xffu) << 16) | (tag << 24);
+}
+// Bounded waits on tagged words: every 64 polls, give up (and set the flag
+// word at rf) once the flag is set or TW_SPIN_TICKS have passed since t0.
+constexpr unsigned long long TW_SPIN_TICKS = 200000000ull;   // 2 s at 100 MHz
+__device__ __forceinline__ bool tw_give_up(tw_rsrc rf, unsigned it, unsigned long long t0) {
+  if ((it & 63u) != 63u) return false;
+  if (__builtin_amdgcn_raw_buffer_load_b32(rf, 0, 0, TW_SC1) != 0u ||
+      __builtin_amdgcn_s_memrealtime() - t0 > TW_SPIN_TICKS) {
+    __builtin_amdgcn_raw_buffer_store_b32(1u, rf, 0, 0, TW_SC1);
+    return true;
+  }
+  return false;
+}
+
 // q|k|v rows: raw BFP out (V dumped here; Q and K post-RoPE by k_attn).
+// tag != 0: the row also goes to a.t_qkv as a tagged word.
 __device__ __forceinline__ void epi_qkv(const LayerArgs &a, int b, int c, long long A, int M,
-                                        bool wr) {
+                                        bool wr, unsigned tag = 0) {
   const int nq = a.D + 2 * a.KV;
   int m, e;
   chunk_quant(A, M, m, e);
   const int lane = threadIdx.x & 15;
   if (wr) a.qkv_m[b * nq + c * 16 + lane] = (int16_t)m;
   if (wr && lane == 0) a.qkv_e[b * (nq / 16) + c] = (int8_t)e;
+  if (wr && tag)
+    __builtin_amdgcn_raw_buffer_store_b32(tw_word(m, e, tag), tw_make(a.t_qkv, 0x7fffffff),
+                                          4 * (b * nq + c * 16 + lane), 0, TW_SC1);
   if (a.dump) {
     // V is not rotated: dump it here (Q and K are dumped post-RoPE by k_attn)
     int cm, ce;
@@ -179,21 +210,6 @@ __device__ __forceinline__ void epi_qkv(const LayerArgs &a, int b, int c, long l
 __device__ __forceinline__ int residual_lane(int om, int oe, int rm, int re, int &e) {
   double s = bfp_val(rm, re) + bfp_val(om, oe);
   return quantize16_lanes(s, e);
-}
-
-// Tagged words between the workgroups of one launch: a BFP value with an
-// 8-bit tag (1..255) of the (step, layer) that wrote it, stored and polled
-// with device-scope (SC1) buffer accesses, which bypass the XCD's L2.
-typedef __amdgpu_buffer_rsrc_t tw_rsrc;
-constexpr int TW_SC1 = 16;
-__device__ __forceinline__ tw_rsrc tw_make(const void *base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
-}
-__device__ __forceinline__ unsigned tw_tag(int step, int layer, int NL) {
-  return (unsigned)(((long long)step * NL + layer) % 255) + 1u;
-}
-__device__ __forceinline__ unsigned tw_word(int m, int e, unsigned tag) {
-  return ((unsigned)m & 0xffffu) | (((unsigned)e & 0xffu) << 16) | (tag << 24);
 }
 
 // o = Wo attn; h1 = q(h + o)   (full.py:284-285)
