@@ -236,6 +236,25 @@ def test_decode_mid_context(gpu, max_ctx):
     gm.close()
 
 
+def test_decode_ragged_batch_joined_launches(gpu):
+    """40 sequences (groups of 16, 16 and 8) on a D=256 model, where the
+    batched decode joins the Q|K|V matvec with the attention and the
+    RMSNorms with the residual matvecs (tagged hand-offs inside a launch):
+    every sequence checked equals its single-sequence decode, and sequence 0
+    the oracle."""
+    cfg = dict(D=256, H_Q=4, H_KV=2, HD=64, FFN=512, NL=2, MAX_CTX=40, VOCAB=512)
+    d, om, gm = _setup(cfg, seed=21, max_batch=40)
+    from bfp import synth
+    prompts = np.stack([synth.make_prompt(d, 6, seed=300 + b) for b in range(40)])
+    toks, _ = gm.decode(prompts, 10)
+    for b in (0, 15, 16, 33, 39):
+        single, _ = gm.decode(prompts[b:b + 1], 10)
+        assert list(single[0]) == list(toks[b]), b
+    want, _, _ = _oracle_decode(om, prompts[0], 10)
+    assert list(toks[0]) == list(want)
+    gm.close()
+
+
 def test_decode_batch64_matches_single(gpu):
     """64 independent sequences in one decode equal their single-sequence
     decodes (and sequence 0 the oracle)."""
