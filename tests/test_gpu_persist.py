@@ -1,4 +1,4 @@
-"""GPU: the persistent batch-1 decode (one cooperative launch, stages
+"""GPU: the persistent batch-1 decode (one launch, stages
 handing over through device-coherent memory) against the per-stage graph
 path and the oracle -- tokens and every layer's output at every step, bit
 for bit, for every attention form (context capacities 32, 200, 300, 600),

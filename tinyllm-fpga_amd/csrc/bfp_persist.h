@@ -57,8 +57,9 @@ inline size_t persist_words(const bfp_dims &d, int grid) {
 // and returns 1 when the persistent kernel covers these dimensions, else 0
 // (the caller then decodes through the per-stage graph).
 int persist_plan(const bfp_dims &d, int max_ctx, int device, PersistArgs &p, int &grid);
-// Cooperative launch of the whole decode on stream s; the argument block is
-// copied to dev_args (device memory, sizeof(PersistArgs)) first.
+// One launch of the whole decode on stream s, one workgroup per compute
+// unit; the argument block is copied to dev_args (device memory,
+// sizeof(PersistArgs)) first.
 int launch_decode_persist(const PersistArgs &p, PersistArgs *dev_args, int grid, int max_ctx,
                           hipStream_t s);
 

@@ -1,6 +1,18 @@
 // Persistent decode kernel: the whole batch-1 greedy decode
-// (rtl/vc707/host/gen_smollm_blockfp_full.py:426-443) as ONE cooperative
-// launch of one workgroup per compute unit.
+// (rtl/vc707/host/gen_smollm_blockfp_full.py:426-443) as ONE launch of one
+// workgroup per compute unit.
+//
+// The workgroups wait on one another, so all of them must be resident at
+// once.  The grid is the compute-unit count and the launch is refused unless
+// the occupancy calculator fits at least one workgroup per compute unit;
+// the library runs nothing else on the device meanwhile (its calls are
+// synchronous), so the dispatcher places every workgroup at once.  This is
+// an ordinary launch, not hipLaunchCooperativeKernel: the kernel uses no
+// grid barrier, and every process that had made a cooperative launch ended
+// in a segmentation fault inside exit() under rocprofv3 (after the
+// profiler's own finalisation), while processes without one exited cleanly.
+// Should a workgroup ever not be placed, the bounded waits below give up
+// and the decode reports BFP_EIO instead of hanging.
 //
 // Why: a decode step is 5 dependent stages per layer x 30 layers + the
 // head.  As separate kernels each stage pays a launch and the reload of its
@@ -806,9 +818,9 @@ int launch_decode_persist(const PersistArgs &p, PersistArgs *dev_args, int grid,
   if (nb < 1) return set_err(BFP_EINVAL, "persistent decode: %zu bytes of LDS do not fit a compute unit", lds);
   HIP_TRY(hipMemcpyAsync(dev_args, &p, sizeof p, hipMemcpyHostToDevice, s));
   HIP_TRY(hipStreamSynchronize(s));   // p is the caller's stack copy
-  void *args[] = {&dev_args};
-  HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(f), dim3(grid), dim3(PT_THREADS), args,
-                                     (unsigned)lds, s));
+  // grid = the compute units (persist_plan) and nb >= 1: every workgroup
+  // is resident at once
+  hipLaunchKernelGGL(f, dim3(grid), dim3(PT_THREADS), lds, s, dev_args);
   return launch_status("persistent decode");
 }
 
