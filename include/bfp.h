@@ -351,7 +351,7 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * prompt token); every step's argmax is recorded, so tokens_out holds
  * batch x (n_prompt + n_gen) tokens (the RTL's result_buf / RTL_TOKENS). */
 #define BFP_DECODE_RTL_LOOP 4
-/* Batch 1 runs the whole decode as one persistent cooperative launch (one
+/* Batch 1 runs the whole decode as one persistent launch (one
  * workgroup per compute unit, stages handing over through device-coherent
  * memory) when the dimensions allow it (D <= 576, FFN <= 1536, NL >= 2, the
  * Q|K|V, O, G/U and D chunks of a layer within the compute units); else, or
@@ -362,6 +362,12 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * input becomes ready and as its output is stored, in the first workgroup of
  * each role, for bfp_decode_trace. */
 #define BFP_DECODE_TRACE 16
+/* Test hook for the bounded waits: the decode's abort word is set after its
+ * per-decode clearing and before its first launch, so every wait for
+ * hand-off words that does not find them at once gives up through its own
+ * bounded loop, the kernels still run to their end, and bfp_decode returns
+ * BFP_EIO.  The next decode clears the word again. */
+#define BFP_DECODE_ABORT_TEST 32
 int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int batch,
                int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags);
 /* How the last bfp_decode ran: BFP_PATH_PERSIST (one persistent launch),
@@ -371,6 +377,20 @@ int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int
 #define BFP_PATH_PERSIST 1
 #define BFP_PATH_EAGER 2
 int bfp_decode_path(const bfp_ctx *ctx);
+/* The launch form of the last bfp_decode's layers (no reference
+ * counterpart; for tests and tuning): BFP_FORM_SINGLE (per-sequence stage
+ * kernels, batches below 4), BFP_FORM_MULTI (multi-sequence kernels on the
+ * vector unit), or BFP_FORM_MX (int8 matrix-core matvecs) with
+ * BFP_FORM_QKV_ATTN when Q|K|V and attention ran as one launch and
+ * BFP_FORM_NORM_FUSED when the RMSNorms ran inside the O and D launches;
+ * BFP_FORM_PERSIST for the persistent batch-1 decode; -1 before any decode. */
+#define BFP_FORM_SINGLE 0
+#define BFP_FORM_MULTI 1
+#define BFP_FORM_MX 2
+#define BFP_FORM_QKV_ATTN 4
+#define BFP_FORM_NORM_FUSED 8
+#define BFP_FORM_PERSIST 16
+int bfp_decode_form(const bfp_ctx *ctx);
 /* The stage trace of the last decode run with BFP_DECODE_TRACE on the
  * persistent path: per (step, layer) 16 stamps -- 0/1 Q|K|V input ready /
  * output stored, 2 (unused), 3 attention output stored, 4/5 O, 6/7 G/U, 8/9 D

@@ -44,11 +44,29 @@ def test_head_argmax_and_logits(gpu):
     q = [sim.tile_quantize(h) for h in hs]
     am, lg = gm.head(np.stack([x[0].reshape(-1) for x in q]), np.stack([x[1] for x in q]),
                      logits=True)
+    same = total = 0
+    worst = 0.0
     for b, h in enumerate(hs):
         want = sim.head_logits(h, om.norm_w_q, om.embed)
-        # float64 logits agree to rounding (BLAS order differs); argmax exactly
-        assert np.allclose(lg[b], want, rtol=1e-13, atol=1e-13)
+        # Both sides sum the same D exact-operand products in different
+        # orders (the kernel's fixed 16-lane tree, numpy's BLAS dgemv), so
+        # each is within gamma_D * sum|h_n,i * E_j,i| of the exact dot
+        # product (Higham, Accuracy and Stability of Numerical Algorithms,
+        # eq. 3.5: gamma_n = n u / (1 - n u), u = 2^-53), and the two within
+        # twice that.  A dropped or doubled term exceeds it by orders of
+        # magnitude.
+        hn = (h / np.sqrt(np.mean(h * h) + 1e-5)) * om.norm_w_q
+        u = 2.0 ** -53
+        gam = d.D * u / (1 - d.D * u)
+        bound = 2 * gam * (np.abs(hn) @ np.abs(om.embed).T)
+        err = np.abs(lg[b] - want)
+        assert (err <= bound).all(), float((err / bound).max())
+        worst = max(worst, float((err / bound).max()))
+        same += int((lg[b] == want).sum())
+        total += want.size
         assert am[b] == int(np.argmax(want))
+    print(f"head logits vs numpy's h_normed @ embed.T: {same}/{total} bit-equal, "
+          f"largest error {worst:.3g} of the bound")
     gm.close()
 
 
@@ -247,6 +265,7 @@ def test_decode_ragged_batch_joined_launches(gpu):
     from bfp import synth
     prompts = np.stack([synth.make_prompt(d, 6, seed=300 + b) for b in range(40)])
     toks, _ = gm.decode(prompts, 10)
+    assert gm.decode_form() == "mx+qkv_attn+norm_fused"
     for b in (0, 15, 16, 33, 39):
         single, _ = gm.decode(prompts[b:b + 1], 10)
         assert list(single[0]) == list(toks[b]), b

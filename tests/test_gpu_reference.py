@@ -164,6 +164,9 @@ def test_config5_decode_on_gpu(gpu):
     gm.load_fp32(synth.make_model(d, seed=int(f["seed"])))
     print(f"[gpu-ref] config 5: decoding {B} sequences x {steps} steps", flush=True)
     toks, (hm, he) = gm.decode(prompts, n_gen, hist=True)
+    # the joined launches ran (Q|K|V with attention, the norms inside the
+    # O and D launches), not the unjoined fallback
+    assert gm.decode_form() == "mx+qkv_attn+norm_fused"
     gm.close()
     for b in range(B):
         got = _digests(hm, he, b, steps, d.NL)

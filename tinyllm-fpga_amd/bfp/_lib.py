@@ -92,6 +92,7 @@ SIGNATURES = {
     "bfp_decode_time": (i32, [vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     "bfp_decode_step_times": (i32, [vp, vp, i32]),
     "bfp_decode_path": (i32, [vp]),
+    "bfp_decode_form": (i32, [vp]),
     "bfp_decode_trace": (i32, [vp, vp, sz]),
     "bfp_vocab_open": (i32, [C.c_char_p, C.POINTER(vp)]),
     "bfp_vocab_parse": (i32, [vp, sz, C.POINTER(vp)]),

@@ -247,7 +247,7 @@ class BfpModel:
 
     # --------------------------------------------------------------- decode
     def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False, rtl_loop=False,
-               persist=True, trace=False):
+               persist=True, trace=False, abort_test=False):
         """Greedy decode (full.py:426-443) of a batch of prompts
         (batch, n_prompt).  Returns (tokens (batch, n_gen), hist) where hist
         is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16)).
@@ -259,7 +259,11 @@ class BfpModel:
 
         persist=False keeps batch 1 off the persistent single-launch kernel
         (decode_path() tells which path the last decode took); trace=True
-        records its stage stamps (decode_trace())."""
+        records its stage stamps (decode_trace()).
+
+        abort_test=True is a test hook: the decode's abort word is set before
+        its first launch, so its bounded waits give up, the kernels run to
+        their end and the call raises BfpError (BFP_EIO)."""
         P = np.ascontiguousarray(np.atleast_2d(np.asarray(prompts, dtype=np.int32)))
         batch, n_prompt = P.shape
         steps = n_prompt + n_gen
@@ -271,7 +275,7 @@ class BfpModel:
             hm = np.zeros((batch, steps, d.NL, d.D), np.int16)
             he = np.zeros((batch, steps, d.NL, d.D // 16), np.int8)
         flags = ((0 if graph else 1) | (2 if step_times else 0) | (4 if rtl_loop else 0)
-                 | (0 if persist else 8) | (16 if trace else 0))
+                 | (0 if persist else 8) | (16 if trace else 0) | (32 if abort_test else 0))
         call("bfp_decode", self._h, _p(P), n_prompt, n_gen, batch, _p(toks),
              _p(hm) if hist else None, _p(he) if hist else None, flags)
         return toks[:, :n_out], ((hm, he) if hist else None)
@@ -287,6 +291,19 @@ class BfpModel:
     def decode_path(self):
         """'persist', 'graph' or 'eager': how the last decode ran."""
         return {0: "graph", 1: "persist", 2: "eager"}.get(lib().bfp_decode_path(self._h), None)
+
+    def decode_form(self):
+        """How the last decode's layers were launched: 'persist', 'single',
+        'multi', or 'mx' followed by '+qkv_attn' (Q|K|V and attention in one
+        launch) and '+norm_fused' (RMSNorms inside the O and D launches)."""
+        f = lib().bfp_decode_form(self._h)
+        if f < 0:
+            return None
+        if f == 16:
+            return "persist"
+        if f < 2:
+            return ("single", "multi")[f]
+        return "mx" + ("+qkv_attn" if f & 4 else "") + ("+norm_fused" if f & 8 else "")
 
     def decode_trace(self):
         """Stage stamps (device clock, 100 MHz) of the last decode(trace=True)

@@ -80,6 +80,7 @@ struct bfp_ctx {
   double *pt_scores = nullptr;   // the long attention form's score exchange
   std::vector<void *> allocs;
   int last_path = -1;   // BFP_PATH_* of the last decode
+  int last_form = -1;   // BFP_FORM_* of the last decode
   float last_decode_ms = 0.f, last_gen_ms = 0.f;
   std::vector<float> step_ms;   // per-step device time of the last decode (BFP_DECODE_STEP_TIMES)
   std::vector<unsigned long long> trace;   // stage stamps of the last traced persistent decode
@@ -217,7 +218,8 @@ bool persist_enabled() {
 
 // The whole batch-1 decode as one persistent launch (bfp_persist.hip).
 int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int n_prompt,
-                   int n_gen, int *dout, int16_t *dhm, int8_t *dhe, bool rtl_loop, bool trace) {
+                   int n_gen, int *dout, int16_t *dhm, int8_t *dhe, bool rtl_loop, bool trace,
+                   bool abort_test) {
   const bfp_dims &d = c->d;
   hipStream_t s = c->stream;
   const int steps = n_prompt + n_gen;
@@ -268,6 +270,7 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
   pa.hist_steps = dhm ? steps : 0;
   pa.trace = dtrace;
   HIP_TRY(hipMemsetAsync(c->pt_words, 0, c->pt_nwords * 4, s));
+  if (abort_test) HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)pa.abort_flag, 1, 1, s));
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   HIP_TRY(hipEventCreate(&ev0));
   HIP_TRY(hipEventCreate(&ev1));
@@ -299,6 +302,7 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
     c->step_ms.resize(steps);
     for (int k = 0; k < steps; ++k) c->step_ms[k] = (float)((double)(clk[k + 1] - clk[k]) * tick_ms);
     c->last_path = BFP_PATH_PERSIST;
+    c->last_form = BFP_FORM_PERSIST;
     if (dtrace) {
       c->trace.resize(ntrace);
       hipError_t e = hipMemcpy(c->trace.data(), dtrace, ntrace * sizeof(unsigned long long),
@@ -1066,7 +1070,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   if (batch == 1 && !(flags & (BFP_DECODE_NO_GRAPH | BFP_DECODE_NO_PERSIST)) && persist_enabled() &&
       persist_plan(d, c->max_ctx, c->device, pa, grid)) {
     BFP_TRY(decode_persist(c, pa, grid, dprompt, n_prompt, n_gen, dout, dhm, dhe, rtl_loop,
-                           (flags & BFP_DECODE_TRACE) != 0));
+                           (flags & BFP_DECODE_TRACE) != 0, (flags & BFP_DECODE_ABORT_TEST) != 0));
     return decode_copy_out(c, batch, steps, n_out, dout, tokens_out, dhm, dhe, hist_m, hist_e);
   }
   c->last_path = (flags & BFP_DECODE_NO_GRAPH) ? BFP_PATH_EAGER : BFP_PATH_GRAPH;
@@ -1075,6 +1079,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   HIP_TRY(hipMemsetAsync(c->t_h, 0, sizeof(unsigned) * batch * d.D, s));
   HIP_TRY(hipMemsetAsync(c->t_qkv, 0, sizeof(unsigned) * batch * (d.D + 2 * d.H_KV * d.HD), s));
   HIP_TRY(hipMemsetAsync(c->t_abort, 0, sizeof(int), s));
+  if (flags & BFP_DECODE_ABORT_TEST) HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)c->t_abort, 1, 1, s));
 
   EmbedArgs ea{d.D, batch, d.VOCAB, c->embed, c->state, c->h_m, c->h_e};
   HeadArgs ha = head_args(c, batch, nullptr);
@@ -1094,6 +1099,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
       a.t_qkv = c->t_qkv;
       a.g1_next = l + 1 < d.NL ? c->g1 + (size_t)(l + 1) * d.D : nullptr;
       a.t_abort = c->t_abort;
+      c->last_form = layer_form(a);
       BFP_TRY(launch_layer(a, s));
     }
     CtlArgs cc = ca;
@@ -1182,6 +1188,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
 }
 
 int bfp_decode_path(const bfp_ctx *c) { return c ? c->last_path : -1; }
+int bfp_decode_form(const bfp_ctx *c) { return c ? c->last_form : -1; }
 
 int bfp_decode_trace(const bfp_ctx *c, uint64_t *out, size_t n) {
   if (!c || (!out && n > 0)) return set_err(BFP_EINVAL, "null argument");

@@ -71,6 +71,8 @@ struct HeadArgs;
 struct CtlArgs;
 struct EmbedArgs;
 int launch_layer(const LayerArgs &a, hipStream_t s);
+// The launch form launch_layer takes for a (BFP_FORM_* bits).
+int layer_form(const LayerArgs &a);
 int prepare_layer_kernels(int max_ctx, int D, int FFN);
 int prepare_head_kernels(int D);
 // Raise a kernel's dynamic-LDS limit on the current device to at least

@@ -996,13 +996,29 @@ static bool mx_fused_norms(const LayerArgs &a) {
          128 * mx_waves_d(a) >= a.D;
 }
 
+// Q|K|V and a short attention form in one launch (k_qkv_attn_mx): when the
+// tagged q|k|v buffer is given, no stage dump is asked for, and the Q|K|V
+// blocks run with the attention's wave count.
+static bool mx_joined_qkv_attn(const LayerArgs &a) {
+  const int G = (a.batch + MX_SEQ - 1) / MX_SEQ, bq = (a.D + 2 * a.KV) / 16;
+  return a.t_qkv && a.t_abort && !a.dump && attn_ppw(a.max_ctx) <= 4 &&
+         mx_waves(a.D / 16, bq * G) == ATT_WAVES;
+}
+
+int layer_form(const LayerArgs &a) {
+  if (!(a.batch >= MULTI_MIN_BATCH && a.xn_m)) return BFP_FORM_SINGLE;
+  if (a.batch < MX_MIN_BATCH) return BFP_FORM_MULTI;
+  return BFP_FORM_MX | (mx_joined_qkv_attn(a) ? BFP_FORM_QKV_ATTN : 0) |
+         (mx_fused_norms(a) ? BFP_FORM_NORM_FUSED : 0);
+}
+
 static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   const int G = (a.batch + MX_SEQ - 1) / MX_SEQ;
   const int bq = (a.D + 2 * a.KV) / 16, bo = a.D / 16, bg = a.FFN / 16;
   const bool fused = mx_fused_norms(a);
   if (!(fused && a.layer > 0)) launch_norm_seq(a, 1, s);   // else the last layer's D launch ran it
-  if (a.t_qkv && a.t_abort && !a.dump && attn_ppw(a.max_ctx) <= 4 && mx_waves(nTD, bq * G) == ATT_WAVES) {
+  if (mx_joined_qkv_attn(a)) {
     // Q|K|V + attention in one launch (batched decode, short forms)
     hipLaunchKernelGGL(qkv_attn_kernel(attn_ppw(a.max_ctx)), dim3(bq * G + a.H_Q * a.batch),
                        dim3(64 * ATT_WAVES), qkv_attn_lds(a), s, a, bq * G);
