@@ -90,6 +90,28 @@ def cpu_info():
     return {"model": model, "nproc": nproc, "cpu_count": os.cpu_count()}
 
 
+def numpy_runtime():
+    """numpy's version, the BLAS core its OpenBLAS picked on this host (the
+    ddot/dgemv kernels behind full.py:278,439) and whether its AVX512F
+    loops (np.exp's SIMD form, full.py:242,246) are dispatched."""
+    import numpy as np
+    out = {"numpy": np.__version__}
+    try:
+        import threadpoolctl
+        blas = [b for b in threadpoolctl.threadpool_info() if b.get("user_api") == "blas"]
+        if blas:
+            out["blas"] = "%s %s %s" % (blas[0].get("internal_api"), blas[0].get("version"),
+                                        blas[0].get("architecture"))
+    except Exception as e:   # noqa: BLE001 - informational only
+        out["blas"] = f"unknown ({type(e).__name__})"
+    try:
+        from numpy._core import _multiarray_umath as mu
+        out["avx512f"] = bool(mu.__cpu_features__.get("AVX512F"))
+    except Exception:   # noqa: BLE001
+        out["avx512f"] = None
+    return out
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,7 +302,7 @@ def cpu_baseline(seconds):
     os.environ.setdefault("OPENBLAS_NUM_THREADS", "1")
     total_b, total_t, done = _cpu_matvec_sample(seconds)
     return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port", "cpu": cpu_info(),
+            "kind": "port",
             "sample": "oracle/bfp_sim.matvec_hw_golden (numpy, 1 thread), reps per shape "
                       + ", ".join(done) + f" in {total_t:.1f} s"}
 
@@ -304,7 +326,6 @@ def cpu_baseline_all_cores(seconds, workers):
     total_b = sum(r["bytes"] for r in res)
     t = max(r["seconds"] for r in res)
     return {"value": round(total_b / t / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
-            "cpu": cpu_info(),
             "sample": f"{workers} concurrent single-threaded processes, each the 1-thread sample "
                       f"({seconds:.0f} s budget), slowest {t:.1f} s"}
 
@@ -605,7 +626,7 @@ def cpu_decode_baselines():
         blas = threads if blas is None else blas
         return {"value": round(value, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
                 "variant": "line-faithful" if kind == "port" else "vectorised",
-                "sample": f"{name[kind]}, OPENBLAS_NUM_THREADS={blas}: {sample}", "cpu": info}
+                "sample": f"{name[kind]}, OPENBLAS_NUM_THREADS={blas}: {sample}"}
 
     out = {"decode": {}, "long_context": {}, "batch64": {}, "layer": {}}
     for (kind, thr), r in runs.items():
@@ -798,6 +819,7 @@ def main():
             achieved / out["stream_ceiling"]["read_ceiling_GB_s"], 4)
     if not args.no_cpu:
         print("[bench] CPU baselines", file=sys.stderr, flush=True)
+        out["cpu"] = dict(cpu_info(), **numpy_runtime())
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         workers = args.cpu_workers or min(cpu_info()["nproc"], 16)
         out["cpu_baseline_all_cores"] = cpu_baseline_all_cores(8.0, workers)
@@ -808,7 +830,34 @@ def main():
                 if leg in out:
                     out[leg]["cpu_baseline"] = cb[key]["faithful_1t"]
                     out[leg]["cpu_baselines"] = cb[key]
-    print(json.dumps(out), flush=True)
+    # the full record (every baseline's sample text) goes to stderr; the
+    # JSON line on stdout keeps every figure in a few KB
+    print("[bench] detail " + json.dumps(out), file=sys.stderr, flush=True)
+    print(json.dumps(compact(out)), flush=True)
+
+
+def compact(out):
+    """The stdout record: the same figures without the long texts --
+    rooflines without their basis text, each leg's alternative CPU
+    baselines as bare values."""
+    def roof(r):
+        return {k: v for k, v in r.items() if k != "basis"}
+
+    res = {}
+    for k, v in out.items():
+        if not isinstance(v, dict) or k in ("config", "roofline", "cpu_baseline", "cpu"):
+            res[k] = v
+            continue
+        leg = {}
+        for kk, vv in v.items():
+            if kk.startswith("roofline"):
+                leg[kk] = roof(vv)
+            elif kk == "cpu_baselines":
+                leg[kk] = {n: b["value"] for n, b in vv.items()}
+            else:
+                leg[kk] = vv
+        res[k] = leg
+    return res
 
 
 if __name__ == "__main__":
