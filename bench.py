@@ -151,6 +151,9 @@ def parse():
     ap.add_argument("--decode-trace", action="store_true",
                     help="with --decode-only: also run config 3 once with the persistent "
                          "kernel's stage stamps and report the per-stage times")
+    ap.add_argument("--decode-trace-long", action="store_true",
+                    help="with --decode-only: the same stage stamps for config 4 (the long "
+                         "attention form), medians over positions 1984-2047")
     return ap.parse_args()
 
 
@@ -381,16 +384,22 @@ def decode_leg(reps, n_gen=64):
 # Stage stamps of the persistent batch-1 decode (csrc/bfp_persist.hip:
 # stamp k of (step, layer), taken by thread 0 of each role's first workgroup
 # on the 100 MHz device clock): Q|K|V 0 (h in), 10 (RMSNorm done), 11
-# (matvec done), 1 (q|k|v stored), 3 (attention job 0 done); O 4 (attention
-# output in), 15, 5; G/U 6 (h1 in), 12, 13, 7; D 8 (mlp in), 14, 9 (h
-# stored).  Head stamps per step: 0 (start), 1 (vocabulary slices done),
-# 2 (token chosen).
+# (matvec done), 1 (q|k|v stored), 3 (attention job 0 done) with the job's
+# phases 16 (q|k|v in, RoPE done), 17 (scores), 18 (softmax), 19 (AV
+# chains); O 4 (attention output in), 15, 5; G/U 6 (h1 in), 12, 13, 7; D 8
+# (mlp in), 14, 9 (h stored).  Head stamps per step: 0 (start), 1
+# (vocabulary slices done), 2 (token chosen).
 TRACE_INTERVALS = [
     ("h in -> Q|K|V start (hand-off)", (-1, 9), (0, 0)),
     ("Q|K|V RMSNorm", (0, 0), (0, 10)),
     ("Q|K|V matvec", (0, 10), (0, 11)),
     ("Q|K|V epilogue + store", (0, 11), (0, 1)),
     ("attention (incl. q|k|v hand-off)", (0, 1), (0, 3)),
+    ("  attention: q|k|v hand-off + RoPE + cache row", (0, 1), (0, 16)),
+    ("  attention: scores", (0, 16), (0, 17)),
+    ("  attention: softmax", (0, 17), (0, 18)),
+    ("  attention: AV chains", (0, 18), (0, 19)),
+    ("  attention: quantise + store", (0, 19), (0, 3)),
     ("attention -> O start (hand-off)", (0, 3), (0, 4)),
     ("O matvec", (0, 4), (0, 15)),
     ("O epilogue + store", (0, 15), (0, 5)),
@@ -405,19 +414,20 @@ TRACE_INTERVALS = [
 ]
 
 
-def decode_trace_leg():
-    """Config 3 once on the persistent path with stage stamps: the median
-    over generated steps and layers 1..NL-1 of each stage interval (us),
-    and of the head's."""
+def decode_trace_leg(long=False):
+    """Config 3 (or config 4 with long=True) once on the persistent path
+    with stage stamps: the median over generated steps (config 4: positions
+    1984-2047) and layers 1..NL-1 of each stage interval (us), and of the
+    head's."""
     import numpy as np
     from bfp import Dims, synth
     from bfp.model import BfpModel
-    n_prompt, n_gen = 8, 64
+    n_prompt, n_gen, seed = (48, 2000, 4) if long else (8, 64, 0)
     d = Dims(MAX_CTX=n_prompt + n_gen)
     gm = BfpModel(d)
     gm.load_fp32(synth.make_model(d, seed=0))
-    prompt = synth.make_prompt(d, n_prompt, seed=0)
-    gm.decode(prompt[None, :], n_gen)
+    prompt = synth.make_prompt(d, n_prompt, seed=seed)
+    gm.decode(prompt[None, :], 16 if long else n_gen)
     gm.decode(prompt[None, :], n_gen, trace=True)
     path = gm.decode_path()
     tr = gm.decode_trace()
@@ -427,7 +437,7 @@ def decode_trace_leg():
     lay, head = tr
     lay = lay.astype(np.int64)
     head = head.astype(np.int64)
-    steps = range(n_prompt, n_prompt + n_gen)
+    steps = range(1984, 2048) if long else range(n_prompt, n_prompt + n_gen)
     out = {}
     for name, (dl0, k0), (dl1, k1) in TRACE_INTERVALS:
         v = [(lay[s, l + dl1, k1] - lay[s, l + dl0, k0]) / 100.0
@@ -443,8 +453,7 @@ def decode_trace_leg():
         [(lay[s + 1, 0, 0] - head[s, 2]) / 100.0 for s in list(steps)[:-1]])), 2)
     out["step"] = round(float(np.median(
         [(lay[s + 1, 0, 0] - lay[s, 0, 0]) / 100.0 for s in list(steps)[:-1]])), 2)
-    return {"path": path, "steps": f"{n_prompt}..{n_prompt + n_gen - 1}",
-            "stages_us": out}
+    return {"path": path, "steps": f"{steps[0]}..{steps[-1]}", "stages_us": out}
 
 
 def long_context_leg():
@@ -737,6 +746,9 @@ def main():
         if args.decode_trace:
             note("config 3 persistent-decode stage trace")
             res["decode_trace"] = decode_trace_leg()
+        if args.decode_trace_long:
+            note("config 4 persistent-decode stage trace (positions 1984-2047)")
+            res["decode_trace_long"] = decode_trace_leg(long=True)
         print(json.dumps(res), flush=True)
         return
     print(f"[bench] building device rings for {len(SHAPES)} shapes x {args.reps} reps",

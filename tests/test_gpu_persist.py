@@ -129,3 +129,33 @@ def test_persist_step_times(gpu):
     assert st.shape == (12,) and (st > 0).all()
     assert 0 < gen <= total and abs(st[4:].sum() - gen) < 1e-3 * max(gen, 1.0) + 1e-3
     gm.close()
+
+
+@pytest.mark.parametrize("max_ctx", [40, 600], ids=["short", "long-form"])
+def test_persist_trace(gpu, max_ctx):
+    """A traced decode (stage stamps, BFP_DECODE_TRACE) gives the untraced
+    tokens and layer outputs, and the Q|K|V role's stamps follow its own
+    order at every (step, layer): input ready, RMSNorm, matvec, q|k|v
+    stored, then attention job 0's phases (q|k|v in and RoPE, scores,
+    softmax, AV chains) and its output stored; the head's three stamps are
+    ordered at every step that ran it."""
+    cfg = dict(D=576, H_Q=9, H_KV=3, HD=64, FFN=1536, NL=2, MAX_CTX=max_ctx, VOCAB=1024)
+    d, fm, gm = _setup(cfg, seed=27)
+    from bfp import synth
+    prompt = synth.make_prompt(d, 8, seed=27)
+    n_gen = 24
+    want = gm.decode(prompt[None, :], n_gen, hist=True)
+    got = gm.decode(prompt[None, :], n_gen, hist=True, trace=True)
+    assert gm.decode_path() == "persist"
+    _same(got, want)
+    lay, head = gm.decode_trace()
+    steps = 8 + n_gen
+    assert lay.shape == (steps, d.NL, 20) and head.shape == (steps, 3)
+    order = [0, 10, 11, 1, 16, 17, 18, 19, 3]
+    for s in range(steps):
+        for li in range(d.NL):
+            v = lay[s, li, order].astype(np.int64)
+            assert (v > 0).all() and (np.diff(v) >= 0).all(), (s, li, v)
+        if s >= 7:   # sim A's loop runs the head from step n_prompt - 1 on
+            assert (head[s] > 0).all() and (np.diff(head[s].astype(np.int64)) >= 0).all(), s
+    gm.close()

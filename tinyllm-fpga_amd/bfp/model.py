@@ -16,6 +16,7 @@ from ._lib import BfpError, DimsC, N_STAGES, StageDumpC, call, lib
 from .dims import Dims
 
 STAGES = ("N1", "Q", "K", "V", "ATTN", "O", "H1", "N2", "G", "U", "MLP", "D", "HOUT")
+TRACE_LAYER = 20   # stage-trace stamps per (step, layer), bfp_decode_trace
 WHICH = {"Wq": 0, "Wk": 1, "Wv": 2, "Wo": 3, "Wg": 4, "Wu": 5, "Wd": 6, "g1": 7, "g2": 8,
          "embed": 9, "norm_w": 10}
 
@@ -307,16 +308,17 @@ class BfpModel:
 
     def decode_trace(self):
         """Stage stamps (device clock, 100 MHz) of the last decode(trace=True)
-        on the persistent path: (layer stamps (steps, NL, 16), head stamps
-        (steps, 3)), or None."""
+        on the persistent path: (layer stamps (steps, NL, 20), head stamps
+        (steps, 3)), or None.  Layer stamps 0-15 are the stages', 16-19 the
+        first attention job's phases (include/bfp.h, bfp_decode_trace)."""
         n = lib().bfp_decode_trace(self._h, None, 0)
         if n <= 0:
             return None
         out = np.zeros(n, np.uint64)
         lib().bfp_decode_trace(self._h, _p(out), n)
-        nl = self.dims.NL
-        steps = n // (nl * 16 + 3)
-        return out[:steps * nl * 16].reshape(steps, nl, 16), out[steps * nl * 16:].reshape(steps, 3)
+        nl, k = self.dims.NL, TRACE_LAYER
+        steps = n // (nl * k + 3)
+        return out[:steps * nl * k].reshape(steps, nl, k), out[steps * nl * k:].reshape(steps, 3)
 
     def decode_time_ms(self):
         t, g = C.c_float(), C.c_float()

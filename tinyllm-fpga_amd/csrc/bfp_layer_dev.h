@@ -367,7 +367,15 @@ struct AttnPlainIO {
     om[idx] = (int16_t)m;
     if (we) oe[idx >> 4] = (int8_t)e;
   }
+  // phase stamps of a traced decode (ATT_MARK_*); none on this path
+  __device__ __forceinline__ void mark(int) const {}
 };
+
+// The attention's phase stamps (IO::mark), in the order they are taken.
+constexpr int ATT_MARK_ROPE = 0;      // q|k|v in, RoPE done, the cache row stored
+constexpr int ATT_MARK_SCORES = 1;    // every score in LDS (after the long form's exchange)
+constexpr int ATT_MARK_SOFTMAX = 2;   // probabilities in LDS
+constexpr int ATT_MARK_AV = 3;        // the AV chains done
 
 // Attention of one q head (full.py:268-283) in workgroups of ATT_WAVES
 // waves:
@@ -619,6 +627,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     }
   }
   lds_barrier();
+  io.mark(ATT_MARK_ROPE);
 
   if constexpr (SHORT) BFP_ATT_LOAD_V(0)   // in flight during the scores
   // scores[t] = float(np.dot(q, K[t])) / sqrt(HD)   (full.py:277-278), one
@@ -699,6 +708,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     for (int d = 0; d < AVL_DEPTH; ++d) load_blk(d, rm[d], re[d]);   // overlaps the softmax
   }
   lds_barrier();
+  io.mark(ATT_MARK_SCORES);
   // softmax_fp (full.py:245-247): e = exp(s - max); p = e / pairwise_sum(e)
   if (SHORT && n <= 128) {
     // wave 0 alone (only it reads p in the short forms' AV chain): lane l
@@ -768,6 +778,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     lds_barrier();
   }
 
+  io.mark(ATT_MARK_SOFTMAX);
   double acc = 0.0;
   if constexpr (SHORT) {
     // attn_h = sum_t p[t] * V[t], ascending t from 0.0 (full.py:280-281):
@@ -917,6 +928,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   }
 #undef BFP_ATT_LOAD_V
 #undef BFP_ATT_STORE_V
+  io.mark(ATT_MARK_AV);
   io.before_out();   // the cache row stored above is visible before the output is
   if (w == 0) {
     // lanes 0-15 of the long form hold its tile; all 64 lanes take part

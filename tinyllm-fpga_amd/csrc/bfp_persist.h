@@ -35,12 +35,15 @@ struct PersistArgs {
   // each role: per (step, layer) PT_TRACE_LAYER stamps -- 0/1 Q|K|V input
   // ready / output stored, 3 attention output stored, 4/5 O, 6/7 G/U, 8/9 D
   // ready / stored, 10/11 Q|K|V norm / matvec done, 12/13 G/U norm / matvecs
-  // done, 14 D matvec done, 15 O matvec done -- then per step PT_TRACE_STEP
-  // stamps of the head (h ready, slice argmax stored, token known)
+  // done, 14 D matvec done, 15 O matvec done, and attention job 0's phases
+  // 16 RoPE (and its q|k|v input) done, 17 scores, 18 softmax, 19 AV chains
+  // done -- then per step PT_TRACE_STEP stamps of the head (h ready, slice
+  // argmax stored, token known)
   unsigned long long *trace;
 };
 constexpr int PT_SFLAGS_PER_HEAD = 4;   // the long attention form's workgroups per head
-constexpr int PT_TRACE_LAYER = 16;
+constexpr int PT_TRACE_LAYER = 20;
+constexpr int PT_TRACE_ATT = 16;        // first attention phase stamp (ATT_MARK_* follow)
 constexpr int PT_TRACE_STEP = 3;
 inline size_t persist_trace_len(int steps, int NL) {
   return (size_t)steps * NL * PT_TRACE_LAYER + (size_t)steps * PT_TRACE_STEP;

@@ -301,6 +301,10 @@ struct AttnCohIO {
   rsrc_t rkm, rke, rvm, rve;      // this layer's KV cache
   const int16_t *km0, *vm0;
   const int8_t *ke0, *ve0;
+  unsigned long long *trace;      // traced decode, first attention job: stamps at trace[k]
+  __device__ __forceinline__ void mark(int k) const {
+    if (trace && threadIdx.x == 0) put_clock(trace, PT_TRACE_ATT + k);
+  }
   __device__ __forceinline__ void qkv(int idx, int &m, int &e) const {
     const unsigned v = w->word(rq, 4 * idx, tag);
     m = tw_m(v);
@@ -565,6 +569,7 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
         io.rsc = rsrc(p.sc_buf);
         io.rfl = rsrc(p.t_sflag);
         io.sc_stride = a.max_ctx;
+        io.trace = (p.trace && c == 0) ? p.trace + ((size_t)s * p.NL + l) * PT_TRACE_LAYER : nullptr;
         attn_body<PPW, SHORT>(a, io, c, 0, [s] { return make_int2(s, s); }, dsm);
         stamp(p, c == 0, s, l, 3);
       }
