@@ -151,6 +151,11 @@ __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 __device__ __forceinline__ int ld_nt(const int8_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float4 ld_nt(const float4 *p) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
+  return make_float4(t.x, t.y, t.z, t.w);
+}
 
 template <int M>
 __device__ __forceinline__ int peer_u32(int v) {

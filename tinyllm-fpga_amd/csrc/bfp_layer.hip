@@ -603,7 +603,7 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
     rr = rr < a.rows_per_wg ? rr : rr - 16;
     const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)(r0 + rr) * a.D);
 #pragma unroll
-    for (int i = 0; i < MAXD64; ++i) f[i] = e4[(EXACT || i < d64 ? i : d64 - 1) * 16 + l16];
+    for (int i = 0; i < MAXD64; ++i) f[i] = ld_nt(e4 + (EXACT || i < d64 ? i : d64 - 1) * 16 + l16);
   };
   load_rows(sub, cur);
   final_norm(a.h_m + b * a.D, a.h_e + b * (a.D / 16), a.norm_w, a.D, dsm, leaf, hn);
@@ -685,7 +685,7 @@ __global__ __launch_bounds__(256) void k_head_gemv(HeadArgs a, int sg) {
     const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)row * a.D);
 #pragma unroll
     for (int i = 0; i < MAXD64; ++i) {
-      float4 f = e4[(EXACT || i < d64 ? i : d64 - 1) * 16 + l16];   // unconditional load
+      float4 f = ld_nt(e4 + (EXACT || i < d64 ? i : d64 - 1) * 16 + l16);   // unconditional load
       if (!EXACT && i >= d64) f = make_float4(0.f, 0.f, 0.f, 0.f);
       eD[r][4 * i] = (double)f.x;
       eD[r][4 * i + 1] = (double)f.y;
@@ -1174,7 +1174,7 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
     const float4 *src = reinterpret_cast<const float4 *>(a.embedp + (long long)(row_lo + 16 * t) * D);
     auto ld = [&](int k) {
       const int q = k * 512 + tid;
-      return src[q < TQ ? q : TQ - 1];
+      return ld_nt(src + (q < TQ ? q : TQ - 1));
     };
     st.v0 = ld(0);
     if constexpr (KQ > 1) st.v1 = ld(1);
