@@ -151,6 +151,9 @@ def parse():
     ap.add_argument("--decode-trace", action="store_true",
                     help="with --decode-only: also run config 3 once with the persistent "
                          "kernel's stage stamps and report the per-stage times")
+    ap.add_argument("--decode-trace-batch", action="store_true",
+                    help="with --decode-only: config 5 once with the matrix-core blocks' phase "
+                         "stamps (the last layer of the last step) and report their medians")
     ap.add_argument("--decode-trace-long", action="store_true",
                     help="with --decode-only: the same stage stamps for config 4 (the long "
                          "attention form), medians over positions 1984-2047")
@@ -456,6 +459,46 @@ def decode_trace_leg(long=False):
     return {"path": path, "steps": f"{steps[0]}..{steps[-1]}", "stages_us": out}
 
 
+MX_PHASES = ("staging (exponents)", "pass 1 (row maxima)", "pass 2 (tile sums)",
+             "A reduction", "epilogue (wave 0)")
+
+
+def batch_trace_leg():
+    """Config 5 once with the matrix-core matvec blocks' phase stamps (the
+    last launch of each kernel: the last layer of the last step): per kernel
+    the blocks stamped, the spread of their start times, the span from the
+    first start to the last epilogue, and the median of each phase (us)."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    B, n_prompt, n_gen = 64, 8, 128
+    d = Dims(MAX_CTX=n_prompt + n_gen)
+    gm = BfpModel(d, max_batch=B)
+    gm.load_fp32(synth.make_model(d, seed=0))
+    prompts = np.stack([synth.make_prompt(d, n_prompt, seed=0)] +
+                       [synth.make_prompt(d, n_prompt, seed=1000 + b) for b in range(1, B)])
+    gm.decode(prompts, 4)
+    gm.decode(prompts, n_gen, trace=True)
+    form = gm.decode_form()
+    tr = gm.decode_trace()
+    gm.close()
+    if tr is None:
+        return {"form": form, "kernels": None}
+    tr = tr.astype(np.int64)
+    out = {}
+    for k, name in enumerate(("Q|K|V", "O", "G/U", "D")):
+        st = tr[k][tr[k][:, 0] > 0]
+        if not len(st):
+            continue
+        t0 = st[:, 0].min()
+        r = {"blocks": int(len(st)), "start_spread_us": round(float((st[:, 0].max() - t0) / 100), 2),
+             "span_us": round(float((st[:, 5].max() - t0) / 100), 2)}
+        for j, ph in enumerate(MX_PHASES):
+            r[ph] = round(float(np.median((st[:, j + 1] - st[:, j]) / 100)), 2)
+        out[name] = r
+    return {"form": form, "step": f"{n_prompt + n_gen - 1} (last layer)", "kernels_us": out}
+
+
 def long_context_leg():
     """30 layers, 48-token prompt, greedy decode through
     position 2047 (2000 new tokens); tokens/s overall and per position
@@ -746,6 +789,9 @@ def main():
         if args.decode_trace:
             note("config 3 persistent-decode stage trace")
             res["decode_trace"] = decode_trace_leg()
+        if args.decode_trace_batch:
+            note("config 5 matrix-core block phase trace")
+            res["decode_trace_batch"] = batch_trace_leg()
         if args.decode_trace_long:
             note("config 4 persistent-decode stage trace (positions 1984-2047)")
             res["decode_trace_long"] = decode_trace_leg(long=True)

@@ -358,9 +358,10 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * with this flag or the environment variable BFP_PERSIST=0, each step is a
  * replayed graph of per-stage kernels.  Both give identical outputs. */
 #define BFP_DECODE_NO_PERSIST 8
-/* Persistent path only: record the device clock (100 MHz) as each stage's
- * input becomes ready and as its output is stored, in the first workgroup of
- * each role, for bfp_decode_trace. */
+/* Record the device clock (100 MHz) for bfp_decode_trace: on the persistent
+ * path as each stage's input becomes ready and as its output is stored, in
+ * the first workgroup of each role; on the batched matrix-core path at the
+ * phases of every block of the four matvec kernels. */
 #define BFP_DECODE_TRACE 16
 /* Test hook for the bounded waits: the decode's abort word is set after its
  * per-decode clearing and before its first launch, so every wait for
@@ -398,7 +399,11 @@ int bfp_decode_form(const bfp_ctx *ctx);
  * norm / matvecs done, 14 D matvec done, 15 O matvec done, and the first
  * attention job's phases: 16 q|k|v in and RoPE done, 17 scores, 18 softmax,
  * 19 AV chains done -- then per step 3 head stamps (h ready, slice argmax
- * stored, token known; 0 where the step ran no head).
+ * stored, token known; 0 where the step ran no head).  After a batched
+ * decode on the matrix cores: per kernel (Q|K|V, O, G/U, D), per block (up to
+ * 1024), 6 stamps -- entry, exponents staged, row maxima reduced, tile sums
+ * formed, sums reduced, epilogue done -- from the last launch of each kernel
+ * (0 for blocks that did not run).
  * Copies up to n values and returns how many were recorded (0 if none). */
 int bfp_decode_trace(const bfp_ctx *ctx, uint64_t *out, size_t n);
 

@@ -287,3 +287,26 @@ def test_decode_batch64_matches_single(gpu):
     want, _, _ = _oracle_decode(om, prompts[0], 12)
     assert list(toks[0]) == list(want)
     gm.close()
+
+
+def test_batched_trace(gpu):
+    """A traced batched decode on the matrix cores gives the untraced tokens,
+    and every stamped block's phases are in order (entry, exponents staged,
+    row maxima, tile sums, sums reduced, epilogue); the four kernels stamp
+    their block counts (chunks x sequence groups)."""
+    cfg = dict(D=256, H_Q=4, H_KV=2, HD=64, FFN=512, NL=2, MAX_CTX=24, VOCAB=512)
+    d, om, gm = _setup(cfg, seed=33, max_batch=24)
+    from bfp import synth
+    prompts = np.stack([synth.make_prompt(d, 6, seed=500 + b) for b in range(24)])
+    want, _ = gm.decode(prompts, 8)
+    got, _ = gm.decode(prompts, 8, trace=True)
+    assert (got == want).all()
+    tr = gm.decode_trace()
+    assert tr is not None and tr.shape == (4, 1024, 6)
+    groups = 2
+    chunks = [(d.D + 2 * d.H_KV * d.HD) // 16, d.D // 16, d.FFN // 16, d.D // 16]
+    for k in range(4):
+        st = tr[k][tr[k][:, 0] > 0].astype(np.int64)
+        assert len(st) == chunks[k] * groups, (k, len(st))
+        assert (np.diff(st, axis=1) >= 0).all(), k
+    gm.close()

@@ -307,15 +307,19 @@ class BfpModel:
         return "mx" + ("+qkv_attn" if f & 4 else "") + ("+norm_fused" if f & 8 else "")
 
     def decode_trace(self):
-        """Stage stamps (device clock, 100 MHz) of the last decode(trace=True)
-        on the persistent path: (layer stamps (steps, NL, 20), head stamps
-        (steps, 3)), or None.  Layer stamps 0-15 are the stages', 16-19 the
-        first attention job's phases (include/bfp.h, bfp_decode_trace)."""
+        """Stamps (device clock, 100 MHz) of the last decode(trace=True): on
+        the persistent path (layer stamps (steps, NL, 20), head stamps
+        (steps, 3)) -- layer stamps 0-15 are the stages', 16-19 the first
+        attention job's phases; on the batched matrix-core path the blocks'
+        phase stamps (4 kernels, 1024 blocks, 6) (include/bfp.h,
+        bfp_decode_trace); None when nothing was recorded."""
         n = lib().bfp_decode_trace(self._h, None, 0)
         if n <= 0:
             return None
         out = np.zeros(n, np.uint64)
         lib().bfp_decode_trace(self._h, _p(out), n)
+        if self.decode_path() != "persist":
+            return out.reshape(4, 1024, 6)
         nl, k = self.dims.NL, TRACE_LAYER
         steps = n // (nl * k + 3)
         return out[:steps * nl * k].reshape(steps, nl, k), out[steps * nl * k:].reshape(steps, 3)

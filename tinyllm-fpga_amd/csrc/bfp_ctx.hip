@@ -11,6 +11,7 @@
 #include "bfp.h"
 #include "bfp_internal.h"
 #include "bfp_layer.h"
+#include "bfp_mx.h"
 #include "bfp_persist.h"
 
 using namespace bfp;
@@ -1074,6 +1075,15 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     return decode_copy_out(c, batch, steps, n_out, dout, tokens_out, dhm, dhe, hist_m, hist_e);
   }
   c->last_path = (flags & BFP_DECODE_NO_GRAPH) ? BFP_PATH_EAGER : BFP_PATH_GRAPH;
+  // traced batched decode: the matrix-core blocks' phase stamps
+  c->trace.clear();
+  unsigned long long *mxtr = nullptr;
+  const size_t nmx = (size_t)MX_TRACE_KERNELS * MX_TRACE_BLOCKS * MX_TRACE_STAMPS;
+  if (flags & BFP_DECODE_TRACE) {
+    BFP_TRY(tmp.alloc((void **)&mxtr, nmx * sizeof(unsigned long long)));
+    HIP_TRY(hipMemsetAsync(mxtr, 0, nmx * sizeof(unsigned long long), s));
+    BFP_TRY(set_mx_trace(mxtr));
+  }
   // no tagged word of an earlier decode may carry a tag of this one
   HIP_TRY(hipMemsetAsync(c->t_h1, 0, sizeof(unsigned) * batch * d.D, s));
   HIP_TRY(hipMemsetAsync(c->t_h, 0, sizeof(unsigned) * batch * d.D, s));
@@ -1100,7 +1110,7 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
       a.g1_next = l + 1 < d.NL ? c->g1 + (size_t)(l + 1) * d.D : nullptr;
       a.t_abort = c->t_abort;
       c->last_form = layer_form(a);
-      BFP_TRY(launch_layer(a, s));
+      BFP_TRY(launch_layer(a, s, mxtr != nullptr));
     }
     CtlArgs cc = ca;
     cc.head = head ? 1 : 0;
@@ -1168,6 +1178,11 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     (void)hipEventElapsedTime(&gms, evg, ev1);
     c->last_decode_ms = ms;
     c->last_gen_ms = gms;
+    if (mxtr) {
+      c->trace.resize(nmx);
+      hipError_t e = hipMemcpy(c->trace.data(), mxtr, nmx * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+      if (e != hipSuccess) rc = set_err(BFP_EIO, "decode trace: %s", hipGetErrorString(e));
+    }
     c->step_ms.clear();
     if (per_step) {
       c->step_ms.resize(steps);

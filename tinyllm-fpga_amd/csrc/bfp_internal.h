@@ -70,7 +70,10 @@ struct LayerArgs;
 struct HeadArgs;
 struct CtlArgs;
 struct EmbedArgs;
-int launch_layer(const LayerArgs &a, hipStream_t s);
+// mx_traced: the matrix-core matvecs stamp their phases into the buffer
+// set_mx_trace names (batched decodes traced with BFP_DECODE_TRACE).
+int launch_layer(const LayerArgs &a, hipStream_t s, bool mx_traced = false);
+int set_mx_trace(unsigned long long *p);
 // The launch form launch_layer takes for a (BFP_FORM_* bits).
 int layer_form(const LayerArgs &a);
 int prepare_layer_kernels(int max_ctx, int D, int FFN);

@@ -337,6 +337,24 @@ __global__ __launch_bounds__(64 * NW) void k_d_res_m(LayerArgs a) {
 // MFMA (bfp_mx.h); the epilogues are the multi-sequence path's.  blockIdx.x
 // is a block of NC chunks, blockIdx.y a group of 16 sequences.  Each
 // 16-lane group runs the epilogue of one (chunk, sequence) pair per pass.
+// The phase stamps of a traced batched decode (MX_TRACE_KERNELS x
+// MX_TRACE_BLOCKS x MX_TRACE_STAMPS), set by set_mx_trace.  Only the kernel
+// instances launched for a traced decode (TR) read it, so an untraced launch
+// carries no stamp code and no extra argument (a null test per phase cost
+// config 5 2.7%, a trace pointer in LayerArgs 0.4%).
+__device__ unsigned long long *g_mx_trace;
+int set_mx_trace(unsigned long long *p) {
+  HIP_TRY(hipMemcpyToSymbol(HIP_SYMBOL(g_mx_trace), &p, sizeof p));
+  return BFP_OK;
+}
+
+// The trace slice of matvec kernel k in a traced launch.
+template <bool TR>
+__device__ __forceinline__ unsigned long long *mx_tr(const LayerArgs &, int k) {
+  if constexpr (TR) return g_mx_trace + (size_t)k * MX_TRACE_BLOCKS * MX_TRACE_STAMPS;
+  return nullptr;
+}
+
 #define BFP_MX_EPI(NPAIR, ...)                                                    \
   {                                                                              \
     const int r_ = threadIdx.x & 15, grp_ = threadIdx.x >> 4;                     \
@@ -354,6 +372,7 @@ __global__ __launch_bounds__(64 * NW) void k_d_res_m(LayerArgs a) {
 
 // Q|K|V: one chunk per block (two chunks per block, half the blocks,
 // measured 8.5 against 6.6 us for the 960 x 576 block of 64 sequences).
+template <bool TR>
 __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_qkv_mx(LayerArgs a) {
   __shared__ long long Ao[16 * MX_SEQ];
   __shared__ int Mo[16 * MX_SEQ];
@@ -361,12 +380,13 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_qkv_mx(LayerArgs a) {
   const int nT = a.D / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
   const int ns = min(MX_SEQ, a.batch - b0);
   mx_block<1>(a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT,
-              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_QKV));
   BFP_MX_EPI(MX_SEQ, {
     const int q_ = r_ * MX_SEQ + j_;
     (void)cc_;
     epi_qkv(a, b, c, mx_A(Ao, q_), Mo[q_], wr_);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
 }
 
 // The attention's q|k|v input from tagged words that the Q|K|V blocks of the
@@ -397,7 +417,7 @@ struct AttnTagIO : AttnPlainIO {
 // has been dispatched before it.  blockDim = 64 * ATT_WAVES; the blocks'
 // Ao / Mo sit in the dynamic LDS after their exponents, so the attention
 // keeps k_attn's LDS and occupancy.
-template <int PPW>
+template <int PPW, bool TR>
 __global__ __launch_bounds__(64 * ATT_WAVES, (PPW == 3 ? 6 : 4)) void k_qkv_attn_mx(LayerArgs a, int nblk) {
   extern __shared__ double dsm[];
   const int nq = a.D + 2 * a.KV;
@@ -415,17 +435,19 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (PPW == 3 ? 6 : 4)) void k_qkv_attn
   long long *Ao = reinterpret_cast<long long *>(mx_ex + mx_lds_bytes(1, nT));   // 32 nT bytes
   int *Mo = reinterpret_cast<int *>(Ao + 16 * MX_SEQ);
   mx_block<1>(a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT,
-              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_QKV));
   BFP_MX_EPI(MX_SEQ, {
     const int q_ = r_ * MX_SEQ + j_;
     (void)cc_;
     epi_qkv(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, tag);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
 }
 
 typedef void (*qa_fn)(LayerArgs, int);
-static qa_fn qkv_attn_kernel(int ppw) {
-  return ppw == 2 ? k_qkv_attn_mx<2> : (ppw == 3 ? k_qkv_attn_mx<3> : k_qkv_attn_mx<4>);
+static qa_fn qkv_attn_kernel(int ppw, bool tr = false) {
+  if (tr) return ppw == 2 ? k_qkv_attn_mx<2, true> : (ppw == 3 ? k_qkv_attn_mx<3, true> : k_qkv_attn_mx<4, true>);
+  return ppw == 2 ? k_qkv_attn_mx<2, false> : (ppw == 3 ? k_qkv_attn_mx<3, false> : k_qkv_attn_mx<4, false>);
 }
 inline size_t qkv_attn_lds(const LayerArgs &a) {
   const size_t sha = attn_lds_bytes(a.max_ctx, attn_ppw(a.max_ctx), AttnPlainIO::kAvBlock);
@@ -434,6 +456,7 @@ inline size_t qkv_attn_lds(const LayerArgs &a) {
 }
 
 // O and residual 1: one chunk per block.
+template <bool TR>
 __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_mx(LayerArgs a) {
   __shared__ long long Ao[16 * MX_SEQ];
   __shared__ int Mo[16 * MX_SEQ];
@@ -441,13 +464,14 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_mx(LayerArgs a) {
   const int nT = a.D / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
   const int ns = min(MX_SEQ, a.batch - b0);
   mx_block<1>(a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT,
-              a.att_m + (long long)b0 * a.D, a.att_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.att_m + (long long)b0 * a.D, a.att_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_O));
   BFP_MX_EPI(MX_SEQ, {
     const int q_ = r_ * MX_SEQ + j_;
     (void)cc_;
     epi_ores(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h_m[b * a.D + c * 16 + r_],
              a.h_e[b * (a.D / 16) + c]);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_O), 5);
 }
 
 // An RMSNorm of sequence b (k_norm_pairs' arithmetic and output; which = 1:
@@ -494,6 +518,7 @@ __device__ __forceinline__ void norm_tagged(const LayerArgs &a, int b, int which
 // workgroups poll.  Workgroups are dispatched in id order and the blocks
 // never wait, so every block a norm workgroup waits for has been dispatched
 // before it.  blockDim >= D / 2.
+template <bool TR>
 __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_norm_mx(LayerArgs a, int nblk) {
   __shared__ long long Ao[16 * MX_SEQ];
   __shared__ int Mo[16 * MX_SEQ];
@@ -506,16 +531,18 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_norm_mx(LayerArgs a
   const int ns = min(MX_SEQ, a.batch - b0);
   const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
   mx_block<1>(a.w_o_m + (long long)c * nT * 32, a.w_o_e + (long long)c * nT * 16, nT,
-              a.att_m + (long long)b0 * a.D, a.att_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.att_m + (long long)b0 * a.D, a.att_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_O));
   BFP_MX_EPI(MX_SEQ, {
     const int q_ = r_ * MX_SEQ + j_;
     (void)cc_;
     epi_ores(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h_m[b * a.D + c * 16 + r_],
              a.h_e[b * (a.D / 16) + c], tag);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_O), 5);
 }
 
 // G and U: the G chunk (2x) and U chunk (2x+1) of FFN chunk x per block.
+template <bool TR>
 __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_gu_mx(LayerArgs a) {
   __shared__ long long Ao[2 * 16 * MX_SEQ];
   __shared__ int Mo[2 * 16 * MX_SEQ];
@@ -523,17 +550,19 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_gu_mx(LayerArgs a) {
   const int nT = a.D / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
   const int ns = min(MX_SEQ, a.batch - b0);
   mx_block<2>(a.w_gu_m + (long long)(2 * c) * nT * 32, a.w_gu_e + (long long)(2 * c) * nT * 16, nT,
-              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_GU));
   BFP_MX_EPI(MX_SEQ, {
     const int qg_ = r_ * MX_SEQ + j_, qu_ = (16 + r_) * MX_SEQ + j_;
     (void)cc_;
     epi_gu(a, b, c, mx_A(Ao, qg_), Mo[qg_], mx_A(Ao, qu_), Mo[qu_], wr_);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_GU), 5);
 }
 
 // D and residual 2: one chunk per block, up to 12 waves (the FFN-input
 // block has 96 tiles: 12 waves measured 9.7 against 10.2 us for 8).
 constexpr int MX_WAVES_D = 12;
+template <bool TR>
 __global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_mx(LayerArgs a) {
   __shared__ long long Ao[16 * MX_SEQ];
   __shared__ int Mo[16 * MX_SEQ];
@@ -541,19 +570,21 @@ __global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_mx(LayerArgs a) {
   const int nT = a.FFN / 16, c = blockIdx.x, b0 = blockIdx.y * MX_SEQ;
   const int ns = min(MX_SEQ, a.batch - b0);
   mx_block<1>(a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT,
-              a.mlp_m + (long long)b0 * a.FFN, a.mlp_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.mlp_m + (long long)b0 * a.FFN, a.mlp_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_D));
   BFP_MX_EPI(MX_SEQ, {
     const int q_ = r_ * MX_SEQ + j_;
     (void)cc_;
     epi_dres(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h1_m[b * a.D + c * 16 + r_],
              a.h1_e[b * (a.D / 16) + c]);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_D), 5);
 }
 
 
 // k_d_res_mx's blocks (ids below nblk) and the next layer's RMSNorm 1 (one
 // workgroup per sequence, ids from nblk, gamma g1_next) in one launch, as
 // k_o_res_norm_mx: the blocks also store h as tagged words.
+template <bool TR>
 __global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_norm_mx(LayerArgs a, int nblk) {
   __shared__ long long Ao[16 * MX_SEQ];
   __shared__ int Mo[16 * MX_SEQ];
@@ -566,13 +597,14 @@ __global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_norm_mx(LayerArgs a, 
   const int ns = min(MX_SEQ, a.batch - b0);
   const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
   mx_block<1>(a.w_d_m + (long long)c * nT * 32, a.w_d_e + (long long)c * nT * 16, nT,
-              a.mlp_m + (long long)b0 * a.FFN, a.mlp_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex);
+              a.mlp_m + (long long)b0 * a.FFN, a.mlp_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_D));
   BFP_MX_EPI(MX_SEQ, {
     const int q_ = r_ * MX_SEQ + j_;
     (void)cc_;
     epi_dres(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, a.h1_m[b * a.D + c * 16 + r_],
              a.h1_e[b * (a.D / 16) + c], tag);
   })
+  mx_mark(mx_tr<TR>(a, MX_K_D), 5);
 }
 
 
@@ -943,6 +975,7 @@ int prepare_layer_kernels(int max_ctx, int D, int FFN) {
     la.max_ctx = max_ctx;
     la.D = D;
     BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(qkv_attn_kernel(ppw)), (int)qkv_attn_lds(la)));
+    BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(qkv_attn_kernel(ppw, true)), (int)qkv_attn_lds(la)));
   }
   int nw, tpt, nwf, tptf;
   shape_for(D / 16, nw, tpt);
@@ -1012,18 +1045,19 @@ int layer_form(const LayerArgs &a) {
          (mx_fused_norms(a) ? BFP_FORM_NORM_FUSED : 0);
 }
 
-static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
+static int launch_layer_mx(const LayerArgs &a, hipStream_t s, bool mx_traced) {
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   const int G = (a.batch + MX_SEQ - 1) / MX_SEQ;
   const int bq = (a.D + 2 * a.KV) / 16, bo = a.D / 16, bg = a.FFN / 16;
   const bool fused = mx_fused_norms(a);
+  const bool tr = mx_traced;
   if (!(fused && a.layer > 0)) launch_norm_seq(a, 1, s);   // else the last layer's D launch ran it
   if (mx_joined_qkv_attn(a)) {
     // Q|K|V + attention in one launch (batched decode, short forms)
-    hipLaunchKernelGGL(qkv_attn_kernel(attn_ppw(a.max_ctx)), dim3(bq * G + a.H_Q * a.batch),
+    hipLaunchKernelGGL(qkv_attn_kernel(attn_ppw(a.max_ctx), tr), dim3(bq * G + a.H_Q * a.batch),
                        dim3(64 * ATT_WAVES), qkv_attn_lds(a), s, a, bq * G);
   } else {
-    hipLaunchKernelGGL(k_qkv_mx, dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
+    hipLaunchKernelGGL((tr ? k_qkv_mx<true> : k_qkv_mx<false>), dim3(bq, G), dim3(64 * mx_waves(nTD, bq * G)),
                        mx_lds_bytes(1, nTD), s, a);
     BFP_TRY(launch_attn(a, s));
   }
@@ -1032,29 +1066,29 @@ static int launch_layer_mx(const LayerArgs &a, hipStream_t s) {
     // O + RMSNorm 2 in one launch (batched decode)
     const size_t shn = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)a.D * 3;
     const size_t sho = mx_lds_bytes(1, nTD);
-    hipLaunchKernelGGL(k_o_res_norm_mx, dim3(bo * G + a.batch), dim3(64 * wo), sho > shn ? sho : shn, s,
+    hipLaunchKernelGGL((tr ? k_o_res_norm_mx<true> : k_o_res_norm_mx<false>), dim3(bo * G + a.batch), dim3(64 * wo), sho > shn ? sho : shn, s,
                        a, bo * G);
   } else {
-    hipLaunchKernelGGL(k_o_res_mx, dim3(bo, G), dim3(64 * wo), mx_lds_bytes(1, nTD), s, a);
+    hipLaunchKernelGGL((tr ? k_o_res_mx<true> : k_o_res_mx<false>), dim3(bo, G), dim3(64 * wo), mx_lds_bytes(1, nTD), s, a);
     launch_norm_seq(a, 2, s);
   }
-  hipLaunchKernelGGL(k_gu_mx, dim3(bg, G), dim3(64 * mx_waves(nTD, bg * G)),
+  hipLaunchKernelGGL((tr ? k_gu_mx<true> : k_gu_mx<false>), dim3(bg, G), dim3(64 * mx_waves(nTD, bg * G)),
                      mx_lds_bytes(2, nTD), s, a);
   const int wd = mx_waves_d(a);
   if (fused && a.g1_next) {
     // D + the next layer's RMSNorm 1 in one launch (batched decode)
     const size_t shn = (size_t)(a.D + PW_MAX_LEAVES) * 8 + (size_t)a.D * 3;
     const size_t shd = mx_lds_bytes(1, nTF);
-    hipLaunchKernelGGL(k_d_res_norm_mx, dim3(bo * G + a.batch), dim3(64 * wd), shd > shn ? shd : shn, s,
+    hipLaunchKernelGGL((tr ? k_d_res_norm_mx<true> : k_d_res_norm_mx<false>), dim3(bo * G + a.batch), dim3(64 * wd), shd > shn ? shd : shn, s,
                        a, bo * G);
   } else {
-    hipLaunchKernelGGL(k_d_res_mx, dim3(bo, G), dim3(64 * wd), mx_lds_bytes(1, nTF), s, a);
+    hipLaunchKernelGGL((tr ? k_d_res_mx<true> : k_d_res_mx<false>), dim3(bo, G), dim3(64 * wd), mx_lds_bytes(1, nTF), s, a);
   }
   return launch_status("layer");
 }
 
-static int launch_layer_multi(const LayerArgs &a, hipStream_t s) {
-  if (a.batch >= MX_MIN_BATCH) return launch_layer_mx(a, s);
+static int launch_layer_multi(const LayerArgs &a, hipStream_t s, bool mx_traced) {
+  if (a.batch >= MX_MIN_BATCH) return launch_layer_mx(a, s, mx_traced);
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   int nw, tpt, nwf, tptf;
   shape_for(nTD, nw, tpt);
@@ -1075,8 +1109,8 @@ static int launch_layer_multi(const LayerArgs &a, hipStream_t s) {
   return launch_status("layer");
 }
 
-int launch_layer(const LayerArgs &a, hipStream_t s) {
-  if (a.batch >= MULTI_MIN_BATCH && a.xn_m) return launch_layer_multi(a, s);
+int launch_layer(const LayerArgs &a, hipStream_t s, bool mx_traced) {
+  if (a.batch >= MULTI_MIN_BATCH && a.xn_m) return launch_layer_multi(a, s, mx_traced);
   const int nTD = a.D / 16, nTF = a.FFN / 16;
   int nw, tpt;
   shape_for(nTD, nw, tpt);

@@ -64,6 +64,20 @@ __device__ __forceinline__ mx_v4 mx_mfma(long a, long b, mx_v4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
 
+// Phase stamps of a traced batched decode (100 MHz clock, thread 0 of each
+// block): MX_TRACE_STAMPS per block -- 0 entry, 1 exponents staged, 2 M
+// reduced, 3 tile sums formed, 4 A reduced, 5 epilogue done (stamped by the
+// kernel) -- for at most MX_TRACE_BLOCKS blocks of each of the MX_TRACE_KERNELS
+// matvec kernels (MX_K_*), the last launch of each kind overwriting the one
+// before.
+constexpr int MX_TRACE_STAMPS = 6, MX_TRACE_BLOCKS = 1024, MX_TRACE_KERNELS = 4;
+constexpr int MX_K_QKV = 0, MX_K_O = 1, MX_K_GU = 2, MX_K_D = 3;
+__device__ __forceinline__ void mx_mark(unsigned long long *tr, int k) {
+  const unsigned b = blockIdx.x + blockIdx.y * gridDim.x;
+  if (tr && threadIdx.x == 0 && b < (unsigned)MX_TRACE_BLOCKS)
+    tr[b * MX_TRACE_STAMPS + k] = __builtin_amdgcn_s_memrealtime();
+}
+
 // LDS bytes mx_block<NC> needs beyond its caller's Ao / Mo: the block's
 // weight and input exponents, tile-major.
 __host__ __device__ constexpr int mx_lds_bytes(int nc, int nT) { return (nc + 1) * 16 * nT; }
@@ -77,7 +91,8 @@ __host__ __device__ constexpr int mx_lds_bytes(int nc, int nT) { return (nc + 1)
 template <int NC>
 __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int8_t *__restrict__ pe, int nT,
                          const int16_t *__restrict__ xm, const int8_t *__restrict__ xe, int ns,
-                         long long *Ao, int *Mo, int8_t *ex) {
+                         long long *Ao, int *Mo, int8_t *ex, unsigned long long *tr = nullptr) {
+  mx_mark(tr, 0);
   constexpr int G = 4;           // tiles whose loads are in flight together
   constexpr int RW = NC * 16;    // rows of the block
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -140,6 +155,7 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
     Mo[q] = -(1 << 29);
   }
   __syncthreads();
+  mx_mark(tr, 1);
   const mx_v4 zero = {0, 0, 0, 0};
   // E = W_e + x_e of chunk c, tile t for this lane's outputs (rows 4 kg + v,
   // sequence i): the four rows' exponents are one 4-byte word of wex
@@ -168,6 +184,7 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
     }
   }
   __syncthreads();
+  mx_mark(tr, 2);
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -212,6 +229,7 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
       }
     }
   }
+  mx_mark(tr, 3);
   if (t0 < t1) {
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -221,6 +239,7 @@ __device__ __forceinline__ void mx_block(const uint4 *__restrict__ pm, const int
                   (unsigned long long)A[c][v]);
   }
   __syncthreads();
+  mx_mark(tr, 4);
 }
 
 // A read back for an epilogue, clipped as the engine clips.
