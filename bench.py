@@ -388,8 +388,8 @@ def decode_leg(reps, n_gen=64):
 # stamp k of (step, layer), taken by thread 0 of each role's first workgroup
 # on the 100 MHz device clock): Q|K|V 0 (h in), 10 (RMSNorm done), 11
 # (matvec done), 1 (q|k|v stored), 3 (attention job 0 done) with the job's
-# phases 16 (q|k|v in, RoPE done), 17 (scores), 18 (softmax), 19 (AV
-# chains); O 4 (attention output in), 15, 5; G/U 6 (h1 in), 12, 13, 7; D 8
+# phases 2 (its q|k|v input in), 16 (RoPE done), 17 (scores), 18 (softmax),
+# 19 (AV chains); O 4 (attention output in), 15, 5; G/U 6 (h1 in), 12, 13, 7; D 8
 # (mlp in), 14, 9 (h stored).  Head stamps per step: 0 (start), 1
 # (vocabulary slices done), 2 (token chosen).
 TRACE_INTERVALS = [
@@ -398,7 +398,8 @@ TRACE_INTERVALS = [
     ("Q|K|V matvec", (0, 10), (0, 11)),
     ("Q|K|V epilogue + store", (0, 11), (0, 1)),
     ("attention (incl. q|k|v hand-off)", (0, 1), (0, 3)),
-    ("  attention: q|k|v hand-off + RoPE + cache row", (0, 1), (0, 16)),
+    ("  attention: q|k|v hand-off", (0, 1), (0, 2)),
+    ("  attention: RoPE + cache row", (0, 2), (0, 16)),
     ("  attention: scores", (0, 16), (0, 17)),
     ("  attention: softmax", (0, 17), (0, 18)),
     ("  attention: AV chains", (0, 18), (0, 19)),

@@ -394,7 +394,8 @@ int bfp_decode_path(const bfp_ctx *ctx);
 int bfp_decode_form(const bfp_ctx *ctx);
 /* The stage trace of the last decode run with BFP_DECODE_TRACE on the
  * persistent path: per (step, layer) 20 stamps -- 0/1 Q|K|V input ready /
- * output stored, 2 (unused), 3 attention output stored, 4/5 O, 6/7 G/U, 8/9 D
+ * output stored, 2 the first attention job's q|k|v input in, 3 attention
+ * output stored, 4/5 O, 6/7 G/U, 8/9 D
  * input ready / output stored, 10/11 Q|K|V norm / matvec done, 12/13 G/U
  * norm / matvecs done, 14 D matvec done, 15 O matvec done, and the first
  * attention job's phases: 16 q|k|v in and RoPE done, 17 scores, 18 softmax,

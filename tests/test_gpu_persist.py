@@ -151,7 +151,7 @@ def test_persist_trace(gpu, max_ctx):
     lay, head = gm.decode_trace()
     steps = 8 + n_gen
     assert lay.shape == (steps, d.NL, 20) and head.shape == (steps, 3)
-    order = [0, 10, 11, 1, 16, 17, 18, 19, 3]
+    order = [0, 10, 11, 1, 2, 16, 17, 18, 19, 3]
     for s in range(steps):
         for li in range(d.NL):
             v = lay[s, li, order].astype(np.int64)

@@ -387,11 +387,10 @@ __device__ __forceinline__ void quantize16_pairs(double y0, double y1, int &m0, 
 
 // RoPE of one 64-wide head held one value per lane of a wave (lane l holds
 // element l, pre-rotation x), re-quantised: returns the lane's mantissa.
-__device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
+// (c, s): the lane's (cos, sin) of pair j = lane % 32.
+__device__ __forceinline__ int rope_lane(double x, double c, double s, int &e) {
   const int l = threadIdx.x & 63;
-  const int j = l & 31;
   double other = peer<32>(x);              // the partner element j+32 / j
-  double c = cs[2 * j], s = cs[2 * j + 1];
   double out;
   if (l < 32) {
     out = x * c - other * s;                 // a*c - b*s
@@ -399,6 +398,10 @@ __device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
     out = x * c + other * s;                 // b*c + a*s
   }
   return quantize16_lanes(out, e);
+}
+__device__ __forceinline__ int rope_lane(double x, const double *cs, int &e) {
+  const int j = threadIdx.x & 31;
+  return rope_lane(x, cs[2 * j], cs[2 * j + 1], e);
 }
 
 }  // namespace bfp

@@ -369,6 +369,11 @@ struct AttnPlainIO {
   }
   // phase stamps of a traced decode (ATT_MARK_*); none on this path
   __device__ __forceinline__ void mark(int) const {}
+  // the (cos, sin) of RoPE pair j from the row at cs
+  __device__ __forceinline__ void rope_cs(const double *cs, int j, double &c, double &s) const {
+    c = cs[2 * j];
+    s = cs[2 * j + 1];
+  }
 };
 
 // The attention's phase stamps (IO::mark), in the order they are taken.
@@ -376,6 +381,7 @@ constexpr int ATT_MARK_ROPE = 0;      // q|k|v in, RoPE done, the cache row stor
 constexpr int ATT_MARK_SCORES = 1;    // every score in LDS (after the long form's exchange)
 constexpr int ATT_MARK_SOFTMAX = 2;   // probabilities in LDS
 constexpr int ATT_MARK_AV = 3;        // the AV chains done
+constexpr int ATT_MARK_QKV = 4;       // wave 0's q|k|v input in (its q head)
 
 // Attention of one q head (full.py:268-283) in workgroups of ATT_WAVES
 // waves:
@@ -515,6 +521,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   // and the rest, which do not use it)
   int in_m, in_e;
   io.qkv(w == 0 ? hq * HD + l : (w == 1 ? a.D + g * HD + l : a.D + a.KV + g * HD + l), in_m, in_e);
+  io.mark(ATT_MARK_QKV);
   // the position is read after the loads that do not depend on it are issued
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   const int2 pp = posf();   // (KV slot, RoPE position)
@@ -522,6 +529,12 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   const int n = pos + 1;
   const double *cs = a.rope_row ? a.rope_row                 // (HD/2) x (cos, sin)
                                 : a.rope + (long long)rpos * HD;
+  // this lane's (cos, sin), read before the K rows below are requested (the
+  // persistent kernel's row is in LDS and is read as such: through a generic
+  // pointer it is a FLAT load, and a wait on one also waits for every vector
+  // load issued before it, which cost the long form 3 us)
+  double rcos = 0.0, rsin = 0.0;
+  if (w < 2) io.rope_cs(cs, l & 31, rcos, rsin);
 
   // AV staging: chunk c holds rows c*AVC .. c*AVC+AVC-1 (clamped to n-1, so
   // no load sits in a branch); thread tid loads 16-byte part tid%8 of rows
@@ -595,7 +608,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   if (w == 0) {            // q head hq
     int idx = hq * HD + l;
     int e;
-    int m = rope_lane(bfp_val(in_m, in_e), cs, e);
+    int m = rope_lane(bfp_val(in_m, in_e), rcos, rsin, e);
     q[l] = bfp_val(m, e);
     if (a.dump && lead) {
       int cm, ce;
@@ -605,7 +618,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     }
   } else if (w == 1) {     // k head g
     int e;
-    int m = rope_lane(bfp_val(in_m, in_e), cs, e);
+    int m = rope_lane(bfp_val(in_m, in_e), rcos, rsin, e);
     kc[l] = bfp_val(m, e);
     long long o = ((long long)pos * a.H_KV + g) * HD + l;
     if (writer) {

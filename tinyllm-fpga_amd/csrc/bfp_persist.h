@@ -33,7 +33,8 @@ struct PersistArgs {
   int hist_steps;
   // optional stage trace (100 MHz clock), written by the first workgroup of
   // each role: per (step, layer) PT_TRACE_LAYER stamps -- 0/1 Q|K|V input
-  // ready / output stored, 3 attention output stored, 4/5 O, 6/7 G/U, 8/9 D
+  // ready / output stored, 2 attention job 0's q|k|v input in (wave 0), 3
+  // attention output stored, 4/5 O, 6/7 G/U, 8/9 D
   // ready / stored, 10/11 Q|K|V norm / matvec done, 12/13 G/U norm / matvecs
   // done, 14 D matvec done, 15 O matvec done, and attention job 0's phases
   // 16 RoPE (and its q|k|v input) done, 17 scores, 18 softmax, 19 AV chains

@@ -304,9 +304,17 @@ struct AttnCohIO {
   rsrc_t rkm, rke, rvm, rve;      // this layer's KV cache
   const int16_t *km0, *vm0;
   const int8_t *ke0, *ve0;
-  unsigned long long *trace;      // traced decode, first attention job: stamps at trace[k]
+  // the step's RoPE row: role_qkv's copy in LDS (rope_s), read as LDS
+  const double *rope_s;
+  __device__ __forceinline__ void rope_cs(const double *, int j, double &c, double &s) const {
+    const double *ls = lds(rope_s);
+    c = ls[2 * j];
+    s = ls[2 * j + 1];
+  }
+  unsigned long long *trace;      // traced decode, first attention job: its (step, layer) stamps
   __device__ __forceinline__ void mark(int k) const {
-    if (trace && threadIdx.x == 0) put_clock(trace, PT_TRACE_ATT + k);
+    // ATT_MARK_ROPE .. ATT_MARK_AV at PT_TRACE_ATT + k, the q|k|v arrival in slot 2
+    if (trace && threadIdx.x == 0) put_clock(trace, k == ATT_MARK_QKV ? 2 : PT_TRACE_ATT + k);
   }
   __device__ __forceinline__ void qkv(int idx, int &m, int &e) const {
     const unsigned v = w->word(rq, 4 * idx, tag);
@@ -572,6 +580,7 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
         io.rsc = rsrc(p.sc_buf);
         io.rfl = rsrc(p.t_sflag);
         io.sc_stride = a.max_ctx;
+        io.rope_s = rope_s;
         io.trace = (p.trace && c == 0) ? p.trace + ((size_t)s * p.NL + l) * PT_TRACE_LAYER : nullptr;
         attn_body<PPW, SHORT>(a, io, c, 0, [s] { return make_int2(s, s); }, dsm);
         stamp(p, c == 0, s, l, 3);
