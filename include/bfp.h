@@ -369,6 +369,17 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * bounded loop, the kernels still run to their end, and bfp_decode returns
  * BFP_EIO.  The next decode clears the word again. */
 #define BFP_DECODE_ABORT_TEST 32
+/* The pipelined batched step: each step's layers as one launch (one
+ * workgroup per compute unit; the sequences pass the stages in groups of 16,
+ * the stages handing over through device-coherent memory), when the
+ * dimensions allow it (HD = 64, D <= 640, FFN <= 1536, D and FFN multiples of
+ * 64, NL <= 32, a KV capacity of at most 512, the Q|K|V, O, G/U and D chunks
+ * of a layer within the compute units).  BFP_DECODE_PIPE asks for it at any
+ * batch size; without it, batches of at least BFP_PIPE_MIN_BATCH sequences
+ * (environment; unset or 0: none) take it; BFP_DECODE_NO_PIPE keeps the
+ * per-stage launches.  Both give identical outputs. */
+#define BFP_DECODE_NO_PIPE 64
+#define BFP_DECODE_PIPE 128
 int bfp_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen, int batch,
                int32_t *tokens_out, int16_t *hist_m, int8_t *hist_e, int flags);
 /* How the last bfp_decode ran: BFP_PATH_PERSIST (one persistent launch),
@@ -384,13 +395,15 @@ int bfp_decode_path(const bfp_ctx *ctx);
  * vector unit), or BFP_FORM_MX (int8 matrix-core matvecs) with
  * BFP_FORM_QKV_ATTN when Q|K|V and attention ran as one launch and
  * BFP_FORM_NORM_FUSED when the RMSNorms ran inside the O and D launches;
- * BFP_FORM_PERSIST for the persistent batch-1 decode; -1 before any decode. */
+ * BFP_FORM_PERSIST for the persistent batch-1 decode, BFP_FORM_PIPE for the
+ * pipelined batched step; -1 before any decode. */
 #define BFP_FORM_SINGLE 0
 #define BFP_FORM_MULTI 1
 #define BFP_FORM_MX 2
 #define BFP_FORM_QKV_ATTN 4
 #define BFP_FORM_NORM_FUSED 8
 #define BFP_FORM_PERSIST 16
+#define BFP_FORM_PIPE 32
 int bfp_decode_form(const bfp_ctx *ctx);
 /* The stage trace of the last decode run with BFP_DECODE_TRACE on the
  * persistent path: per (step, layer) 20 stamps -- 0/1 Q|K|V input ready /

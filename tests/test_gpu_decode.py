@@ -264,7 +264,7 @@ def test_decode_ragged_batch_joined_launches(gpu):
     d, om, gm = _setup(cfg, seed=21, max_batch=40)
     from bfp import synth
     prompts = np.stack([synth.make_prompt(d, 6, seed=300 + b) for b in range(40)])
-    toks, _ = gm.decode(prompts, 10)
+    toks, _ = gm.decode(prompts, 10, pipe=False)
     assert gm.decode_form() == "mx+qkv_attn+norm_fused"
     for b in (0, 15, 16, 33, 39):
         single, _ = gm.decode(prompts[b:b + 1], 10)
@@ -298,8 +298,8 @@ def test_batched_trace(gpu):
     d, om, gm = _setup(cfg, seed=33, max_batch=24)
     from bfp import synth
     prompts = np.stack([synth.make_prompt(d, 6, seed=500 + b) for b in range(24)])
-    want, _ = gm.decode(prompts, 8)
-    got, _ = gm.decode(prompts, 8, trace=True)
+    want, _ = gm.decode(prompts, 8, pipe=False)
+    got, _ = gm.decode(prompts, 8, trace=True, pipe=False)
     assert (got == want).all()
     tr = gm.decode_trace()
     assert tr is not None and tr.shape == (4, 1024, 6)

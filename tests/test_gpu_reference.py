@@ -144,10 +144,12 @@ def test_config4_decode_on_gpu(gpu, path_env, monkeypatch):
     assert list(toks[0]) == [int(t) for t in f["tokens"]]
 
 
-def test_config5_decode_on_gpu(gpu):
-    """the 64 sequences decoded together (the batched
-    matrix-core path), every sequence's per-step layer-output digests and
-    its 128 tokens against the reference's own single-sequence runs."""
+@pytest.mark.parametrize("pipe", [False, True], ids=["launches", "pipelined"])
+def test_config5_decode_on_gpu(gpu, pipe):
+    """the 64 sequences decoded together -- on the
+    per-stage matrix-core launches and on the pipelined one-launch step --
+    every sequence's per-step layer-output digests and its 128 tokens
+    against the reference's own single-sequence runs."""
     from bfp import Dims, synth
     from bfp.model import BfpModel
     path = GOLDEN / "ref_decode_cfg5.npz"
@@ -163,10 +165,8 @@ def test_config5_decode_on_gpu(gpu):
     gm = BfpModel(d, max_batch=B)
     gm.load_fp32(synth.make_model(d, seed=int(f["seed"])))
     print(f"[gpu-ref] config 5: decoding {B} sequences x {steps} steps", flush=True)
-    toks, (hm, he) = gm.decode(prompts, n_gen, hist=True)
-    # the joined launches ran (Q|K|V with attention, the norms inside the
-    # O and D launches), not the unjoined fallback
-    assert gm.decode_form() == "mx+qkv_attn+norm_fused"
+    toks, (hm, he) = gm.decode(prompts, n_gen, hist=True, pipe=pipe)
+    assert gm.decode_form() == ("pipe" if pipe else "mx+qkv_attn+norm_fused")
     gm.close()
     for b in range(B):
         got = _digests(hm, he, b, steps, d.NL)

@@ -45,3 +45,45 @@ def test_split_identity_and_bounds():
         assert abs(lo) < 2 ** 31   # the 32-bit low part of the kernel
         worst = max(worst, abs(lo))
     assert worst < 2 ** 29
+
+
+def _mfma32(a, b):
+    """One 32-deep int8 product sum as v_mfma_i32_16x16x32_i8 forms it for a
+    (row, sequence) pair: k-groups 0-1 and 2-3 hold the 16-element tile
+    twice; a and b are (32,) int8 operands."""
+    a, b = np.asarray(a, np.int64), np.asarray(b, np.int64)
+    assert a.min() >= -128 and a.max() <= 127 and b.min() >= -128 and b.max() <= 127
+    return int((a * b).sum())
+
+
+def test_select_free_doubled_form():
+    """The select-free form of the kernels: every operand holds both copies
+    of the tile except the constant k1 (ones in the first copy, zeros in the
+    second), so each 32-deep product is twice the tile's, and with
+    sum x = 256 sum xh + sum xl' + 2048
+      2 S = 65536 (P(Wh, xh) + P(Wh, k1) + P(k1, xh) + 8)
+            + 256 (P(Wh, xl') + P(Wl', xh) + P(Wl', k1) + P(k1, xl'))
+            + P(Wl', xl')
+    with P the MFMA's 32-deep sum; floor(S / 2^d) = floor(2S / 2^(d+1)).
+    Each accumulator and the 32-bit low part fit int32."""
+    rng = np.random.default_rng(1)
+    ext = [-32768, -32767, -256, -129, -128, -1, 0, 1, 127, 128, 255, 256, 32767]
+    cases = [(rng.integers(-32768, 32768, 16), rng.integers(-32768, 32768, 16)) for _ in range(2000)]
+    for a in (-32768, 32767):
+        for b in (-32768, 32767):
+            cases.append((np.full(16, a), np.full(16, b)))
+    cases += [(rng.choice(ext, 16), rng.choice(ext, 16)) for _ in range(2000)]
+    k1 = np.array([1] * 16 + [0] * 16)
+    for W, x in cases:
+        Wh, Wl = _split(W)
+        xh, xl = _split(x)
+        dup = lambda v: np.concatenate([v, v])   # noqa: E731
+        hh = _mfma32(dup(xh), k1) + 8 + _mfma32(dup(Wh), dup(xh)) + _mfma32(dup(Wh), k1)
+        cr = _mfma32(dup(xl), k1) + _mfma32(dup(Wh), dup(xl)) + _mfma32(dup(Wl), dup(xh)) + _mfma32(dup(Wl), k1)
+        ll = _mfma32(dup(Wl), dup(xl))
+        S = int((np.asarray(W, np.int64) * np.asarray(x, np.int64)).sum())
+        lo = (cr << 8) + ll
+        assert 65536 * hh + lo == 2 * S
+        assert abs(hh) < 2 ** 20 and abs(cr) < 2 ** 22 and abs(ll) < 2 ** 20 and abs(lo) < 2 ** 31
+        for d in (0, 1, 5, 16, 17, 33, 47):
+            assert (2 * S) >> (d + 1) == S >> d

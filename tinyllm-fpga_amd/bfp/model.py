@@ -17,6 +17,7 @@ from .dims import Dims
 
 STAGES = ("N1", "Q", "K", "V", "ATTN", "O", "H1", "N2", "G", "U", "MLP", "D", "HOUT")
 TRACE_LAYER = 20   # stage-trace stamps per (step, layer), bfp_decode_trace
+PIPE_TRACE_JOBS, PIPE_TRACE_W = 1024, 8   # the pipelined step's trace: job slots per workgroup, words each
 WHICH = {"Wq": 0, "Wk": 1, "Wv": 2, "Wo": 3, "Wg": 4, "Wu": 5, "Wd": 6, "g1": 7, "g2": 8,
          "embed": 9, "norm_w": 10}
 
@@ -248,7 +249,7 @@ class BfpModel:
 
     # --------------------------------------------------------------- decode
     def decode(self, prompts, n_gen, hist=False, graph=True, step_times=False, rtl_loop=False,
-               persist=True, trace=False, abort_test=False):
+               persist=True, trace=False, abort_test=False, pipe=None):
         """Greedy decode (full.py:426-443) of a batch of prompts
         (batch, n_prompt).  Returns (tokens (batch, n_gen), hist) where hist
         is None or (m (batch, steps, NL, D), e (batch, steps, NL, D/16)).
@@ -259,8 +260,11 @@ class BfpModel:
         prediction, (batch, n_prompt + n_gen).
 
         persist=False keeps batch 1 off the persistent single-launch kernel
-        (decode_path() tells which path the last decode took); trace=True
-        records its stage stamps (decode_trace()).
+        (decode_path() tells which path the last decode took); pipe=True
+        runs batches on the pipelined one-launch step where it covers the
+        dimensions, pipe=False on the per-stage launches, None leaves the
+        choice to the library (decode_form() tells which ran); trace=True
+        records the stage stamps (decode_trace()).
 
         abort_test=True is a test hook: the decode's abort word is set before
         its first launch, so its bounded waits give up, the kernels run to
@@ -276,7 +280,8 @@ class BfpModel:
             hm = np.zeros((batch, steps, d.NL, d.D), np.int16)
             he = np.zeros((batch, steps, d.NL, d.D // 16), np.int8)
         flags = ((0 if graph else 1) | (2 if step_times else 0) | (4 if rtl_loop else 0)
-                 | (0 if persist else 8) | (16 if trace else 0) | (32 if abort_test else 0))
+                 | (0 if persist else 8) | (16 if trace else 0) | (32 if abort_test else 0)
+                 | (0 if pipe is None else (128 if pipe else 64)))
         call("bfp_decode", self._h, _p(P), n_prompt, n_gen, batch, _p(toks),
              _p(hm) if hist else None, _p(he) if hist else None, flags)
         return toks[:, :n_out], ((hm, he) if hist else None)
@@ -294,14 +299,17 @@ class BfpModel:
         return {0: "graph", 1: "persist", 2: "eager"}.get(lib().bfp_decode_path(self._h), None)
 
     def decode_form(self):
-        """How the last decode's layers were launched: 'persist', 'single',
-        'multi', or 'mx' followed by '+qkv_attn' (Q|K|V and attention in one
-        launch) and '+norm_fused' (RMSNorms inside the O and D launches)."""
+        """How the last decode's layers were launched: 'persist', 'pipe' (the
+        pipelined batched step), 'single', 'multi', or 'mx' followed by
+        '+qkv_attn' (Q|K|V and attention in one launch) and '+norm_fused'
+        (RMSNorms inside the O and D launches)."""
         f = lib().bfp_decode_form(self._h)
         if f < 0:
             return None
         if f == 16:
             return "persist"
+        if f == 32:
+            return "pipe"
         if f < 2:
             return ("single", "multi")[f]
         return "mx" + ("+qkv_attn" if f & 4 else "") + ("+norm_fused" if f & 8 else "")
@@ -310,14 +318,20 @@ class BfpModel:
         """Stamps (device clock, 100 MHz) of the last decode(trace=True): on
         the persistent path (layer stamps (steps, NL, 20), head stamps
         (steps, 3)) -- layer stamps 0-15 are the stages', 16-19 the first
-        attention job's phases; on the batched matrix-core path the blocks'
-        phase stamps (4 kernels, 1024 blocks, 6) (include/bfp.h,
-        bfp_decode_trace); None when nothing was recorded."""
+        attention job's phases; on the pipelined batched step every job of
+        the last step's launch (workgroups, PIPE_TRACE_JOBS, 8: job code + 1,
+        start, inputs in, end, -, and a matvec's row maxima, tile sums and
+        epilogue stored); on the per-stage
+        matrix-core launches the blocks' phase stamps (4 kernels, 1024
+        blocks, 6) (include/bfp.h, bfp_decode_trace); None when nothing was
+        recorded."""
         n = lib().bfp_decode_trace(self._h, None, 0)
         if n <= 0:
             return None
         out = np.zeros(n, np.uint64)
         lib().bfp_decode_trace(self._h, _p(out), n)
+        if self.decode_form() == "pipe":
+            return out.reshape(-1, PIPE_TRACE_JOBS, PIPE_TRACE_W)
         if self.decode_path() != "persist":
             return out.reshape(4, 1024, 6)
         nl, k = self.dims.NL, TRACE_LAYER

@@ -13,6 +13,7 @@
 #include "bfp_layer.h"
 #include "bfp_mx.h"
 #include "bfp_persist.h"
+#include "bfp_pipe.h"
 
 using namespace bfp;
 
@@ -79,6 +80,19 @@ struct bfp_ctx {
   PersistArgs *pt_args = nullptr;
   unsigned long long *pt_clock = nullptr;
   double *pt_scores = nullptr;   // the long attention form's score exchange
+  // the pipelined batched step (bfp_pipe.hip), made on its first use: its
+  // tagged hand-off words, the layer blocks, the argument block, and one
+  // schedule per batch size
+  unsigned *pp_words = nullptr;
+  size_t pp_nwords = 0;
+  LayerArgs *pp_layers = nullptr;
+  PipeArgs *pp_args = nullptr;
+  struct PipeSched {
+    PipePlan pl;
+    int *role = nullptr, *jstart = nullptr, *jobs = nullptr;
+    bool ok = false;
+  };
+  std::vector<PipeSched> pp_sched;   // by batch size (index batch - 1)
   std::vector<void *> allocs;
   int last_path = -1;   // BFP_PATH_* of the last decode
   int last_form = -1;   // BFP_FORM_* of the last decode
@@ -215,6 +229,95 @@ void stage_lens(const bfp_dims &d, int len[ST_COUNT]) {
 bool persist_enabled() {
   const char *v = getenv("BFP_PERSIST");
   return !(v && v[0] == '0');
+}
+
+// Batches from BFP_PIPE_MIN_BATCH sequences (0, the default: none; the
+// BFP_DECODE_PIPE flag: every batch the plan covers) run each decode step
+// as one pipelined launch (bfp_pipe.hip).
+int pipe_min_batch() {
+  const char *v = getenv("BFP_PIPE_MIN_BATCH");
+  const int n = v ? atoi(v) : 0;
+  return n > 0 ? n : 1 << 30;
+}
+
+// The pipelined step's schedule for `batch` sequences and its buffers, or
+// null (*out) when the plan does not cover the dimensions.
+int pipe_get(bfp_ctx *c, int batch, bfp_ctx::PipeSched **out) {
+  *out = nullptr;
+  const bfp_dims &d = c->d;
+  if ((int)c->pp_sched.size() < c->max_batch) c->pp_sched.resize(c->max_batch);
+  bfp_ctx::PipeSched &ps = c->pp_sched[batch - 1];
+  if (!ps.ok) {
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device));
+    if (!pipe_plan(d, batch, c->max_ctx, cus, ps.pl)) return BFP_OK;
+    BFP_TRY(pipe_prepare(ps.pl));
+    if (!c->pp_words) {
+      c->pp_nwords = pipe_words(d, c->max_batch);
+      const char *cg = getenv("BFP_PIPE_COARSE");
+      if (cg && cg[0] == '1') BFP_TRY(c->alloc((void **)&c->pp_words, c->pp_nwords * 4));
+      else BFP_TRY(c->alloc_fine((void **)&c->pp_words, c->pp_nwords * 4));
+      BFP_TRY(c->alloc((void **)&c->pp_layers, sizeof(LayerArgs) * d.NL));
+      BFP_TRY(c->alloc((void **)&c->pp_args, sizeof(PipeArgs)));
+      std::vector<LayerArgs> la(d.NL);
+      for (int l = 0; l < d.NL; ++l) la[l] = layer_args(c, l, c->max_batch);
+      HIP_TRY(hipMemcpy(c->pp_layers, la.data(), sizeof(LayerArgs) * d.NL, hipMemcpyHostToDevice));
+    }
+    BFP_TRY(c->alloc((void **)&ps.role, sizeof(int) * ps.pl.role.size()));
+    BFP_TRY(c->alloc((void **)&ps.jstart, sizeof(int) * ps.pl.jstart.size()));
+    BFP_TRY(c->alloc((void **)&ps.jobs, sizeof(int) * std::max<size_t>(ps.pl.jobs.size(), 1)));
+    HIP_TRY(hipMemcpy(ps.role, ps.pl.role.data(), sizeof(int) * ps.pl.role.size(), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(ps.jstart, ps.pl.jstart.data(), sizeof(int) * ps.pl.jstart.size(), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(ps.jobs, ps.pl.jobs.data(), sizeof(int) * ps.pl.jobs.size(), hipMemcpyHostToDevice));
+    ps.ok = true;
+  }
+  *out = &ps;
+  return BFP_OK;
+}
+
+// The pipelined step's argument block for this decode (its flags cleared),
+// copied to the device.
+int pipe_args(bfp_ctx *c, const bfp_ctx::PipeSched &ps, int batch, int16_t *dhm, int8_t *dhe, int steps,
+              unsigned long long *trace) {
+  const bfp_dims &d = c->d;
+  hipStream_t s = c->stream;
+  PipeArgs pa{};
+  pa.L = c->pp_layers;
+  pa.D = d.D;
+  pa.FFN = d.FFN;
+  pa.KV = d.H_KV * d.HD;
+  pa.NL = d.NL;
+  pa.H_Q = d.H_Q;
+  pa.batch = batch;
+  pa.ngrp = ps.pl.ngrp;
+  pa.nq16 = (d.D + 2 * pa.KV) / 16;
+  pa.nd16 = d.D / 16;
+  pa.nf16 = d.FFN / 16;
+  pa.state = c->state;
+  pa.h_m = c->h_m;
+  pa.h_e = c->h_e;
+  const size_t B = c->max_batch, D = d.D, nq = D + 2 * (size_t)pa.KV;
+  unsigned *w = c->pp_words;
+  pa.w_h = w;
+  pa.w_x1 = (w += B * D);
+  pa.w_qkv = (w += B * D);
+  pa.w_att = (w += B * nq);
+  pa.w_h1 = (w += B * D);
+  pa.w_x2 = (w += B * D);
+  pa.w_mlp = (w += B * D);
+  pa.abort_flag = c->t_abort;
+  pa.role = ps.role;
+  pa.jstart = ps.jstart;
+  pa.jobs = ps.jobs;
+  pa.hist_m = dhm;
+  pa.hist_e = dhe;
+  pa.hist_steps = dhm ? steps : 0;
+  pa.trace = trace;
+  // no word of an earlier decode may carry a tag of this one
+  HIP_TRY(hipMemsetAsync(c->pp_words, 0, c->pp_nwords * 4, s));
+  HIP_TRY(hipMemcpyAsync(c->pp_args, &pa, sizeof pa, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipStreamSynchronize(s));   // pa is a stack copy
+  return BFP_OK;
 }
 
 // The whole batch-1 decode as one persistent launch (bfp_persist.hip).
@@ -1075,11 +1178,24 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     return decode_copy_out(c, batch, steps, n_out, dout, tokens_out, dhm, dhe, hist_m, hist_e);
   }
   c->last_path = (flags & BFP_DECODE_NO_GRAPH) ? BFP_PATH_EAGER : BFP_PATH_GRAPH;
-  // traced batched decode: the matrix-core blocks' phase stamps
+  // the pipelined step (one launch for the step's layers) unless the
+  // per-stage launches are asked for or traced
+  bfp_ctx::PipeSched *pipe = nullptr;
+  if (((flags & BFP_DECODE_PIPE) || batch >= pipe_min_batch()) && !(flags & BFP_DECODE_NO_PIPE))
+    BFP_TRY(pipe_get(c, batch, &pipe));
   c->trace.clear();
+  // traced pipelined step: every job's stamps of the last step's launch
+  unsigned long long *pptr = nullptr;
+  const size_t npp = pipe ? (size_t)pipe->pl.grid * PIPE_TRACE_JOBS * PIPE_TRACE_W : 0;
+  if (pipe && (flags & BFP_DECODE_TRACE)) {
+    BFP_TRY(tmp.alloc((void **)&pptr, npp * sizeof(unsigned long long)));
+    HIP_TRY(hipMemsetAsync(pptr, 0, npp * sizeof(unsigned long long), s));
+  }
+  if (pipe) BFP_TRY(pipe_args(c, *pipe, batch, dhm, dhe, steps, pptr));
+  // traced batched decode: the matrix-core blocks' phase stamps
   unsigned long long *mxtr = nullptr;
   const size_t nmx = (size_t)MX_TRACE_KERNELS * MX_TRACE_BLOCKS * MX_TRACE_STAMPS;
-  if (flags & BFP_DECODE_TRACE) {
+  if (!pipe && (flags & BFP_DECODE_TRACE)) {
     BFP_TRY(tmp.alloc((void **)&mxtr, nmx * sizeof(unsigned long long)));
     HIP_TRY(hipMemsetAsync(mxtr, 0, nmx * sizeof(unsigned long long), s));
     BFP_TRY(set_mx_trace(mxtr));
@@ -1098,7 +1214,11 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
   // A step: the layers, the head, then k_ctl_embed (the token loop, the step
   // increment and the next step's embedding); step 0's embedding goes first.
   auto enqueue_step = [&](bool head) -> int {
-    for (int l = 0; l < d.NL; ++l) {
+    if (pipe) {
+      BFP_TRY(launch_pipe_step(pipe->pl, c->pp_args, s));
+      c->last_form = BFP_FORM_PIPE;
+    }
+    for (int l = 0; l < d.NL && !pipe; ++l) {
       LayerArgs a = layer_args(c, l, batch);
       a.pos_ptr = c->state;
       a.hist_m = dhm;
@@ -1181,6 +1301,11 @@ int bfp_decode(bfp_ctx *c, const int32_t *prompt, int n_prompt, int n_gen, int b
     if (mxtr) {
       c->trace.resize(nmx);
       hipError_t e = hipMemcpy(c->trace.data(), mxtr, nmx * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+      if (e != hipSuccess) rc = set_err(BFP_EIO, "decode trace: %s", hipGetErrorString(e));
+    }
+    if (pptr) {
+      c->trace.resize(npp);
+      hipError_t e = hipMemcpy(c->trace.data(), pptr, npp * sizeof(unsigned long long), hipMemcpyDeviceToHost);
       if (e != hipSuccess) rc = set_err(BFP_EIO, "decode trace: %s", hipGetErrorString(e));
     }
     c->step_ms.clear();

@@ -35,6 +35,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "bfp_device.h"
 
 namespace bfp {
@@ -63,6 +65,54 @@ __device__ __forceinline__ int mx_sum8(const uint4 w) {
 __device__ __forceinline__ mx_v4 mx_mfma(long a, long b, mx_v4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
+
+// The select-free form of one tile's sums (the pipelined batched step,
+// bfp_pipe.hip, whose weights are split once per layer).  Every operand carries the tile
+// in both k copies, so each 32-deep product is twice the tile's; only the
+// per-lane constant k1 (ones in the first copy, zeros in the second) counts
+// once.  With P the 32-deep sum and sum x = 256 sum xh + sum xl' + 2048,
+//   2 S = 65536 (P(Wh, xh) + P(Wh, k1) + P(k1, xh) + 8)
+//         + 256 (P(Wh, xl') + P(Wl', xh) + P(Wl', k1) + P(k1, xl'))
+//         + P(Wl', xl')
+// and floor(S / 2^d) = floor(2S / 2^(d+1)).  |hh| < 2^20 and the low part
+// lo = 256 cr + ll fits 31 bits (tests/test_mx_split.py).  The two input
+// sums P(k1, xh) + 8, P(k1, xl') are one pair per tile (mx_xsum), the
+// initial accumulators of every chunk's hh and cr (8 is an inline operand
+// of the product; 2^19 as the low sum's start would be a register copy per
+// tile).
+__device__ __forceinline__ long mx_k1() { return (threadIdx.x & 63) < 32 ? 0x0101010101010101L : 0L; }
+__device__ __forceinline__ void mx_xsum(long xh, long xl, long k1, mx_v4 &sh, mx_v4 &sl) {
+  const mx_v4 zero = {0, 0, 0, 0}, c8 = {8, 8, 8, 8};
+  sh = mx_mfma(k1, xh, c8);
+  sl = mx_mfma(k1, xl, zero);
+}
+__device__ __forceinline__ void mx_tile2(long wh, long wl, long xh, long xl, long k1, const mx_v4 &sh,
+                                         const mx_v4 &sl, mx_v4 &hh, mx_v4 &lo) {
+  const mx_v4 zero = {0, 0, 0, 0};
+  hh = mx_mfma(wh, xh, sh);
+  mx_v4 cr = mx_mfma(wh, xl, sl);
+  const mx_v4 ll = mx_mfma(wl, xl, zero);
+  hh = mx_mfma(wh, k1, hh);
+  cr = mx_mfma(wl, xh, cr);
+  cr = mx_mfma(wl, k1, cr);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) lo[v] = (cr[v] << 8) + ll[v];
+}
+// floor(S / 2^d) of a tile from (hh, lo) of mx_tile2 with q = d + 1; WIN:
+// 0 past the engine's 47-bit window (d > ALIGN_MAX), without a branch (a
+// wave whose every (tile, output) lies inside the window skips the test).
+template <bool WIN>
+__device__ __forceinline__ long long mx_align2(int hh, int lo, int q) {
+  const long long s2 = ((long long)hh << 16) + lo;
+  if constexpr (!WIN) return s2 >> q;
+  const long long t = s2 >> (q & 63);
+  return q <= ALIGN_MAX + 1 ? t : 0;
+}
+
+// (The per-stage launches keep the form above with the second copy zeroed:
+// there the blocks are bound by the matrix cores, and the select-free form's
+// eight products a tile instead of five made G/U 5.5 -> 6.7 us and D
+// 4.0 -> 5.3 us of tile sums at batch 64.)
 
 // Phase stamps of a traced batched decode (100 MHz clock, thread 0 of each
 // block): MX_TRACE_STAMPS per block -- 0 entry, 1 exponents staged, 2 M
