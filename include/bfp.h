@@ -373,8 +373,8 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
  * workgroup per compute unit; the sequences pass the stages in groups of 16,
  * the stages handing over through device-coherent memory), when the
  * dimensions allow it (HD = 64, D <= 640, FFN <= 1536, D and FFN multiples of
- * 64, NL <= 32, a KV capacity of at most 512, the Q|K|V, O, G/U and D chunks
- * of a layer within the compute units).  BFP_DECODE_PIPE asks for it at any
+ * 64, NL <= 32, at most 4 query heads per KV group, a KV capacity of at most
+ * 256, the Q|K|V, O, G/U and D chunks of a layer within the compute units).  BFP_DECODE_PIPE asks for it at any
  * batch size; without it, batches of at least BFP_PIPE_MIN_BATCH sequences
  * (environment; unset or 0: none) take it; BFP_DECODE_NO_PIPE keeps the
  * per-stage launches.  Both give identical outputs. */

@@ -186,6 +186,11 @@ LayerArgs layer_args(bfp_ctx *c, int layer, int batch) {
   a.max_ctx = c->max_ctx;
   a.batch = batch;
   a.inv_sqrt_hd_div = sqrt((double)d.HD);
+  {
+    int ex = 0;   // score_mul is exact only for a power-of-two divisor (check_dims: HD = 64)
+    if (frexp(a.inv_sqrt_hd_div, &ex) != 0.5) abort();
+    a.score_mul = 1.0 / a.inv_sqrt_hd_div;
+  }
   a.w_qkv_m = reinterpret_cast<const uint4 *>(c->qkv_m + layer * c->s_qkv_m);
   a.w_qkv_e = c->qkv_e + layer * c->s_qkv_e;
   a.w_o_m = reinterpret_cast<const uint4 *>(c->o_m + layer * c->s_o_m);
@@ -288,6 +293,7 @@ int pipe_args(bfp_ctx *c, const bfp_ctx::PipeSched &ps, int batch, int16_t *dhm,
   pa.KV = d.H_KV * d.HD;
   pa.NL = d.NL;
   pa.H_Q = d.H_Q;
+  pa.H_KV = d.H_KV;
   pa.batch = batch;
   pa.ngrp = ps.pl.ngrp;
   pa.nq16 = (d.D + 2 * pa.KV) / 16;

@@ -20,6 +20,12 @@ struct StageDump {
 struct LayerArgs {
   int D, H_Q, H_KV, HD, FFN, KV, max_ctx, batch;
   double inv_sqrt_hd_div;   // math.sqrt(HD), the divisor of the scores
+  // 1 / math.sqrt(HD), exact: sqrt(HD) is a power of two (HD = 64: 8), so
+  // score / sqrt(HD) == score * score_mul for every score (both round the
+  // same real, a power-of-two scaling of the score, subnormals included)
+  // and the kernels multiply instead of dividing (a float64 division is a
+  // sequence of about ten instructions per score)
+  double score_mul;
   // weights of this layer, device layout
   const uint4 *w_qkv_m;     // (D + 2KV) x D   rows: q | k | v
   const int8_t *w_qkv_e;

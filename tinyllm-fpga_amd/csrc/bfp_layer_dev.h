@@ -671,14 +671,14 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
         const double sl = (t01 + peer<8>(f)) + f;
         const double s2 = sl + peer<2>(sl);
         const double tot = s2 + peer<1>(s2);
-        if (j == 31 && t < n) sc[t] = tot / a.inv_sqrt_hd_div;
+        if (j == 31 && t < n) sc[t] = tot * a.score_mul;
       }
     }
   } else if constexpr (SHORT) {
     // contexts of at most NT positions: one row per thread, the one in
     // flight since the RoPE phase
-    if (tid < n) sc[tid] = ddot64_skx_bfp(q, kr[0].m, kr[0].e4) / a.inv_sqrt_hd_div;
-    if (tid == pos) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
+    if (tid < n) sc[tid] = ddot64_skx_bfp(q, kr[0].m, kr[0].e4) * a.score_mul;
+    if (tid == pos) sc[pos] = ddot64_skx(q, kc) * a.score_mul;
   } else {
     // passes of KR rows per thread: rows t = RS u + r0, u = u0 + tid + j*NT;
     // kr[0] of the next pass is loaded as soon as this pass's kr[0] is
@@ -693,7 +693,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
 #pragma unroll
       for (int j = 0; j < KR; ++j) {
         const int t = RS * (u0 + tid + j * NT) + r0;
-        const double sj = ddot64_skx_bfp(q, kr[j].m, kr[j].e4) / a.inv_sqrt_hd_div;
+        const double sj = ddot64_skx_bfp(q, kr[j].m, kr[j].e4) * a.score_mul;
         if (j == 0) {
           const int tn = t + RS * KR * NT;
           load_krow(io, kr[0], Km, Ke, ((long long)(tn < n ? tn : last) * a.H_KV + g) * HD);
@@ -702,7 +702,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
       }
     }
     // row pos from LDS, by the thread that scored it from the cache
-    if ((pos - r0) % RS == 0 && tid == ((pos - r0) / RS) % NT) sc[pos] = ddot64_skx(q, kc) / a.inv_sqrt_hd_div;
+    if ((pos - r0) % RS == 0 && tid == ((pos - r0) / RS) % NT) sc[pos] = ddot64_skx(q, kc) * a.score_mul;
     if constexpr (RS > 1) {
       // exchange: publish this workgroup's rows, then read the other
       // workgroups' (the same q, K rows and ddot order, so the same bits)

@@ -23,14 +23,15 @@ constexpr int PIPE_MAX_LAYERS = 32, PIPE_MAX_GROUPS = 128;
 // A job: (layer << 26) | (stage << 23) | (group << 16) | index, where index
 // is the sequence (RMSNorms), the chunk (matvecs: q|k|v, O and D 16-row
 // chunks; G/U the FFN chunk whose G and U halves are adjacent chunks of the
-// interleaved block), or sequence * H_Q + head (attention).
+// interleaved block), or sequence * H_KV + KV group (attention: every query
+// head of the group).
 inline int pipe_job(int layer, int stage, int g, int idx) {
   return (layer << 26) | (stage << 23) | (g << 16) | idx;
 }
 
 struct PipeArgs {
   const LayerArgs *L;          // NL layer blocks (device memory): weights, gammas, RoPE, KV cache
-  int D, FFN, KV, NL, H_Q, batch, ngrp;
+  int D, FFN, KV, NL, H_Q, H_KV, batch, ngrp;
   int nq16, nd16, nf16;        // 16-row chunks of q|k|v, of D, of FFN
   const int *state;            // state[0]: the step (its position)
   // BFP (batch-major): layer 0's input, which k_ctl_embed stores, and the
@@ -53,7 +54,8 @@ struct PipeArgs {
   // job code + 1, then the 100 MHz clock at the job's start,
   // when its inputs were in (LDS), and when its outputs were stored; a matvec
   // job also stamps its row maxima (5), its tile sums (6) and its
-  // epilogue's stores issued (7)
+  // epilogue's stores issued (7), an attention job its RoPE and cache row
+  // (4), scores (5), softmax (6) and AV chains (7)
   unsigned long long *trace;
 };
 constexpr int PIPE_TRACE_JOBS = 1024, PIPE_TRACE_W = 8;

@@ -17,9 +17,11 @@
 //   G/U chunk c    nf16               G and U chunks + SwiGLU -> mlp
 //   D chunk c      nd16               the chunk + residual -> h
 //   (any)                             RMSNorm 1 / 2 of one sequence, and the
-//                                     attention of one (head, sequence),
-//                                     spread over the workgroups by the
-//                                     host's schedule (pipe_plan)
+//                                     attention of one (KV group, sequence):
+//                                     all the group's query heads
+//                                     (bfp_attn_grp.h), spread over the
+//                                     workgroups by the host's schedule
+//                                     (pipe_plan)
 //
 // Group g runs stage s of layer L at beat 7L + s + g.  Every dependency of a
 // job lies on an earlier beat and each workgroup runs its jobs in beat
@@ -53,6 +55,7 @@
 #include <vector>
 
 #include "bfp.h"
+#include "bfp_attn_grp.h"
 #include "bfp_coh.h"
 #include "bfp_device.h"
 #include "bfp_f64.h"
@@ -68,19 +71,22 @@ namespace bfp {
 constexpr int PP_NW = PIPE_THREADS / 64;
 constexpr int PP_TPW_D = 5;    // input tiles per wave of a D-input chunk (D <= 640)
 constexpr int PP_TPW_F = 12;   // of an FFN-input chunk (FFN <= 1536)
+constexpr int PP_AV_ROWS = 64; // AV product rows per head in LDS (one workgroup a CU)
 
 // ------------------------------------------------------------ hand-off
 // The tagged words q = tid + k * PIPE_THREADS < nq (16-byte quads of r),
 // NQ per thread: every thread's loads are issued together, then each quad
 // that does not carry the tag yet is polled on its own (bounded); put(q, v)
-// receives each quad.
-template <int NQ, class Put>
+// receives each quad.  (Ordinary first loads, re-polling only the words
+// without the tag at the device-coherent level, left a stale copy cached
+// that the re-polls kept returning: the waits gave up.)
+template <int NQ, int POL = CPOL_SC1, class Put>
 __device__ __forceinline__ void pp_poll_quads(Wait &w, rsrc_t r, int nq, unsigned tag, Put put) {
   uint4 v[NQ];
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
     const int q = threadIdx.x + k * PIPE_THREADS;
-    v[k] = ld_b128<CPOL_SC1>(r, 16 * (q < nq ? q : nq - 1));
+    v[k] = ld_b128<POL>(r, 16 * (q < nq ? q : nq - 1));
   }
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
@@ -350,6 +356,7 @@ struct AttnPipeIO {
   unsigned long long *tr;          // traced launch: this job's stamps
   __device__ __forceinline__ void mark(int k) const {
     if (k == ATT_MARK_QKV) pp_clock(tr, 2);   // wave 0's q|k|v input in
+    else pp_clock(tr, 4 + k);                 // RoPE, scores, softmax, AV chains done
   }
   __device__ __forceinline__ void rope_cs(const double *cs, int j, double &c, double &s) const {
     const uint4 u = ld_b128<0>(rrope, (int)((cs - rope0) + 2 * j) * 8);
@@ -416,9 +423,10 @@ __device__ __forceinline__ void job_norm(const PipeArgs &p, const PT_CONST Layer
   }
 }
 
-// The attention of head hq of sequence b at layer l.
+// The attention of KV group gk (all its query heads) of sequence b at
+// layer l.
 template <int PPW>
-__device__ __forceinline__ void job_attn(const PipeArgs &p, const PT_CONST LayerArgs *LA, Wait &w, int l, int hq,
+__device__ __forceinline__ void job_attn(const PipeArgs &p, const PT_CONST LayerArgs *LA, Wait &w, int l, int gk,
                                          int b, int pos, double *dsm, unsigned long long *tr) {
   const int nq = p.D + 2 * p.KV;
   LayerArgs a = cload(LA + l);
@@ -441,7 +449,7 @@ __device__ __forceinline__ void job_attn(const PipeArgs &p, const PT_CONST Layer
   io.rrope = rsrc(a.rope);
   io.tr = tr;
   lds_barrier();   // the previous job's LDS reads are done
-  attn_body<PPW, true>(a, io, hq, b, [pos] { return make_int2(pos, pos); }, dsm);
+  attn_group_body<PPW, PP_AV_ROWS>(a, io, gk, b, [pos] { return make_int2(pos, pos); }, dsm);
 }
 
 // The epilogue pairs of a block: 16-lane group j (waves 0-3) owns sequence
@@ -605,7 +613,7 @@ __device__ __noinline__ void pipe_role(const PT_CONST PipeArgs *pp, double *dsm,
     if (st == PS_N1 || st == PS_N2) {
       job_norm(p, LA, w, l, idx, st == PS_N1 ? 1 : 2, pos, dsm, tr);
     } else if (st == PS_ATT) {
-      job_attn<PPW>(p, LA, w, l, idx % p.H_Q, idx / p.H_Q, pos, dsm, tr);
+      job_attn<PPW>(p, LA, w, l, idx % p.H_KV, idx / p.H_KV, pos, dsm, tr);
     } else if constexpr (MV) {
       if (fresh) {
         pw_split(W);
@@ -640,18 +648,17 @@ __global__ __launch_bounds__(PIPE_THREADS, 1) void k_pipe_step(const PipeArgs *g
 
 // ------------------------------------------------------------------ host
 typedef void (*pp_fn)(const PipeArgs *);
-static pp_fn pipe_kernel(int ppw) {
-  return ppw == 2 ? k_pipe_step<2> : (ppw == 3 ? k_pipe_step<3> : k_pipe_step<4>);
-}
+static pp_fn pipe_kernel(int ppw) { return ppw == 2 ? k_pipe_step<2> : k_pipe_step<3>; }
 
 int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) {
   const int ppw = attn_ppw(max_ctx);
   const int nq16 = (d.D + 2 * d.H_KV * d.HD) / 16, nd16 = d.D / 16, nf16 = d.FFN / 16;
   const int ngrp = (batch + PIPE_SEQ - 1) / PIPE_SEQ;
   const int roles = nq16 + nd16 + nf16 + nd16;
-  const int NL = d.NL, HQ = d.H_Q, KVC = d.H_KV * d.HD / 16, grp = d.H_Q / d.H_KV;
-  if (d.HD != 64 || ppw > 4 || d.D % 64 || d.FFN % 64 || nd16 > PP_NW * PP_TPW_D ||
-      nf16 > PP_NW * PP_TPW_F || d.D > 2 * PIPE_THREADS || batch < 1 || (long long)batch * d.H_Q > 65535 ||
+  const int NL = d.NL, HKV = d.H_KV, KVC = d.H_KV * d.HD / 16, grp = d.H_Q / d.H_KV;
+  if (d.HD != 64 || ppw > 3 || grp > AG_MAXG || grp + 2 > ATT_WAVES || d.D % 64 || d.FFN % 64 ||
+      nd16 > PP_NW * PP_TPW_D ||
+      nf16 > PP_NW * PP_TPW_F || d.D > 2 * PIPE_THREADS || batch < 1 || (long long)batch * d.H_KV > 65535 ||
       ngrp > PIPE_MAX_GROUPS || roles > cus || NL < 1 || NL > PIPE_MAX_LAYERS)
     return 0;
   pl.batch = batch;
@@ -664,16 +671,18 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
   // group) order; a free workgroup takes its own next matvec job when that
   // is ready, else the oldest ready RMSNorm or attention job.  Each list is
   // in simulated start order, and every job starts after its inputs' jobs
-  // end, so in any run the earliest unfinished job can proceed.
-  const double t_lat = 1.0, t_n = 1.5, t_att = 4.6;
-  const double t_mv[PS_COUNT] = {0, 3.1, 0, 3.4, 0, 5.5, 6.1};
+  // end, so in any run the earliest unfinished job can proceed.  A job's
+  // time is its inputs' poll (once they are complete) plus its work, as
+  // measured with the job trace at config 5.
+  const double t_lat = 0.3, t_n = 2.8, t_att = 8.3;
+  const double t_mv[PS_COUNT] = {0, 4.5, 0, 5.2, 0, 7.2, 10.8};
   struct Job {
     int code = 0, npend = 0;
     double dur = 0.0, ready = 0.0, end = 0.0;
     std::vector<int> out;   // jobs that read this one's outputs
   };
   std::vector<Job> J;
-  // job ids: per (layer, group): N1 ns, QKV nq16, ATT ns*HQ, O nd16, N2 ns, GU nf16, D nd16
+  // job ids: per (layer, group): N1 ns, QKV nq16, ATT ns*HKV, O nd16, N2 ns, GU nf16, D nd16
   std::vector<int> base((size_t)NL * ngrp + 1);
   auto nsg = [&](int g) { return std::min(PIPE_SEQ, batch - g * PIPE_SEQ); };
   {
@@ -681,7 +690,7 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
     for (int l = 0; l < NL; ++l)
       for (int g = 0; g < ngrp; ++g) {
         base[(size_t)l * ngrp + g] = n;
-        n += 2 * nsg(g) + nsg(g) * HQ + nq16 + 2 * nd16 + nf16;
+        n += 2 * nsg(g) + nsg(g) * HKV + nq16 + 2 * nd16 + nf16;
       }
     base[(size_t)NL * ngrp] = n;
     J.resize(n);
@@ -692,11 +701,11 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
     switch (st) {
       case PS_N1: return o + (idx - b0);
       case PS_QKV: return o + ns + idx;
-      case PS_ATT: return o + ns + nq16 + (idx - b0 * HQ);
-      case PS_O: return o + ns + nq16 + ns * HQ + idx;
-      case PS_N2: return o + ns + nq16 + ns * HQ + nd16 + (idx - b0);
-      case PS_GU: return o + 2 * ns + nq16 + ns * HQ + nd16 + idx;
-      default: return o + 2 * ns + nq16 + ns * HQ + nd16 + nf16 + idx;
+      case PS_ATT: return o + ns + nq16 + (idx - b0 * HKV);
+      case PS_O: return o + ns + nq16 + ns * HKV + idx;
+      case PS_N2: return o + ns + nq16 + ns * HKV + nd16 + (idx - b0);
+      case PS_GU: return o + 2 * ns + nq16 + ns * HKV + nd16 + idx;
+      default: return o + 2 * ns + nq16 + ns * HKV + nd16 + nf16 + idx;
     }
   };
   auto dep = [&](int from, int to) { J[from].out.push_back(to); };
@@ -717,13 +726,12 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
         for (int b = b0; b < b1; ++b) dep(id_of(l, PS_N1, g, b), j);
       }
       for (int b = b0; b < b1; ++b)
-        for (int h = 0; h < HQ; ++h) {
-          const int j = id_of(l, PS_ATT, g, b * HQ + h);
-          J[j].code = pipe_job(l, PS_ATT, g, b * HQ + h);
+        for (int kv = 0; kv < HKV; ++kv) {
+          const int j = id_of(l, PS_ATT, g, b * HKV + kv);
+          J[j].code = pipe_job(l, PS_ATT, g, b * HKV + kv);
           J[j].dur = t_att;
-          const int kv = h / grp;
-          for (int k = 0; k < 4; ++k) {   // its q, k and v rows: 64 each
-            dep(id_of(l, PS_QKV, g, 4 * h + k), j);
+          for (int k = 0; k < 4; ++k) {   // its heads' q rows, its k and v rows: 64 each
+            for (int h = kv * grp; h < kv * grp + grp; ++h) dep(id_of(l, PS_QKV, g, 4 * h + k), j);
             dep(id_of(l, PS_QKV, g, nd16 + 4 * kv + k), j);
             dep(id_of(l, PS_QKV, g, nd16 + KVC + 4 * kv + k), j);
           }
@@ -733,7 +741,7 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
         J[j].code = pipe_job(l, PS_O, g, c);
         J[j].dur = t_mv[PS_O];
         for (int b = b0; b < b1; ++b)
-          for (int h = 0; h < HQ; ++h) dep(id_of(l, PS_ATT, g, b * HQ + h), j);
+          for (int kv = 0; kv < HKV; ++kv) dep(id_of(l, PS_ATT, g, b * HKV + kv), j);
       }
       for (int b = b0; b < b1; ++b) {
         const int j = id_of(l, PS_N2, g, b);
@@ -754,7 +762,10 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
         for (int c2 = 0; c2 < nf16; ++c2) dep(id_of(l, PS_GU, g, c2), j);
       }
     }
-  // roles: workgroup of each matvec chunk; its jobs in (layer, group) order
+  // roles: the workgroup of each matvec chunk; its jobs in (layer, group)
+  // order.  (Two workgroups a D chunk taking alternate groups, with the
+  // Q|K|V chunks in pairs to free them, made the simulated step longer: the
+  // stage chain of a group, not the D role, bounds the layer.)
   pl.role.assign(cus, -1);
   std::vector<std::vector<int>> pinned(cus);
   std::vector<size_t> pnext(cus, 0);
@@ -862,7 +873,7 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
   // LDS: the attention's, a matvec job's (inputs, exponents, A and M) and
   // an RMSNorm's
   const int nTmax = std::max(nd16, nf16);
-  const size_t att = attn_lds_bytes(max_ctx, ppw, AttnPipeIO::kAvBlock);
+  const size_t att = attn_grp_lds_bytes(max_ctx, grp, PP_AV_ROWS);
   const size_t mv = ((size_t)16 * nTmax * 32 + 16 * nTmax + 7) / 8 * 8 + (size_t)2 * 256 * 12;
   const size_t nrm = (size_t)(d.D + PW_MAX_LEAVES) * 8 + (size_t)d.D * 2 + nd16;
   pl.lds = (std::max(att, std::max(mv, nrm)) + 15) & ~(size_t)15;
