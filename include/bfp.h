@@ -393,7 +393,10 @@ int bfp_decode_path(const bfp_ctx *ctx);
  * counterpart; for tests and tuning): BFP_FORM_SINGLE (per-sequence stage
  * kernels, batches below 4), BFP_FORM_MULTI (multi-sequence kernels on the
  * vector unit), or BFP_FORM_MX (int8 matrix-core matvecs) with
- * BFP_FORM_QKV_ATTN when Q|K|V and attention ran as one launch and
+ * BFP_FORM_QKV_ATTN when Q|K|V and attention ran as one launch (with
+ * BFP_FORM_ATT_GROUP when its attention workgroups each took a whole KV
+ * group's query heads: contexts of at most 256, the default; the environment
+ * variable BFP_ATT_GROUP=0 keeps one head per workgroup) and
  * BFP_FORM_NORM_FUSED when the RMSNorms ran inside the O and D launches;
  * BFP_FORM_PERSIST for the persistent batch-1 decode, BFP_FORM_PIPE for the
  * pipelined batched step; -1 before any decode. */
@@ -404,6 +407,7 @@ int bfp_decode_path(const bfp_ctx *ctx);
 #define BFP_FORM_NORM_FUSED 8
 #define BFP_FORM_PERSIST 16
 #define BFP_FORM_PIPE 32
+#define BFP_FORM_ATT_GROUP 64
 int bfp_decode_form(const bfp_ctx *ctx);
 /* The stage trace of the last decode run with BFP_DECODE_TRACE on the
  * persistent path: per (step, layer) 20 stamps -- 0/1 Q|K|V input ready /

@@ -63,7 +63,7 @@ def test_batched_decode_abort(gpu):
     d, om, gm = _setup(cfg, seed=32, max_batch=24)
     from bfp import synth
     prompts = np.stack([synth.make_prompt(d, 6, seed=400 + b) for b in range(24)])
-    _abort_then_recover(gm, om, prompts, 8, "graph", "mx+qkv_attn+norm_fused", pipe=False)
+    _abort_then_recover(gm, om, prompts, 8, "graph", "mx+qkv_attn+attn_group+norm_fused", pipe=False)
     gm.close()
 
 

@@ -254,18 +254,22 @@ def test_decode_mid_context(gpu, max_ctx):
     gm.close()
 
 
-def test_decode_ragged_batch_joined_launches(gpu):
+@pytest.mark.parametrize("grouped", [True, False], ids=["kv_group", "one_head"])
+def test_decode_ragged_batch_joined_launches(gpu, grouped, monkeypatch):
     """40 sequences (groups of 16, 16 and 8) on a D=256 model, where the
-    batched decode joins the Q|K|V matvec with the attention and the
-    RMSNorms with the residual matvecs (tagged hand-offs inside a launch):
-    every sequence checked equals its single-sequence decode, and sequence 0
-    the oracle."""
+    batched decode joins the Q|K|V matvec with the attention -- a KV group's
+    query heads per workgroup (the default) or one head each
+    (BFP_ATT_GROUP=0) -- and the RMSNorms with the residual matvecs (tagged
+    hand-offs inside a launch): every sequence checked equals its
+    single-sequence decode, and sequence 0 the oracle."""
+    if not grouped:
+        monkeypatch.setenv("BFP_ATT_GROUP", "0")
     cfg = dict(D=256, H_Q=4, H_KV=2, HD=64, FFN=512, NL=2, MAX_CTX=40, VOCAB=512)
     d, om, gm = _setup(cfg, seed=21, max_batch=40)
     from bfp import synth
     prompts = np.stack([synth.make_prompt(d, 6, seed=300 + b) for b in range(40)])
     toks, _ = gm.decode(prompts, 10, pipe=False)
-    assert gm.decode_form() == "mx+qkv_attn+norm_fused"
+    assert gm.decode_form() == ("mx+qkv_attn+attn_group+norm_fused" if grouped else "mx+qkv_attn+norm_fused")
     for b in (0, 15, 16, 33, 39):
         single, _ = gm.decode(prompts[b:b + 1], 10)
         assert list(single[0]) == list(toks[b]), b

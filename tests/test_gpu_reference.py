@@ -166,7 +166,7 @@ def test_config5_decode_on_gpu(gpu, pipe):
     gm.load_fp32(synth.make_model(d, seed=int(f["seed"])))
     print(f"[gpu-ref] config 5: decoding {B} sequences x {steps} steps", flush=True)
     toks, (hm, he) = gm.decode(prompts, n_gen, hist=True, pipe=pipe)
-    assert gm.decode_form() == ("pipe" if pipe else "mx+qkv_attn+norm_fused")
+    assert gm.decode_form() == ("pipe" if pipe else "mx+qkv_attn+attn_group+norm_fused")
     gm.close()
     for b in range(B):
         got = _digests(hm, he, b, steps, d.NL)

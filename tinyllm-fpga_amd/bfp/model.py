@@ -301,8 +301,9 @@ class BfpModel:
     def decode_form(self):
         """How the last decode's layers were launched: 'persist', 'pipe' (the
         pipelined batched step), 'single', 'multi', or 'mx' followed by
-        '+qkv_attn' (Q|K|V and attention in one launch) and '+norm_fused'
-        (RMSNorms inside the O and D launches)."""
+        '+qkv_attn' (Q|K|V and attention in one launch), '+attn_group' (its
+        attention a KV group per workgroup) and '+norm_fused' (RMSNorms
+        inside the O and D launches)."""
         f = lib().bfp_decode_form(self._h)
         if f < 0:
             return None
@@ -312,7 +313,8 @@ class BfpModel:
             return "pipe"
         if f < 2:
             return ("single", "multi")[f]
-        return "mx" + ("+qkv_attn" if f & 4 else "") + ("+norm_fused" if f & 8 else "")
+        return ("mx" + ("+qkv_attn" if f & 4 else "") + ("+attn_group" if f & 64 else "")
+                + ("+norm_fused" if f & 8 else ""))
 
     def decode_trace(self):
         """Stamps (device clock, 100 MHz) of the last decode(trace=True): on

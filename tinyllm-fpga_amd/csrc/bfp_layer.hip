@@ -24,6 +24,7 @@
 #include "bfp_mv.h"
 #include "bfp_mx.h"
 
+#include "bfp_attn_grp.h"
 #include "bfp_layer_dev.h"
 
 namespace bfp {
@@ -444,10 +445,63 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (PPW == 3 ? 6 : 4)) void k_qkv_attn
   mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
 }
 
+// The same launch with one attention workgroup per (KV group, sequence):
+// all the group's query heads (bfp_attn_grp.h), H_KV x batch workgroups
+// from nblk (group id % H_KV, sequence id / H_KV).
+template <int PPW, int PB, bool TR>
+__global__ __launch_bounds__(64 * ATT_WAVES, 2) void k_qkv_attng_mx(LayerArgs a, int nblk) {
+  extern __shared__ double dsm[];
+  const int nq = a.D + 2 * a.KV;
+  const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
+  if ((int)blockIdx.x >= nblk) {
+    const int L = blockIdx.x - nblk, gk = L % a.H_KV, b = L / a.H_KV;
+    AttnTagIO io{{a.qkv_m + b * nq, a.qkv_e + b * (nq / 16), a.att_m + b * a.D, a.att_e + b * (a.D / 16)},
+                 tw_make(a.t_qkv + (long long)b * nq, nq * 4), tw_make(a.t_abort, 4), tag};
+    attn_group_body<PPW, PB>(a, io, gk, b, [&] { return make_int2(cur_kv_pos(a), cur_pos(a)); }, dsm);
+    return;
+  }
+  const int nT = a.D / 16, bq = nq / 16, c = blockIdx.x % bq, b0 = blockIdx.x / bq * MX_SEQ;
+  const int ns = min(MX_SEQ, a.batch - b0);
+  int8_t *mx_ex = reinterpret_cast<int8_t *>(dsm);
+  long long *Ao = reinterpret_cast<long long *>(mx_ex + mx_lds_bytes(1, nT));   // 32 nT bytes
+  int *Mo = reinterpret_cast<int *>(Ao + 16 * MX_SEQ);
+  mx_block<1>(a.w_qkv_m + (long long)c * nT * 32, a.w_qkv_e + (long long)c * nT * 16, nT,
+              a.xn_m + (long long)b0 * a.D, a.xn_e + (long long)b0 * nT, ns, Ao, Mo, mx_ex, mx_tr<TR>(a, MX_K_QKV));
+  BFP_MX_EPI(MX_SEQ, {
+    const int q_ = r_ * MX_SEQ + j_;
+    (void)cc_;
+    epi_qkv(a, b, c, mx_A(Ao, q_), Mo[q_], wr_, tag);
+  })
+  mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
+}
+// AV product rows per head in LDS: 16 keeps two workgroups a CU (config 5
+// 35.63k tokens/s against 35.38k with 32 rows and one a CU)
+constexpr int ATTG_PB = 16;
+// BFP_ATT_GROUP=0 keeps the one-head-per-workgroup form (read per launch).
+static int att_group_env() {
+  const char *v = getenv("BFP_ATT_GROUP");
+  return v ? atoi(v) : 1;
+}
+
 typedef void (*qa_fn)(LayerArgs, int);
 static qa_fn qkv_attn_kernel(int ppw, bool tr = false) {
   if (tr) return ppw == 2 ? k_qkv_attn_mx<2, true> : (ppw == 3 ? k_qkv_attn_mx<3, true> : k_qkv_attn_mx<4, true>);
   return ppw == 2 ? k_qkv_attn_mx<2, false> : (ppw == 3 ? k_qkv_attn_mx<3, false> : k_qkv_attn_mx<4, false>);
+}
+static qa_fn qkv_attng_kernel(int ppw, bool tr) {
+  if (tr) return ppw == 2 ? k_qkv_attng_mx<2, ATTG_PB, true> : k_qkv_attng_mx<3, ATTG_PB, true>;
+  return ppw == 2 ? k_qkv_attng_mx<2, ATTG_PB, false> : k_qkv_attng_mx<3, ATTG_PB, false>;
+}
+// Grouped attention in the joined launch: the lane-split short forms, at
+// most AG_MAXG heads a group (and BFP_ATT_GROUP set).
+static bool mx_attn_grouped(const LayerArgs &a) {
+  const int grp = a.H_Q / a.H_KV;
+  return att_group_env() && attn_ppw(a.max_ctx) <= 3 && grp <= AG_MAXG && grp + 2 <= ATT_WAVES;
+}
+inline size_t qkv_attng_lds(const LayerArgs &a) {
+  const size_t sha = attn_grp_lds_bytes(a.max_ctx, a.H_Q / a.H_KV, ATTG_PB);
+  const size_t shq = (size_t)mx_lds_bytes(1, a.D / 16) + 16 * MX_SEQ * 12;
+  return sha > shq ? sha : shq;
 }
 inline size_t qkv_attn_lds(const LayerArgs &a) {
   const size_t sha = attn_lds_bytes(a.max_ctx, attn_ppw(a.max_ctx), AttnPlainIO::kAvBlock);
@@ -977,6 +1031,15 @@ int prepare_layer_kernels(int max_ctx, int D, int FFN) {
     BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(qkv_attn_kernel(ppw)), (int)qkv_attn_lds(la)));
     BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(qkv_attn_kernel(ppw, true)), (int)qkv_attn_lds(la)));
   }
+  if (ppw <= 3) {   // the grouped form, for up to AG_MAXG heads a group
+    LayerArgs la{};
+    la.max_ctx = max_ctx;
+    la.D = D;
+    la.H_Q = AG_MAXG;
+    la.H_KV = 1;
+    for (bool tr : {false, true})
+      BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(qkv_attng_kernel(ppw, tr)), (int)qkv_attng_lds(la)));
+  }
   int nw, tpt, nwf, tptf;
   shape_for(D / 16, nw, tpt);
   shape_for(FFN / 16, nwf, tptf);
@@ -1042,6 +1105,7 @@ int layer_form(const LayerArgs &a) {
   if (!(a.batch >= MULTI_MIN_BATCH && a.xn_m)) return BFP_FORM_SINGLE;
   if (a.batch < MX_MIN_BATCH) return BFP_FORM_MULTI;
   return BFP_FORM_MX | (mx_joined_qkv_attn(a) ? BFP_FORM_QKV_ATTN : 0) |
+         (mx_joined_qkv_attn(a) && mx_attn_grouped(a) ? BFP_FORM_ATT_GROUP : 0) |
          (mx_fused_norms(a) ? BFP_FORM_NORM_FUSED : 0);
 }
 
@@ -1052,7 +1116,11 @@ static int launch_layer_mx(const LayerArgs &a, hipStream_t s, bool mx_traced) {
   const bool fused = mx_fused_norms(a);
   const bool tr = mx_traced;
   if (!(fused && a.layer > 0)) launch_norm_seq(a, 1, s);   // else the last layer's D launch ran it
-  if (mx_joined_qkv_attn(a)) {
+  if (mx_joined_qkv_attn(a) && mx_attn_grouped(a)) {
+    // Q|K|V + attention by KV group in one launch
+    hipLaunchKernelGGL(qkv_attng_kernel(attn_ppw(a.max_ctx), tr), dim3(bq * G + a.H_KV * a.batch),
+                       dim3(64 * ATT_WAVES), qkv_attng_lds(a), s, a, bq * G);
+  } else if (mx_joined_qkv_attn(a)) {
     // Q|K|V + attention in one launch (batched decode, short forms)
     hipLaunchKernelGGL(qkv_attn_kernel(attn_ppw(a.max_ctx), tr), dim3(bq * G + a.H_Q * a.batch),
                        dim3(64 * ATT_WAVES), qkv_attn_lds(a), s, a, bq * G);
