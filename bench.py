@@ -154,6 +154,12 @@ def parse():
     ap.add_argument("--decode-trace-batch", action="store_true",
                     help="with --decode-only: config 5 once with the matrix-core blocks' phase "
                          "stamps (the last layer of the last step) and report their medians")
+    ap.add_argument("--batch64-pipe", action="store_true",
+                    help="with --decode-only: also run config 5 on the pipelined step (one "
+                         "launch per step) and record it as batch64_pipelined")
+    ap.add_argument("--decode-trace-pipe", action="store_true",
+                    help="with --decode-only: config 5 once on the pipelined step with its job "
+                         "stamps (the last step) and report per-stage medians")
     ap.add_argument("--decode-trace-long", action="store_true",
                     help="with --decode-only: the same stage stamps for config 4 (the long "
                          "attention form), medians over positions 1984-2047")
@@ -500,6 +506,69 @@ def batch_trace_leg():
     return {"form": form, "step": f"{n_prompt + n_gen - 1} (last layer)", "kernels_us": out}
 
 
+PIPE_STAGES = ("N1", "QKV", "ATT", "O", "N2", "GU", "D")
+
+
+def pipe_trace_leg(n_gen=128):
+    """Config 5 once on the pipelined step with its job stamps (the last
+    step's launch: every job's start, inputs in LDS, end, and per kind its
+    phases), summarised per stage in us: jobs, median and 90th percentile of
+    the wait (start to inputs in) and of the work (inputs in to end); the
+    matrix-core jobs' phases (inputs to row maxima, to tile sums, to the
+    epilogue's stores, to the end) and the attention jobs' (start to q|k|v
+    in, RoPE, scores, softmax, AV chains, outputs); the launch's span and
+    the workgroups' busy fraction (work over span)."""
+    import numpy as np
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    B, n_prompt = 64, 8
+    d = Dims(MAX_CTX=n_prompt + 128)
+    gm = BfpModel(d, max_batch=B)
+    gm.load_fp32(synth.make_model(d, seed=0))
+    prompts = np.stack([synth.make_prompt(d, n_prompt, seed=0)] +
+                       [synth.make_prompt(d, n_prompt, seed=1000 + b) for b in range(1, B)])
+    gm.decode(prompts, 4, pipe=True)
+    gm.decode(prompts, n_gen, trace=True, pipe=True)
+    form = gm.decode_form()
+    _, g = gm.decode_time_ms()
+    tr = gm.decode_trace()
+    gm.close()
+    if form != "pipe" or tr is None:
+        return {"form": form, "stages": None}
+    tr = tr.astype(np.int64)
+    used = tr[:, :, 0] > 0
+    code = tr[:, :, 0] - 1
+    stage = (code >> 23) & 7
+    t0 = tr[:, :, 1][used].min()
+    span = (tr[:, :, 3][used].max() - t0) / 100
+
+    def q(v):
+        return {"med": round(float(np.median(v)), 2), "p90": round(float(np.percentile(v, 90)), 2)}
+    out = {}
+    for k, name in enumerate(PIPE_STAGES):
+        m = used & (stage == k)
+        if not m.any():
+            continue
+        j = tr[m]
+        r = {"jobs": int(m.sum()), "wait": q((j[:, 2] - j[:, 1]) / 100),
+             "work": q((j[:, 3] - j[:, 2]) / 100)}
+        if name in ("QKV", "O", "GU", "D"):
+            ph = np.stack([j[:, 5] - j[:, 2], j[:, 6] - j[:, 5], j[:, 7] - j[:, 6],
+                           j[:, 3] - j[:, 7]], 1) / 100
+            r["phases_med"] = dict(zip(("row maxima", "tile sums", "epilogue stored", "end"),
+                                       [round(float(v), 2) for v in np.median(ph, 0)]))
+        if name == "ATT":
+            ph = np.stack([j[:, 2] - j[:, 1], j[:, 4] - j[:, 2], j[:, 5] - j[:, 4],
+                           j[:, 6] - j[:, 5], j[:, 7] - j[:, 6], j[:, 3] - j[:, 7]], 1) / 100
+            r["phases_med"] = dict(zip(("q|k|v in", "RoPE", "scores", "softmax", "AV", "outputs"),
+                                       [round(float(v), 2) for v in np.median(ph, 0)]))
+        out[name] = r
+    busy = ((tr[:, :, 3] - tr[:, :, 2]) * used).sum(1) / 100 / span
+    return {"form": form, "step": f"{n_prompt + n_gen - 1}", "ms_per_step": round(g / n_gen, 4),
+            "launch_span_us": round(float(span), 1), "workgroups": int(tr.shape[0]),
+            "busy_frac_med": round(float(np.median(busy)), 3), "stages_us": out}
+
+
 def long_context_leg():
     """30 layers, 48-token prompt, greedy decode through
     position 2047 (2000 new tokens); tokens/s overall and per position
@@ -538,10 +607,12 @@ def long_context_leg():
                                                    "the same over positions 1984..2047")}
 
 
-def batch_leg(n_gen=128):
+def batch_leg(n_gen=128, pipe=None):
     """64 independent sequences, 8-token prompts, 128
     greedy tokens each; aggregate tokens/s.  Every sequence's tokens are
-    checked against the reference's own runs (tests/golden/ref_decode_cfg5.npz)."""
+    checked against the reference's own runs (tests/golden/ref_decode_cfg5.npz).
+    pipe=True runs the pipelined step (one launch per step) instead of the
+    per-stage launches."""
     import numpy as np
     from bfp import Dims, synth
     from bfp.model import BfpModel
@@ -551,9 +622,10 @@ def batch_leg(n_gen=128):
     gm.load_fp32(synth.make_model(d, seed=0))
     prompts = np.stack([synth.make_prompt(d, n_prompt, seed=0)] +
                        [synth.make_prompt(d, n_prompt, seed=1000 + b) for b in range(1, B)])
-    gm.decode(prompts, 4)                                # warm-up
-    toks, _ = gm.decode(prompts, n_gen)
+    gm.decode(prompts, 4, pipe=pipe)                     # warm-up
+    toks, _ = gm.decode(prompts, n_gen, pipe=pipe)
     t, g = gm.decode_time_ms()
+    form = gm.decode_form()
     gm.close()
     f = _fixture("ref_decode_cfg5.npz")
     exact = None
@@ -564,6 +636,7 @@ def batch_leg(n_gen=128):
     return {"workload": f"config 5: 64 sequences, prompt 8, {n_gen} greedy tokens each",
             "tokens_per_s": round(B * n_gen / (g * 1e-3), 1),
             "ms_per_step": round(g / n_gen, 4), "all_tokens_match_reference": exact,
+            "form": form,
             "roofline": hbm_roofline(nbytes, g * 1e-3,
                                      "per generated step: 30 layers' BFP weights once + the "
                                      "fp32 embedding once + each sequence's KV rows 0..pos")}
@@ -784,6 +857,9 @@ def main():
         if args.batch64:
             note("config 5 batch 64")
             res["batch64"] = batch_leg(args.batch64_tokens)
+        if args.batch64_pipe:
+            note("config 5 batch 64, pipelined step")
+            res["batch64_pipelined"] = batch_leg(args.batch64_tokens, pipe=True)
         if args.decode_probe:
             note("HBM ceiling probe")
             res["stream_ceiling"] = stream_probe()
@@ -793,6 +869,9 @@ def main():
         if args.decode_trace_batch:
             note("config 5 matrix-core block phase trace")
             res["decode_trace_batch"] = batch_trace_leg()
+        if args.decode_trace_pipe:
+            note("config 5 pipelined-step job trace")
+            res["decode_trace_pipe"] = pipe_trace_leg(args.batch64_tokens)
         if args.decode_trace_long:
             note("config 4 persistent-decode stage trace (positions 1984-2047)")
             res["decode_trace_long"] = decode_trace_leg(long=True)

@@ -129,3 +129,77 @@ def test_wave_scheme_equals_numpy():
             assert np.float64(got).view(np.int64) == np.float64(want).view(np.int64), (D, trial)
     assert _equal_leaves(576) == (8, 72)
     assert _equal_leaves(1536) is None
+
+
+def _wave256_scheme(a):
+    """csrc/bfp_f64.h pairwise_sum_wave256 on 64 lanes: up to three leaves
+    (numpy's split of n > 128, and of a right part longer than 128), lane
+    group k = lane / 8 on leaf k: accumulator j = lane % 8 over the leaf's
+    elements below its last multiple of 8, quad swaps i^1, i^2 and the
+    8-lane half-mirror, then the leftover elements in order (a leaf of
+    fewer than 8: 0.0 plus its elements); lanes 0, 8, 16 combined as
+    L0, L0 + L1 or L0 + (L1 + L2), plus numpy's initial 0.0."""
+    n = len(a)
+    n2, nr, m2 = n, 0, 0
+    if n > 128:
+        n2 = n // 2 - (n // 2) % 8
+        nr = n - n2
+        m2 = nr
+        if nr > 128:
+            m2 = nr // 2 - (nr // 2) % 8
+    lanes, fns, flos = [], [], []
+    for lane in range(64):
+        k, j = lane >> 3, lane & 7
+        flo = 0 if k == 0 else (n2 if k == 1 else n2 + m2)
+        fn = n2 if k == 0 else (m2 if k == 1 else (nr - m2 if k == 2 else 0))
+        top = fn - fn % 8
+        r = a[flo + j] if j < top else 0.0
+        t = flo + 8 + j
+        while t < flo + top:
+            r = r + a[t]
+            t += 8
+        lanes.append(r)
+        fns.append(fn)
+        flos.append(flo)
+
+    def step(partner):
+        return [lanes[i] + lanes[partner(i)] for i in range(64)]
+    lanes = step(lambda i: i ^ 1)
+    lanes = step(lambda i: i ^ 2)
+    lanes = step(lambda i: (i & ~7) | (7 - (i & 7)))
+    res = []
+    for lane in range(64):
+        fn, flo = fns[lane], flos[lane]
+        top = fn - fn % 8
+        if fn < 8:
+            r = 0.0
+            for t in range(fn):
+                r += a[flo + t]
+        else:
+            r = lanes[lane]
+            for t in range(flo + top, flo + fn):
+                r += a[t]
+        res.append(r)
+    root = res[0]
+    if n > 128:
+        root = root + (res[8] + res[16]) if nr > 128 else root + res[8]
+    return 0.0 + root
+
+
+def test_wave256_scheme_equals_numpy():
+    """The one-wave softmax denominator of the grouped attention
+    (tinyllm-fpga_amd/csrc/bfp_attn_grp.h) equals np.add.reduce bit for bit
+    for every n of 1..256 (softmax terms in (0, 1], wide-range and
+    cancelling inputs); n = 255 has three leaves (120, 64, 71)."""
+    rng = np.random.default_rng(12)
+    for n in range(1, 257):
+        for trial in range(6):
+            if trial % 3 == 0:
+                a = np.exp(-np.abs(rng.standard_normal(n)) * 3.0)
+            elif trial % 3 == 1:
+                a = rng.standard_normal(n) * 10.0 ** rng.integers(-8, 8, n)
+            else:
+                a = rng.standard_normal(n)
+            want = np.add.reduce(a)
+            got = _wave256_scheme([float(v) for v in a])
+            assert np.float64(got).view(np.int64) == np.float64(want).view(np.int64), (n, trial)

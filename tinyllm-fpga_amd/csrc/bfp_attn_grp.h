@@ -7,10 +7,12 @@
 // that takes the whole group loads each K row and stages each V row once
 // for all of them: wave h < G rotates q head h, wave G the group's k and
 // wave G + 1 its v; every 32-lane half-wave scores one position against all
-// G heads; wave h runs head h's short softmax and AV add chain.  The
+// G heads; wave h runs head h's softmax and AV add chain.  The
 // arithmetic of each head -- the SkylakeX ddot order of the scores, numpy's
 // softmax and pairwise sum, the ascending-t AV chain -- is attn_body's, so
-// the outputs are bit-identical to the one-head-per-workgroup form.
+// the outputs are bit-identical to the one-head-per-workgroup form (whose
+// softmax past 128 positions is block-wide: here each head's stays in its
+// wave, up to 256).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -25,7 +27,7 @@ constexpr int AG_MAXG = 4;   // query heads per KV group
 // products per head.
 inline size_t attn_grp_lds_bytes(int max_ctx, int G, int PB) {
   const size_t scl = (size_t)((max_ctx + 1) & ~1);
-  return ((size_t)64 * G + 192) * 8 + (size_t)G * scl * 8 + (size_t)2 * ATT_AVC * (64 * 2 + 4) +
+  return ((size_t)64 * G + 128) * 8 + (size_t)G * scl * 8 + (size_t)2 * ATT_AVC * (64 * 2 + 4) +
          (size_t)G * PB * 64 * 8;
 }
 
@@ -50,12 +52,10 @@ __device__ __forceinline__ void attn_group_body(const LayerArgs &a, IO &io, int 
   double *q = dsm;                   // G x 64
   double *kc = dsm + 64 * G;         // 64 (current position, post-rope)
   double *vc = kc + 64;              // 64
-  double *leaf = vc + 64;            // PW_MAX_LEAVES (= 64)
-  double *sc = leaf + 64;            // G x scl: scores, then probabilities
+  double *sc = vc + 64;              // G x scl: scores, then probabilities
   int16_t *vsm = reinterpret_cast<int16_t *>(sc + G * scl);   // 2 x AVC x 64
   int8_t *vse = reinterpret_cast<int8_t *>(vsm + 2 * AVC * 64);  // 2 x AVC x 4
   double *prod = reinterpret_cast<double *>(vse + 2 * AVC * 4);  // G x PB x 64
-  __shared__ double red[ATT_WAVES];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const long long kv_tok = (long long)a.H_KV * HD;   // elements per position
   int16_t *Km = a.k_m + (long long)b * a.max_ctx * kv_tok;
@@ -179,68 +179,41 @@ __device__ __forceinline__ void attn_group_body(const LayerArgs &a, IO &io, int 
   store_v(0);
   lds_barrier();
   io.mark(ATT_MARK_SCORES);
-  // softmax_fp (full.py:245-247) of each head: attn_body's two forms
-  if (n <= 128) {
-    if (w < G) {   // wave h: head h, positions l and l + 64
+  // softmax_fp (full.py:245-247) of each head, wave h on head h: lane l
+  // holds positions l + 64i; numpy's pairwise sum in one wave (at most
+  // three leaves, pairwise_sum_wave256), so the G heads run side by side
+  {
+    constexpr int NV = PPW == 2 ? 2 : 4;   // positions per lane
+    if (w < G) {
       double *sh = sc + w * scl;
-      const double s0 = l < n ? sh[l] : -INFINITY, s1 = l + 64 < n ? sh[l + 64] : -INFINITY;
-      double mx = fmax(s0, s1);
+      double s[NV], e[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) s[i] = l + 64 * i < n ? sh[l + 64 * i] : -INFINITY;
+      double mx = s[0];
+#pragma unroll
+      for (int i = 1; i < NV; ++i) mx = fmax(mx, s[i]);
       mx = fmax(mx, peer<32>(mx));
       mx = fmax(mx, peer<16>(mx));
       mx = fmax(mx, peer<8>(mx));
       mx = fmax(mx, peer<4>(mx));
       mx = fmax(mx, peer<2>(mx));
       mx = fmax(mx, peer<1>(mx));
-      const double e0 = exp_f64(s0 - mx), e1 = exp_f64(s1 - mx);
-      if (l < n) sh[l] = e0;
-      if (l + 64 < n) sh[l + 64] = e1;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (64 * i < n) {   // uniform
+          e[i] = exp_f64(s[i] - mx);
+          if (l + 64 * i < n) sh[l + 64 * i] = e[i];
+        }
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-      double res;
-      if (n < 8) {
-        res = 0.0;
-        for (int t = 0; t < n; ++t) res += sh[t];
-      } else {
-        const int top = n - n % 8, j = l & 7;
-        double r = sh[j];
-        for (int t = 8 + j; t < top; t += 8) r = r + sh[t];
-        r = r + dpp_f64(r, 0xB1);
-        r = r + dpp_f64(r, 0x4E);
-        r = r + dpp_f64(r, 0x141);
-        const long long rb = __double_as_longlong(r);
-        res = __longlong_as_double(
-            (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(rb >> 32), 0) << 32) |
-                        (unsigned)__builtin_amdgcn_readlane((int)(rb & 0xffffffffLL), 0)));
-        for (int t = top; t < n; ++t) res += sh[t];
-      }
-      const double sum = 0.0 + res;
-      if (l < n) sh[l] = e0 / sum;
-      if (l + 64 < n) sh[l + 64] = e1 / sum;
+      const double sum = pairwise_sum_wave256(sh, n);
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (l + 64 * i < n) sh[l + 64 * i] = e[i] / sum;
     }
     lds_barrier();
-  } else {
-    for (int h = 0; h < G; ++h) {
-      double *sh = sc + h * scl;
-      double mx = -INFINITY;
-      for (int t = tid; t < n; t += NT) mx = fmax(mx, sh[t]);
-      mx = fmax(mx, peer<32>(mx));
-      mx = fmax(mx, peer<16>(mx));
-      mx = fmax(mx, peer<8>(mx));
-      mx = fmax(mx, peer<4>(mx));
-      mx = fmax(mx, peer<2>(mx));
-      mx = fmax(mx, peer<1>(mx));
-      if (l == 0) red[w] = mx;
-      lds_barrier();
-      mx = red[0];
-#pragma unroll
-      for (int i = 1; i < ATT_WAVES; ++i) mx = fmax(mx, red[i]);
-      for (int t = tid; t < n; t += NT) sh[t] = exp_f64(sh[t] - mx);
-      lds_barrier();
-      const double sum = pairwise_sum_block(sh, n, leaf);
-      for (int t = tid; t < n; t += NT) sh[t] = sh[t] / sum;
-      lds_barrier();
-    }
   }
   io.mark(ATT_MARK_SOFTMAX);
 

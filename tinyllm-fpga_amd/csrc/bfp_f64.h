@@ -363,6 +363,55 @@ __host__ __device__ inline bool pw_equal_leaves(int n, int &nl, int &L) {
   return nl <= 8 && L % 8 == 0 && L >= 8;
 }
 
+// numpy's add-reduce of a[0..n) (1 <= n <= 256, in LDS) by one wave, every
+// lane returning 0.0 + the sum.  Up to 128 elements are one leaf; above, the
+// range splits at n2 = n/2 rounded down to a multiple of 8 and a right part
+// longer than 128 splits once more, so there are at most three leaves (each
+// of at least 64 elements).  Lane group k = l / 8 sums leaf k: accumulator
+// j = l % 8 over elements j, j + 8, ... below the leaf's last multiple of
+// 8, the ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) tree from the quad swaps and
+// the 8-lane half-mirror (sum_sq_wave's), then the leftover elements in
+// order; a leaf of fewer than 8 (n < 8) is 0.0 plus its elements in order.
+// The leaves combine as numpy nests them: L0, L0 + L1 or L0 + (L1 + L2).
+__device__ __forceinline__ double pairwise_sum_wave256(const double *a, int n) {
+  const int l = threadIdx.x & 63, k = l >> 3, j = l & 7;
+  int n2 = n, nr = 0, m2 = 0;   // leaves [0, n2), [n2, n2 + m2), [n2 + m2, n)
+  if (n > 128) {
+    n2 = n / 2;
+    n2 -= n2 % 8;
+    nr = n - n2;
+    m2 = nr;
+    if (nr > 128) {
+      m2 = nr / 2;
+      m2 -= m2 % 8;
+    }
+  }
+  const int flo = k == 0 ? 0 : (k == 1 ? n2 : n2 + m2);
+  const int fn = k == 0 ? n2 : (k == 1 ? m2 : (k == 2 ? nr - m2 : 0));
+  const int top = fn - fn % 8;
+  double r = j < top ? a[flo + j] : 0.0;
+  for (int t = flo + 8 + j; t < flo + top; t += 8) r = r + a[t];
+  r = r + dpp_f64(r, 0xB1);
+  r = r + dpp_f64(r, 0x4E);
+  r = r + dpp_f64(r, 0x141);
+  double res = r;
+  if (fn < 8) {
+    res = 0.0;
+    for (int t = 0; t < fn; ++t) res += a[flo + t];
+  } else {
+    for (int t = flo + top; t < flo + fn; ++t) res += a[t];
+  }
+  auto lane_val = [&](int src) {
+    const long long b = __double_as_longlong(res);
+    const int lo32 = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), src);
+    const int hi32 = __builtin_amdgcn_readlane((int)(b >> 32), src);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi32 << 32) | (unsigned)lo32));
+  };
+  double root = lane_val(0);
+  if (n > 128) root = nr > 128 ? root + (lane_val(8) + lane_val(16)) : root + lane_val(8);
+  return 0.0 + root;
+}
+
 // tile_quantize of the 16 values held two per lane by an 8-lane group
 // (elements 2j and 2j+1 in lane j of the group): the tile exponent in e and
 // this lane's two mantissas, canonical when `canonical` (the same values as
