@@ -468,13 +468,17 @@ def decode_trace_leg(long=False):
 
 MX_PHASES = ("staging (exponents)", "pass 1 (row maxima)", "pass 2 (tile sums)",
              "A reduction", "epilogue (wave 0)")
+ATT_PHASES = ("q|k|v in (wave 0)", "RoPE, rows staged", "scores", "softmax (wave 0)",
+              "AV chains (wave 0)")
 
 
 def batch_trace_leg():
     """Config 5 once with the matrix-core matvec blocks' phase stamps (the
     last launch of each kernel: the last layer of the last step): per kernel
     the blocks stamped, the spread of their start times, the span from the
-    first start to the last epilogue, and the median of each phase (us)."""
+    first start to the last epilogue, and the median of each phase (us);
+    likewise the attention workgroups of the joined Q|K|V launch (entry to
+    q|k|v in, RoPE and staging, scores, softmax, AV chains)."""
     import numpy as np
     from bfp import Dims, synth
     from bfp.model import BfpModel
@@ -493,6 +497,21 @@ def batch_trace_leg():
         return {"form": form, "kernels": None}
     tr = tr.astype(np.int64)
     out = {}
+    # the joined Q|K|V launch: its matvec blocks first, then the attention
+    # workgroups (one per KV group and sequence), whose rows hold their own
+    # phases
+    nblk = (d.D + 2 * d.H_KV * d.HD) // 16 * ((B + 15) // 16)
+    att = tr[0][nblk:]
+    att = att[att[:, 0] > 0]
+    if "attn_group" in form and len(att):
+        t0 = att[:, 0].min()
+        r = {"workgroups": int(len(att)), "start_spread_us": round(float((att[:, 0].max() - t0) / 100), 2),
+             "span_us": round(float((att[:, 5].max() - t0) / 100), 2)}
+        for j, ph in enumerate(ATT_PHASES):
+            r[ph] = round(float(np.median((att[:, j + 1] - att[:, j]) / 100)), 2)
+        out["attention"] = r
+        tr = tr.copy()
+        tr[0][nblk:] = 0
     for k, name in enumerate(("Q|K|V", "O", "G/U", "D")):
         st = tr[k][tr[k][:, 0] > 0]
         if not len(st):

@@ -361,7 +361,9 @@ int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, dou
 /* Record the device clock (100 MHz) for bfp_decode_trace: on the persistent
  * path as each stage's input becomes ready and as its output is stored, in
  * the first workgroup of each role; on the batched matrix-core path at the
- * phases of every block of the four matvec kernels. */
+ * phases of every block of the four matvec kernels; on the pipelined step
+ * (BFP_DECODE_PIPE) at the start, inputs-in, phases and end of every job of
+ * the last step's launch. */
 #define BFP_DECODE_TRACE 16
 /* Test hook for the bounded waits: the decode's abort word is set after its
  * per-decode clearing and before its first launch, so every wait for
@@ -421,7 +423,15 @@ int bfp_decode_form(const bfp_ctx *ctx);
  * decode on the matrix cores: per kernel (Q|K|V, O, G/U, D), per block (up to
  * 1024), 6 stamps -- entry, exponents staged, row maxima reduced, tile sums
  * formed, sums reduced, epilogue done -- from the last launch of each kernel
- * (0 for blocks that did not run).
+ * (0 for blocks that did not run); in the Q|K|V kernel's rows the grouped
+ * attention workgroups of the joined launch follow its matvec blocks, with
+ * entry, q|k|v in, RoPE and staged rows, scores, softmax and AV chains.
+ * After a pipelined decode: per workgroup
+ * 1024 job slots of 8 stamps -- the job code + 1 ((layer << 26) | (stage <<
+ * 23) | (group << 16) | index; 0 for an unused slot), start, inputs in,
+ * end, then a matvec job's row maxima (5), tile sums (6) and epilogue
+ * stored (7), an attention job's RoPE (4), scores (5), softmax (6) and AV
+ * chains (7) -- from the last step's launch.
  * Copies up to n values and returns how many were recorded (0 if none). */
 int bfp_decode_trace(const bfp_ctx *ctx, uint64_t *out, size_t n);
 

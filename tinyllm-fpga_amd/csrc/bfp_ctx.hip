@@ -259,9 +259,9 @@ int pipe_get(bfp_ctx *c, int batch, bfp_ctx::PipeSched **out) {
     BFP_TRY(pipe_prepare(ps.pl));
     if (!c->pp_words) {
       c->pp_nwords = pipe_words(d, c->max_batch);
-      const char *cg = getenv("BFP_PIPE_COARSE");
-      if (cg && cg[0] == '1') BFP_TRY(c->alloc((void **)&c->pp_words, c->pp_nwords * 4));
-      else BFP_TRY(c->alloc_fine((void **)&c->pp_words, c->pp_nwords * 4));
+      // fine-grained, like the other tagged words (coarse-grained measured the
+      // same: the hand-off loads and stores bypass the L2 either way)
+      BFP_TRY(c->alloc_fine((void **)&c->pp_words, c->pp_nwords * 4));
       BFP_TRY(c->alloc((void **)&c->pp_layers, sizeof(LayerArgs) * d.NL));
       BFP_TRY(c->alloc((void **)&c->pp_args, sizeof(PipeArgs)));
       std::vector<LayerArgs> la(d.NL);

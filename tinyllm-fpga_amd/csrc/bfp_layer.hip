@@ -445,19 +445,33 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (PPW == 3 ? 6 : 4)) void k_qkv_attn
   mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
 }
 
+// AttnTagIO whose phase stamps, in a traced launch (TR), go to the Q|K|V
+// kernel's trace rows at the workgroup's id (past the matvec blocks'):
+// 0 entry, 1 wave 0's q|k|v in, 2 RoPE and the staged rows in LDS, 3
+// scores, 4 wave 0's softmax, 5 wave 0's AV chains.
+template <bool TR>
+struct AttnTagIOT : AttnTagIO {
+  unsigned long long *tr;
+  __device__ __forceinline__ void mark(int k) const {
+    if constexpr (TR) mx_mark(tr, k == ATT_MARK_QKV ? 1 : 2 + k);
+  }
+};
+
 // The same launch with one attention workgroup per (KV group, sequence):
 // all the group's query heads (bfp_attn_grp.h), H_KV x batch workgroups
 // from nblk (group id % H_KV, sequence id / H_KV).
-template <int PPW, int PB, bool TR>
+template <int PPW, bool TR>
 __global__ __launch_bounds__(64 * ATT_WAVES, 2) void k_qkv_attng_mx(LayerArgs a, int nblk) {
   extern __shared__ double dsm[];
   const int nq = a.D + 2 * a.KV;
   const unsigned tag = tw_tag(cur_pos(a), a.layer, a.NL);
   if ((int)blockIdx.x >= nblk) {
     const int L = blockIdx.x - nblk, gk = L % a.H_KV, b = L / a.H_KV;
-    AttnTagIO io{{a.qkv_m + b * nq, a.qkv_e + b * (nq / 16), a.att_m + b * a.D, a.att_e + b * (a.D / 16)},
-                 tw_make(a.t_qkv + (long long)b * nq, nq * 4), tw_make(a.t_abort, 4), tag};
-    attn_group_body<PPW, PB>(a, io, gk, b, [&] { return make_int2(cur_kv_pos(a), cur_pos(a)); }, dsm);
+    mx_mark(mx_tr<TR>(a, MX_K_QKV), 0);
+    AttnTagIOT<TR> io{{{a.qkv_m + b * nq, a.qkv_e + b * (nq / 16), a.att_m + b * a.D, a.att_e + b * (a.D / 16)},
+                       tw_make(a.t_qkv + (long long)b * nq, nq * 4), tw_make(a.t_abort, 4), tag},
+                      mx_tr<TR>(a, MX_K_QKV)};
+    attn_group_body<PPW>(a, io, gk, b, [&] { return make_int2(cur_kv_pos(a), cur_pos(a)); }, dsm);
     return;
   }
   const int nT = a.D / 16, bq = nq / 16, c = blockIdx.x % bq, b0 = blockIdx.x / bq * MX_SEQ;
@@ -474,9 +488,6 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 2) void k_qkv_attng_mx(LayerArgs a,
   })
   mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
 }
-// AV product rows per head in LDS: 16 keeps two workgroups a CU (config 5
-// 35.63k tokens/s against 35.38k with 32 rows and one a CU)
-constexpr int ATTG_PB = 16;
 // BFP_ATT_GROUP=0 keeps the one-head-per-workgroup form (read per launch).
 static int att_group_env() {
   const char *v = getenv("BFP_ATT_GROUP");
@@ -489,8 +500,8 @@ static qa_fn qkv_attn_kernel(int ppw, bool tr = false) {
   return ppw == 2 ? k_qkv_attn_mx<2, false> : (ppw == 3 ? k_qkv_attn_mx<3, false> : k_qkv_attn_mx<4, false>);
 }
 static qa_fn qkv_attng_kernel(int ppw, bool tr) {
-  if (tr) return ppw == 2 ? k_qkv_attng_mx<2, ATTG_PB, true> : k_qkv_attng_mx<3, ATTG_PB, true>;
-  return ppw == 2 ? k_qkv_attng_mx<2, ATTG_PB, false> : k_qkv_attng_mx<3, ATTG_PB, false>;
+  if (tr) return ppw == 2 ? k_qkv_attng_mx<2, true> : k_qkv_attng_mx<3, true>;
+  return ppw == 2 ? k_qkv_attng_mx<2, false> : k_qkv_attng_mx<3, false>;
 }
 // Grouped attention in the joined launch: the lane-split short forms, at
 // most AG_MAXG heads a group (and BFP_ATT_GROUP set).
@@ -499,7 +510,7 @@ static bool mx_attn_grouped(const LayerArgs &a) {
   return att_group_env() && attn_ppw(a.max_ctx) <= 3 && grp <= AG_MAXG && grp + 2 <= ATT_WAVES;
 }
 inline size_t qkv_attng_lds(const LayerArgs &a) {
-  const size_t sha = attn_grp_lds_bytes(a.max_ctx, a.H_Q / a.H_KV, ATTG_PB);
+  const size_t sha = attn_grp_lds_bytes(a.max_ctx, a.H_Q / a.H_KV);
   const size_t shq = (size_t)mx_lds_bytes(1, a.D / 16) + 16 * MX_SEQ * 12;
   return sha > shq ? sha : shq;
 }

@@ -71,7 +71,6 @@ namespace bfp {
 constexpr int PP_NW = PIPE_THREADS / 64;
 constexpr int PP_TPW_D = 5;    // input tiles per wave of a D-input chunk (D <= 640)
 constexpr int PP_TPW_F = 12;   // of an FFN-input chunk (FFN <= 1536)
-constexpr int PP_AV_ROWS = 64; // AV product rows per head in LDS (one workgroup a CU)
 
 // ------------------------------------------------------------ hand-off
 // The tagged words q = tid + k * PIPE_THREADS < nq (16-byte quads of r),
@@ -312,8 +311,6 @@ __device__ __forceinline__ long long pp_A(const MvLds &S, int q) {
 // words, the KV cache -- rows 0..pos-1 written by earlier launches, row pos
 // by this job for later ones -- with ordinary buffer accesses.
 struct AttnPipeIO {
-  static constexpr bool kSplitScores = false;
-  static constexpr int kAvBlock = ATT_AVC;   // a whole staged chunk's products (one workgroup a CU)
   rsrc_t rq, ro;                  // this sequence's q|k|v and attention output words
   unsigned tag;
   Wait *w;
@@ -424,9 +421,11 @@ __device__ __forceinline__ void job_norm(const PipeArgs &p, const PT_CONST Layer
 }
 
 // The attention of KV group gk (all its query heads) of sequence b at
-// layer l.
+// layer l.  A function of its own: inlined into the role functions, its
+// scalar values spilled into vector-register lanes and the job took 12.2 us
+// at position 135 of config 5 instead of 8.0.
 template <int PPW>
-__device__ __forceinline__ void job_attn(const PipeArgs &p, const PT_CONST LayerArgs *LA, Wait &w, int l, int gk,
+__device__ __noinline__ void job_attn(const PipeArgs &p, const PT_CONST LayerArgs *LA, Wait &w, int l, int gk,
                                          int b, int pos, double *dsm, unsigned long long *tr) {
   const int nq = p.D + 2 * p.KV;
   LayerArgs a = cload(LA + l);
@@ -449,7 +448,7 @@ __device__ __forceinline__ void job_attn(const PipeArgs &p, const PT_CONST Layer
   io.rrope = rsrc(a.rope);
   io.tr = tr;
   lds_barrier();   // the previous job's LDS reads are done
-  attn_group_body<PPW, PP_AV_ROWS>(a, io, gk, b, [pos] { return make_int2(pos, pos); }, dsm);
+  attn_group_body<PPW>(a, io, gk, b, [pos] { return make_int2(pos, pos); }, dsm);
 }
 
 // The epilogue pairs of a block: 16-lane group j (waves 0-3) owns sequence
@@ -873,7 +872,7 @@ int pipe_plan(const bfp_dims &d, int batch, int max_ctx, int cus, PipePlan &pl) 
   // LDS: the attention's, a matvec job's (inputs, exponents, A and M) and
   // an RMSNorm's
   const int nTmax = std::max(nd16, nf16);
-  const size_t att = attn_grp_lds_bytes(max_ctx, grp, PP_AV_ROWS);
+  const size_t att = attn_grp_lds_bytes(max_ctx, grp);
   const size_t mv = ((size_t)16 * nTmax * 32 + 16 * nTmax + 7) / 8 * 8 + (size_t)2 * 256 * 12;
   const size_t nrm = (size_t)(d.D + PW_MAX_LEAVES) * 8 + (size_t)d.D * 2 + nd16;
   pl.lds = (std::max(att, std::max(mv, nrm)) + 15) & ~(size_t)15;
