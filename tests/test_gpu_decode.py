@@ -297,7 +297,10 @@ def test_batched_trace(gpu):
     """A traced batched decode on the matrix cores gives the untraced tokens,
     and every stamped block's phases are in order (entry, exponents staged,
     row maxima, tile sums, sums reduced, epilogue); the four kernels stamp
-    their block counts (chunks x sequence groups)."""
+    their block counts (chunks x sequence groups), and the grouped attention
+    workgroups of the joined Q|K|V launch (one per KV group and sequence,
+    after the matvec blocks) theirs (entry, q|k|v in, RoPE and staged rows,
+    scores, softmax, AV chains)."""
     cfg = dict(D=256, H_Q=4, H_KV=2, HD=64, FFN=512, NL=2, MAX_CTX=24, VOCAB=512)
     d, om, gm = _setup(cfg, seed=33, max_batch=24)
     from bfp import synth
@@ -309,6 +312,14 @@ def test_batched_trace(gpu):
     assert tr is not None and tr.shape == (4, 1024, 6)
     groups = 2
     chunks = [(d.D + 2 * d.H_KV * d.HD) // 16, d.D // 16, d.FFN // 16, d.D // 16]
+    assert "attn_group" in gm.decode_form()
+    nblk = chunks[0] * groups
+    att = tr[0][nblk:].astype(np.int64)
+    att = att[att[:, 0] > 0]
+    assert len(att) == d.H_KV * 24
+    assert (np.diff(att, axis=1) >= 0).all()
+    tr = tr.copy()
+    tr[0][nblk:] = 0
     for k in range(4):
         st = tr[k][tr[k][:, 0] > 0].astype(np.int64)
         assert len(st) == chunks[k] * groups, (k, len(st))
