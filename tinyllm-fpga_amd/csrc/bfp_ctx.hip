@@ -347,7 +347,7 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
     BFP_TRY(c->alloc((void **)&c->pt_layers, sizeof(LayerArgs) * d.NL));
     BFP_TRY(c->alloc((void **)&c->pt_args, sizeof(PersistArgs)));
     BFP_TRY(c->alloc((void **)&c->pt_clock, sizeof(unsigned long long) * (c->max_ctx + 1)));
-    BFP_TRY(c->alloc_fine((void **)&c->pt_scores, sizeof(double) * (size_t)d.H_Q * c->max_ctx));
+    BFP_TRY(c->alloc_fine((void **)&c->pt_scores, sizeof(double) * (size_t)d.H_Q * attn_sc_stride(c->max_ctx)));
     std::vector<LayerArgs> la(d.NL);
     for (int l = 0; l < d.NL; ++l) la[l] = layer_args(c, l, 1);
     HIP_TRY(hipMemcpy(c->pt_layers, la.data(), sizeof(LayerArgs) * d.NL, hipMemcpyHostToDevice));

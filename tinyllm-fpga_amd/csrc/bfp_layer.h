@@ -140,6 +140,14 @@ inline int attn_ppw(int max_ctx) {
   return max_ctx <= 128 ? 2 : (max_ctx <= 256 ? 3 : (max_ctx <= 512 ? 4 : 8));
 }
 
+// Long attention form: workgroups per head, each owning 16 dimensions.
+constexpr int ATT_DSPLIT = 4;
+// Doubles per head of the long form's score exchange: workgroup dg's rows
+// t = ATT_DSPLIT u + dg at dg * ceil(max_ctx / ATT_DSPLIT) + u, so each
+// workgroup's stores and each block of another's loads are contiguous.
+__host__ __device__ inline int attn_sc_block(int max_ctx) { return (max_ctx + ATT_DSPLIT - 1) / ATT_DSPLIT; }
+__host__ __device__ inline int attn_sc_stride(int max_ctx) { return ATT_DSPLIT * attn_sc_block(max_ctx); }
+
 // Rows per workgroup of the batch > 1 head: 16 row slots x 2 rows for
 // D <= 576, x 1 row above (register budget).
 inline int head_rows_multi(int D) { return D <= 576 ? 32 : 16; }

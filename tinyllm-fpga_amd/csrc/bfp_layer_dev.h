@@ -355,6 +355,12 @@ struct AttnPlainIO {
   __device__ __forceinline__ int km1(const int16_t *p) const { return *p; }
   __device__ __forceinline__ int ke1(const int8_t *p) const { return *p; }
   __device__ __forceinline__ int ve1(const int8_t *p) const { return *p; }
+  // loads of rows that may lie past the position (live false): read anyway,
+  // the clamped row is a cache hit
+  __device__ __forceinline__ uint4 k16l(const int16_t *p, bool) const { return k16(p); }
+  __device__ __forceinline__ int ke4l(const int8_t *p, bool) const { return ke4(p); }
+  __device__ __forceinline__ uint4 v16l(const int16_t *p, bool) const { return v16(p); }
+  __device__ __forceinline__ int ve1l(const int8_t *p, bool) const { return ve1(p); }
   __device__ __forceinline__ void k_put(int16_t *pm, int8_t *pe, int m, int e, bool we) const {
     *pm = (int16_t)m;
     if (we) *pe = (int8_t)e;
@@ -419,7 +425,7 @@ constexpr int ATT_AVC = 128;
 // chain lane of dimension d reads two positions per 16-byte load at
 // d*AVL_TBP: the padding of 2 puts the 16 lanes in 16 distinct bank
 // groups.
-constexpr int ATT_DSPLIT = 4;
+// ATT_DSPLIT, attn_sc_block, attn_sc_stride: bfp_layer.h
 constexpr int AVL_PW = 3;
 constexpr int AVL_TB = AVL_PW * 64;
 constexpr int AVL_TBP = AVL_TB + 2;
@@ -428,9 +434,15 @@ constexpr int AVL_G = 8;        // chain: positions per group of LDS reads
 constexpr int AVL_AHEAD = 3;    // chain: groups of reads in flight ahead of the adds
 // av_block: rows of the short forms' AV products held in LDS at once
 // (IO::kAvBlock)
-inline size_t attn_lds_bytes(int max_ctx, int ppw, int av_block) {
+// The long form with split scores (IO::kSplitScores) stages a pass of K rows
+// (64 * ATT_WAVES of them, ATT_KS mantissas and 4 exponents a row) in the
+// AV buffers' space before the AV phase: kstage.
+constexpr int ATT_KS = 72;   // 144-byte rows: 8 consecutive rows' 16-byte reads hit distinct bank groups
+inline size_t attn_lds_bytes(int max_ctx, int ppw, int av_block, bool kstage = false) {
   const size_t sc_len = (size_t)((max_ctx + 1) & ~1);
-  const size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4) : (size_t)2 * 16 * AVL_TBP * 8;
+  size_t av = ppw <= 4 ? (size_t)2 * ATT_AVC * (64 * 2 + 4) : (size_t)2 * 16 * AVL_TBP * 8;
+  const size_t ks = (size_t)64 * ATT_WAVES * (ATT_KS * 2 + 4);
+  if (ppw > 4 && kstage && ks > av) av = ks;
   const size_t pr = ppw <= 4 ? (size_t)av_block * 64 * 8 : 0;
   return (256 + sc_len) * 8 + av + pr;
 }
@@ -440,12 +452,14 @@ struct KRow {
   uint4 m[8];
   int e4;
 };
+// live: the row is at or before the position (else the IO may skip the
+// memory request: the values are never used)
 template <class IO>
 __device__ __forceinline__ void load_krow(const IO &io, KRow &r, const int16_t *Km, const int8_t *Ke,
-                                          long long o) {
+                                          long long o, bool live) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r.m[i] = io.k16(Km + o + 8 * i);
-  r.e4 = io.ke4(Ke + (o >> 4));
+  for (int i = 0; i < 8; ++i) r.m[i] = io.k16l(Km + o + 8 * i, live);
+  r.e4 = io.ke4l(Ke + (o >> 4), live);
 }
 
 // The attention of one head (or one tile of it) for one sequence.  The body
@@ -582,10 +596,11 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       int t = k * TB + tt0 + r;
-      t = t < n ? t : n - 1;
+      const bool live = t < n;
+      t = live ? t : n - 1;
       const long long o = ((long long)t * a.H_KV + g) * HD + 16 * dg + 8 * hh;
-      m[r] = io.v16(Vm + o);
-      e[r] = io.ve1(Ve + (o >> 4));
+      m[r] = io.v16l(Vm + o, live);
+      e[r] = io.ve1l(Ve + (o >> 4), live);
     }
   };
 
@@ -600,9 +615,38 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
   constexpr int RS = (!SHORT && IO::kSplitScores) ? ATT_DSPLIT : 1;
   const int r0 = RS > 1 ? dg : 0;
   const int nu = (n - r0 + RS - 1) / RS;
-  if constexpr (!LANE_SPLIT) {
+  // long form with split scores: each pass of the workgroup's rows (u0 ..
+  // u0 + NT - 1) is staged through LDS with coalesced loads -- 8 lanes per
+  // row, lane l part l % 8 of row l / 8 + 8i of its wave's 64 -- instead of
+  // each thread loading its own row (the same bytes at a third of the rate
+  // per CU); rows from pos on are never loaded (row pos is scored from kc)
+  constexpr bool KST = !SHORT && IO::kSplitScores;
+  int16_t *kst = reinterpret_cast<int16_t *>(buf);          // NT x ATT_KS
+  int8_t *kex = reinterpret_cast<int8_t *>(kst + NT * ATT_KS);   // NT x 4
+  uint4 ks[KST ? 8 : 1];
+  int kse = 0;
+  auto kst_load = [&](int u0) {
+#pragma unroll
+    for (int i = 0; i < (KST ? 8 : 1); ++i) {
+      const int t = RS * (u0 + 64 * w + 8 * i + (l >> 3)) + r0;
+      const bool live = t < pos;
+      ks[i] = io.k16l(Km + ((long long)(live ? t : 0) * a.H_KV + g) * HD + 8 * (l & 7), live);
+    }
+    const int t = RS * (u0 + tid) + r0;
+    const bool live = t < pos;
+    kse = io.ke4l(Ke + ((((long long)(live ? t : 0) * a.H_KV + g) * HD) >> 4), live);
+  };
+  auto kst_store = [&]() {
+#pragma unroll
+    for (int i = 0; i < (KST ? 8 : 1); ++i)
+      *reinterpret_cast<uint4 *>(kst + (64 * w + 8 * i + (l >> 3)) * ATT_KS + 8 * (l & 7)) = ks[i];
+    *reinterpret_cast<int *>(kex + 4 * tid) = kse;
+  };
+  if constexpr (KST) {
+    kst_load(0);
+  } else if constexpr (!LANE_SPLIT) {
     const int t = RS * tid + r0;
-    load_krow(io, kr[0], Km, Ke, ((long long)(t < n ? t : n - 1) * a.H_KV + g) * HD);
+    load_krow(io, kr[0], Km, Ke, ((long long)(t < n ? t : n - 1) * a.H_KV + g) * HD, t < n);
   }
 
   if (w == 0) {            // q head hq
@@ -639,6 +683,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
       io.v_put(Vm + o, Ve + (o >> 4), m, e, (l & 15) == 0);
     }
   }
+  if constexpr (KST) kst_store();   // the first pass's K rows
   lds_barrier();
   io.mark(ATT_MARK_ROPE);
 
@@ -679,6 +724,47 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     // flight since the RoPE phase
     if (tid < n) sc[tid] = ddot64_skx_bfp(q, kr[0].m, kr[0].e4) * a.score_mul;
     if (tid == pos) sc[pos] = ddot64_skx(q, kc) * a.score_mul;
+  } else if constexpr (KST) {
+    // one staged row per thread and pass (the first pass's rows were
+    // written to LDS before the RoPE barrier)
+    for (int u0 = 0; u0 < nu; u0 += NT) {   // uniform
+      if (u0 > 0) {
+        lds_barrier();   // the previous pass's rows are read
+        kst_load(u0);
+        kst_store();
+        lds_barrier();
+      }
+      const int t = RS * (u0 + tid) + r0;
+      const double sj = ddot64_skx_bfp(q, reinterpret_cast<const uint4 *>(kst + tid * ATT_KS),
+                                       *reinterpret_cast<const int *>(kex + 4 * tid)) * a.score_mul;
+      if (t < n) sc[t] = sj;
+    }
+    if ((pos - r0) % RS == 0 && tid == ((pos - r0) / RS) % NT) sc[pos] = ddot64_skx(q, kc) * a.score_mul;
+    if constexpr (RS > 1) {
+      // exchange: publish this workgroup's rows, then read the other
+      // workgroups' (the same q, K rows and ddot order, so the same bits);
+      // each workgroup's block is contiguous (attn_sc_block), and a
+      // thread's loads are all issued before the first is used
+      lds_barrier();
+      for (int u = tid; u < nu; u += NT) io.score_put(hq, r0, u, sc[RS * u + r0]);
+      io.scores_publish(hq, dg);
+      io.scores_wait(hq, dg);
+      const int nb = (n + RS - 1) / RS;   // rows of the longest block
+      constexpr int GL = 4;
+      for (int i0 = 0; i0 < RS * nb; i0 += GL * NT) {   // uniform
+        double v[GL];
+#pragma unroll
+        for (int k = 0; k < GL; ++k) {
+          const int i = min(i0 + tid + k * NT, RS * nb - 1);
+          v[k] = io.score_get(hq, i / nb, i % nb);
+        }
+#pragma unroll
+        for (int k = 0; k < GL; ++k) {
+          const int i = i0 + tid + k * NT, d_ = i / nb, t = RS * (i % nb) + d_;
+          if (i < RS * nb && d_ != r0 && t < n) sc[t] = v[k];
+        }
+      }
+    }
   } else {
     // passes of KR rows per thread: rows t = RS u + r0, u = u0 + tid + j*NT;
     // kr[0] of the next pass is loaded as soon as this pass's kr[0] is
@@ -688,7 +774,7 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
 #pragma unroll
       for (int j = 1; j < KR; ++j) {
         const int t = RS * (u0 + tid + j * NT) + r0;
-        load_krow(io, kr[j], Km, Ke, ((long long)(t < n ? t : last) * a.H_KV + g) * HD);
+        load_krow(io, kr[j], Km, Ke, ((long long)(t < n ? t : last) * a.H_KV + g) * HD, t < n);
       }
 #pragma unroll
       for (int j = 0; j < KR; ++j) {
@@ -696,23 +782,13 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
         const double sj = ddot64_skx_bfp(q, kr[j].m, kr[j].e4) * a.score_mul;
         if (j == 0) {
           const int tn = t + RS * KR * NT;
-          load_krow(io, kr[0], Km, Ke, ((long long)(tn < n ? tn : last) * a.H_KV + g) * HD);
+          load_krow(io, kr[0], Km, Ke, ((long long)(tn < n ? tn : last) * a.H_KV + g) * HD, tn < n);
         }
         if (t < n) sc[t] = sj;
       }
     }
     // row pos from LDS, by the thread that scored it from the cache
     if ((pos - r0) % RS == 0 && tid == ((pos - r0) / RS) % NT) sc[pos] = ddot64_skx(q, kc) * a.score_mul;
-    if constexpr (RS > 1) {
-      // exchange: publish this workgroup's rows, then read the other
-      // workgroups' (the same q, K rows and ddot order, so the same bits)
-      lds_barrier();
-      for (int u = tid; u < nu; u += NT) io.score_put(hq, RS * u + r0, sc[RS * u + r0]);
-      io.scores_publish(hq, dg);
-      io.scores_wait(hq, dg);
-      for (int t = tid; t < n; t += NT)
-        if (t % RS != r0) sc[t] = io.score_get(hq, t);
-    }
   }
   if constexpr (SHORT) {
     BFP_ATT_STORE_V(0)

@@ -177,15 +177,16 @@ __device__ __forceinline__ int clamp_tok(const PersistArgs &p, int t) {
 // tagged words, the KV cache through SC1 buffer loads and stores.
 struct AttnCohIO {
   // long form: the head's ATT_DSPLIT workgroups split the scores and
-  // exchange them through sc_buf (rsc: hq * max_ctx + t doubles) and one
-  // tagged flag word per (head, workgroup) (rfl)
+  // exchange them through sc_buf (rsc: head hq's at hq * sc_stride, in
+  // blocks per workgroup, attn_sc_stride) and one tagged flag word per
+  // (head, workgroup) (rfl)
   static constexpr bool kSplitScores = true;
   static constexpr int kAvBlock = ATT_AVC;   // a whole staged chunk's products (one workgroup a CU)
   rsrc_t rq, ro;                  // this step's q|k|v and attention output words
   unsigned tag;
   Wait *w;
   rsrc_t rsc, rfl;
-  int sc_stride;
+  int sc_stride, sc_block;
   rsrc_t rkm, rke, rvm, rve;      // this layer's KV cache
   const int16_t *km0, *vm0;
   const int8_t *ke0, *ve0;
@@ -223,6 +224,24 @@ struct AttnCohIO {
   __device__ __forceinline__ int ve1(const int8_t *p) const {
     return (int)(signed char)__builtin_amdgcn_raw_buffer_load_b8(rve, (int)(p - ve0), 0, CPOL_SC1);
   }
+  // loads of rows that may lie past the position (live false): those go to
+  // an offset past the buffer's end (kDead >= the descriptors' 0x7fffffff
+  // bytes), where a buffer load returns zeros without a memory request --
+  // device-coherent loads are not cached, and the clamped row the callers
+  // name would cost as much as a live one
+  static constexpr int kDead = (int)0x80000000u;
+  __device__ __forceinline__ uint4 k16l(const int16_t *p, bool live) const {
+    return ld_b128<CPOL_SC1>(rkm, live ? (int)(p - km0) * 2 : kDead);
+  }
+  __device__ __forceinline__ int ke4l(const int8_t *p, bool live) const {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(rke, live ? (int)(p - ke0) : kDead, 0, CPOL_SC1);
+  }
+  __device__ __forceinline__ uint4 v16l(const int16_t *p, bool live) const {
+    return ld_b128<CPOL_SC1>(rvm, live ? (int)(p - vm0) * 2 : kDead);
+  }
+  __device__ __forceinline__ int ve1l(const int8_t *p, bool live) const {
+    return (int)(signed char)__builtin_amdgcn_raw_buffer_load_b8(rve, live ? (int)(p - ve0) : kDead, 0, CPOL_SC1);
+  }
   __device__ __forceinline__ void k_put(int16_t *pm, int8_t *pe, int m, int e, bool we) const {
     __builtin_amdgcn_raw_buffer_store_b16((unsigned short)m, rkm, (int)(pm - km0) * 2, 0, CPOL_SC1);
     if (we) __builtin_amdgcn_raw_buffer_store_b8((unsigned char)e, rke, (int)(pe - ke0), 0, CPOL_SC1);
@@ -240,17 +259,18 @@ struct AttnCohIO {
     lds_barrier();
   }
   __device__ __forceinline__ void out(int idx, int m, int e, bool) const { st_coh(ro, 4 * idx, tagged(m, e, tag)); }
-  __device__ __forceinline__ void score_put(int hq, int t, double v) const {
+  // row u of workgroup dg's block (its position ATT_DSPLIT u + dg)
+  __device__ __forceinline__ void score_put(int hq, int dg, int u, double v) const {
     typedef unsigned v2u __attribute__((ext_vector_type(2)));
     const unsigned long long b = (unsigned long long)__double_as_longlong(v);
     v2u x;
     x.x = (unsigned)b;
     x.y = (unsigned)(b >> 32);
-    __builtin_amdgcn_raw_buffer_store_b64(x, rsc, 8 * (hq * sc_stride + t), 0, CPOL_SC1);
+    __builtin_amdgcn_raw_buffer_store_b64(x, rsc, 8 * (hq * sc_stride + dg * sc_block + u), 0, CPOL_SC1);
   }
-  __device__ __forceinline__ double score_get(int hq, int t) const {
+  __device__ __forceinline__ double score_get(int hq, int dg, int u) const {
     typedef unsigned v2u __attribute__((ext_vector_type(2)));
-    const v2u x = __builtin_amdgcn_raw_buffer_load_b64(rsc, 8 * (hq * sc_stride + t), 0, CPOL_SC1);
+    const v2u x = __builtin_amdgcn_raw_buffer_load_b64(rsc, 8 * (hq * sc_stride + dg * sc_block + u), 0, CPOL_SC1);
     return __longlong_as_double((long long)(((unsigned long long)x.y << 32) | x.x));
   }
   // every wave's score stores complete (vmcnt 0), then one flag word
@@ -464,7 +484,8 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
         io.rve = rsrc(a.v_e);
         io.rsc = rsrc(p.sc_buf);
         io.rfl = rsrc(p.t_sflag);
-        io.sc_stride = a.max_ctx;
+        io.sc_stride = attn_sc_stride(a.max_ctx);
+        io.sc_block = attn_sc_block(a.max_ctx);
         io.rope_s = rope_s;
         io.trace = (p.trace && c == 0) ? p.trace + ((size_t)s * p.NL + l) * PT_TRACE_LAYER : nullptr;
         attn_body<PPW, SHORT>(a, io, c, 0, [s] { return make_int2(s, s); }, dsm);
@@ -679,7 +700,7 @@ static size_t persist_lds(const PersistArgs &p, int max_ctx) {
   const size_t head = (size_t)(3 * D + PW_MAX_LEAVES) * 8 + (size_t)D * 2 + nT;
   // the Q|K|V role keeps the step's RoPE row (64 doubles) ahead of both its
   // norm work space and the attention's
-  size_t lds = attn_lds_bytes(max_ctx, attn_ppw(max_ctx), AttnCohIO::kAvBlock) + 64 * 8;
+  size_t lds = attn_lds_bytes(max_ctx, attn_ppw(max_ctx), AttnCohIO::kAvBlock, AttnCohIO::kSplitScores) + 64 * 8;
   lds = lds > norm + 64 * 8 ? lds : norm + 64 * 8;
   lds = lds > dx ? lds : dx;
   lds = lds > head ? lds : head;
