@@ -79,7 +79,7 @@ struct bfp_ctx {
   LayerArgs *pt_layers = nullptr;
   PersistArgs *pt_args = nullptr;
   unsigned long long *pt_clock = nullptr;
-  double *pt_scores = nullptr;   // the long attention form's score exchange
+  unsigned *pt_scores = nullptr;   // the long attention form's score exchange (tagged words)
   // the pipelined batched step (bfp_pipe.hip), made on its first use: its
   // tagged hand-off words, the layer blocks, the argument block, and one
   // schedule per batch size
@@ -347,7 +347,7 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
     BFP_TRY(c->alloc((void **)&c->pt_layers, sizeof(LayerArgs) * d.NL));
     BFP_TRY(c->alloc((void **)&c->pt_args, sizeof(PersistArgs)));
     BFP_TRY(c->alloc((void **)&c->pt_clock, sizeof(unsigned long long) * (c->max_ctx + 1)));
-    BFP_TRY(c->alloc_fine((void **)&c->pt_scores, sizeof(double) * (size_t)d.H_Q * attn_sc_stride(c->max_ctx)));
+    BFP_TRY(c->alloc_fine((void **)&c->pt_scores, 16 * (size_t)d.H_Q * attn_sc_stride(c->max_ctx)));
     std::vector<LayerArgs> la(d.NL);
     for (int l = 0; l < d.NL; ++l) la[l] = layer_args(c, l, 1);
     HIP_TRY(hipMemcpy(c->pt_layers, la.data(), sizeof(LayerArgs) * d.NL, hipMemcpyHostToDevice));
@@ -361,9 +361,8 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
   pa.t_qkv = (w += 2 * D);
   pa.t_mlp = (w += 2 * nq);
   pa.t_part = (w += 2 * F);
-  pa.t_sflag = (w += 2 * 4 * (size_t)grid);
   pa.sc_buf = c->pt_scores;
-  pa.abort_flag = (w += PT_SFLAGS_PER_HEAD * (size_t)d.H_Q);
+  pa.abort_flag = (w += 2 * 4 * (size_t)grid);
   pa.L = c->pt_layers;
   pa.steps = steps;
   pa.n_prompt = n_prompt;
@@ -380,6 +379,8 @@ int decode_persist(bfp_ctx *c, PersistArgs pa, int grid, const int *dprompt, int
   pa.hist_steps = dhm ? steps : 0;
   pa.trace = dtrace;
   HIP_TRY(hipMemsetAsync(c->pt_words, 0, c->pt_nwords * 4, s));
+  // the score words too: their tags repeat from one decode to the next
+  HIP_TRY(hipMemsetAsync(c->pt_scores, 0, 16 * (size_t)d.H_Q * attn_sc_stride(c->max_ctx), s));
   if (abort_test) HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)pa.abort_flag, 1, 1, s));
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   HIP_TRY(hipEventCreate(&ev0));

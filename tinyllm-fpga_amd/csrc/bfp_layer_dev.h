@@ -741,27 +741,25 @@ __device__ __forceinline__ void attn_body(const LayerArgs &a, IO &io, int bx, in
     }
     if ((pos - r0) % RS == 0 && tid == ((pos - r0) / RS) % NT) sc[pos] = ddot64_skx(q, kc) * a.score_mul;
     if constexpr (RS > 1) {
-      // exchange: publish this workgroup's rows, then read the other
-      // workgroups' (the same q, K rows and ddot order, so the same bits);
-      // each workgroup's block is contiguous (attn_sc_block), and a
-      // thread's loads are all issued before the first is used
-      lds_barrier();
+      // exchange: publish this workgroup's rows (each thread the rows it
+      // scored), then read the other workgroups' (the same q, K rows and
+      // ddot order, so the same bits); each workgroup's block is contiguous
+      // (attn_sc_block), and a thread's reads are all issued before the
+      // first is used
       for (int u = tid; u < nu; u += NT) io.score_put(hq, r0, u, sc[RS * u + r0]);
-      io.scores_publish(hq, dg);
-      io.scores_wait(hq, dg);
       const int nb = (n + RS - 1) / RS;   // rows of the longest block
       constexpr int GL = 4;
       for (int i0 = 0; i0 < RS * nb; i0 += GL * NT) {   // uniform
-        double v[GL];
+        uint4 v[GL];
 #pragma unroll
         for (int k = 0; k < GL; ++k) {
           const int i = min(i0 + tid + k * NT, RS * nb - 1);
-          v[k] = io.score_get(hq, i / nb, i % nb);
+          v[k] = io.score_raw(hq, i / nb, i % nb);
         }
 #pragma unroll
         for (int k = 0; k < GL; ++k) {
           const int i = i0 + tid + k * NT, d_ = i / nb, t = RS * (i % nb) + d_;
-          if (i < RS * nb && d_ != r0 && t < n) sc[t] = v[k];
+          if (i < RS * nb && d_ != r0 && t < n) sc[t] = io.score_val(v[k], hq, d_, i % nb);
         }
       }
     }

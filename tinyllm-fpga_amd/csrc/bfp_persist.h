@@ -22,10 +22,9 @@ struct PersistArgs {
   // tagged activation words, two of each (step parity): h, h1, att (D),
   // q|k|v (D + 2KV), mlp (FFN); the head's per-workgroup argmax, 4 words each
   unsigned *t_h, *t_h1, *t_att, *t_qkv, *t_mlp, *t_part;
-  // the long attention form's score exchange: one tagged flag word per
-  // (head, workgroup) and H_Q x max_ctx float64 scores
-  unsigned *t_sflag;
-  double *sc_buf;
+  // the long attention form's score exchange: per head attn_sc_stride
+  // entries of 4 tagged words (16 bits of a float64 score each)
+  unsigned *sc_buf;
   unsigned *abort_flag;          // set by a wait that gave up
   unsigned long long *clock;     // steps + 1 stamps of the 100 MHz clock, or null
   int16_t *hist_m;               // optional per-(step, layer) outputs
@@ -42,7 +41,6 @@ struct PersistArgs {
   // argmax stored, token known)
   unsigned long long *trace;
 };
-constexpr int PT_SFLAGS_PER_HEAD = 4;   // the long attention form's workgroups per head
 constexpr int PT_TRACE_LAYER = 20;
 constexpr int PT_TRACE_ATT = 16;        // first attention phase stamp (ATT_MARK_* follow)
 constexpr int PT_TRACE_STEP = 3;
@@ -54,7 +52,7 @@ inline size_t persist_trace_len(int steps, int NL) {
 // before each launch; the abort flag is the last word).
 inline size_t persist_words(const bfp_dims &d, int grid) {
   const size_t nq = (size_t)d.D + 2 * (size_t)d.H_KV * d.HD;
-  return 2 * (3 * (size_t)d.D + nq + (size_t)d.FFN) + 2 * 4 * (size_t)grid + PT_SFLAGS_PER_HEAD * (size_t)d.H_Q + 1;
+  return 2 * (3 * (size_t)d.D + nq + (size_t)d.FFN) + 2 * 4 * (size_t)grid + 1;
 }
 
 // Fills the shape fields of p and the grid (one workgroup per compute unit)

@@ -71,7 +71,6 @@
 namespace bfp {
 
 constexpr int PT_THREADS = 512;   // 8 waves: the attention body's workgroup size
-static_assert(PT_SFLAGS_PER_HEAD == ATT_DSPLIT, "one score flag per long-form workgroup of a head");
 constexpr int PT_NW = PT_THREADS / 64;
 constexpr int PT_HEAD_D64 = 9;    // head rows of at most 576 elements
 
@@ -177,15 +176,16 @@ __device__ __forceinline__ int clamp_tok(const PersistArgs &p, int t) {
 // tagged words, the KV cache through SC1 buffer loads and stores.
 struct AttnCohIO {
   // long form: the head's ATT_DSPLIT workgroups split the scores and
-  // exchange them through sc_buf (rsc: head hq's at hq * sc_stride, in
-  // blocks per workgroup, attn_sc_stride) and one tagged flag word per
-  // (head, workgroup) (rfl)
+  // exchange them through sc_buf (rsc: head hq's at hq * sc_stride entries,
+  // in blocks per workgroup, attn_sc_stride), each score as four tagged
+  // words, which the readers poll: no flag, no wait for the stores'
+  // completion
   static constexpr bool kSplitScores = true;
   static constexpr int kAvBlock = ATT_AVC;   // a whole staged chunk's products (one workgroup a CU)
   rsrc_t rq, ro;                  // this step's q|k|v and attention output words
   unsigned tag;
   Wait *w;
-  rsrc_t rsc, rfl;
+  rsrc_t rsc;
   int sc_stride, sc_block;
   rsrc_t rkm, rke, rvm, rve;      // this layer's KV cache
   const int16_t *km0, *vm0;
@@ -259,32 +259,31 @@ struct AttnCohIO {
     lds_barrier();
   }
   __device__ __forceinline__ void out(int idx, int m, int e, bool) const { st_coh(ro, 4 * idx, tagged(m, e, tag)); }
-  // row u of workgroup dg's block (its position ATT_DSPLIT u + dg)
+  // row u of workgroup dg's block (its position ATT_DSPLIT u + dg): bits
+  // 16k .. 16k+15 of the score in word k, with the (step, layer) tag
+  __device__ __forceinline__ int sc_off(int hq, int dg, int u) const { return 16 * (hq * sc_stride + dg * sc_block + u); }
   __device__ __forceinline__ void score_put(int hq, int dg, int u, double v) const {
-    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const unsigned long long b = (unsigned long long)__double_as_longlong(v);
-    v2u x;
-    x.x = (unsigned)b;
-    x.y = (unsigned)(b >> 32);
-    __builtin_amdgcn_raw_buffer_store_b64(x, rsc, 8 * (hq * sc_stride + dg * sc_block + u), 0, CPOL_SC1);
+    const unsigned tg = tag << 24;
+    v4u x;
+    x.x = (unsigned)(b & 0xffffu) | tg;
+    x.y = (unsigned)((b >> 16) & 0xffffu) | tg;
+    x.z = (unsigned)((b >> 32) & 0xffffu) | tg;
+    x.w = (unsigned)((b >> 48) & 0xffffu) | tg;
+    __builtin_amdgcn_raw_buffer_store_b128(x, rsc, sc_off(hq, dg, u), 0, CPOL_SC1);
   }
-  __device__ __forceinline__ double score_get(int hq, int dg, int u) const {
-    typedef unsigned v2u __attribute__((ext_vector_type(2)));
-    const v2u x = __builtin_amdgcn_raw_buffer_load_b64(rsc, 8 * (hq * sc_stride + dg * sc_block + u), 0, CPOL_SC1);
-    return __longlong_as_double((long long)(((unsigned long long)x.y << 32) | x.x));
+  // a first read of the entry (issued with the others before any is used),
+  // then its value, waiting (bounded) while its words carry another tag
+  __device__ __forceinline__ uint4 score_raw(int hq, int dg, int u) const {
+    return ld_b128<CPOL_SC1>(rsc, sc_off(hq, dg, u));
   }
-  // every wave's score stores complete (vmcnt 0), then one flag word
-  __device__ __forceinline__ void scores_publish(int hq, int dg) const {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    lds_barrier();
-    if (threadIdx.x == 0) st_coh(rfl, 4 * (hq * ATT_DSPLIT + dg), tag << 24);
-  }
-  // lanes 0..ATT_DSPLIT-1 of wave 0 wait for the other workgroups' flags
-  __device__ __forceinline__ void scores_wait(int hq, int dg) const {
-    if (threadIdx.x < ATT_DSPLIT && (int)threadIdx.x != dg) w->word(rfl, 4 * (hq * ATT_DSPLIT + threadIdx.x), tag);
-    lds_barrier();
+  __device__ __forceinline__ double score_val(uint4 v, int hq, int dg, int u) const {
+    if (!Wait::ok4(v, tag)) v = w->quad(rsc, sc_off(hq, dg, u), tag);
+    const unsigned long long b = (unsigned long long)(v.x & 0xffffu) | ((unsigned long long)(v.y & 0xffffu) << 16) |
+                                 ((unsigned long long)(v.z & 0xffffu) << 32) |
+                                 ((unsigned long long)(v.w & 0xffffu) << 48);
+    return __longlong_as_double((long long)b);
   }
 };
 
@@ -483,7 +482,6 @@ __device__ void role_qkv(const PT_CONST PersistArgs *pp, double *dsm, int c) {
         io.rvm = rsrc(a.v_m);
         io.rve = rsrc(a.v_e);
         io.rsc = rsrc(p.sc_buf);
-        io.rfl = rsrc(p.t_sflag);
         io.sc_stride = attn_sc_stride(a.max_ctx);
         io.sc_block = attn_sc_block(a.max_ctx);
         io.rope_s = rope_s;
