@@ -74,26 +74,46 @@ constexpr int PP_TPW_F = 12;   // of an FFN-input chunk (FFN <= 1536)
 
 // ------------------------------------------------------------ hand-off
 // The tagged words q = tid + k * PIPE_THREADS < nq (16-byte quads of r),
-// NQ per thread: every thread's loads are issued together, then each quad
-// that does not carry the tag yet is polled on its own (bounded); put(q, v)
-// receives each quad.  (Ordinary first loads, re-polling only the words
-// without the tag at the device-coherent level, left a stale copy cached
-// that the re-polls kept returning: the waits gave up.)
+// NQ per thread: every thread's loads are issued together; then, in rounds,
+// every quad that does not carry the tag yet is loaded again, all of them
+// at once (one round trip a round, not one per quad: a job that starts
+// before its inputs are complete would otherwise wait for its NQ quads one
+// after another), the rounds bounded like Wait's; put(q, v) receives each
+// quad.  (Ordinary first loads, re-polling only the words without the tag
+// at the device-coherent level, left a stale copy cached that the re-polls
+// kept returning: the waits gave up.)
 template <int NQ, int POL = CPOL_SC1, class Put>
 __device__ __forceinline__ void pp_poll_quads(Wait &w, rsrc_t r, int nq, unsigned tag, Put put) {
+  static_assert(NQ <= 32, "pending-quad mask");
   uint4 v[NQ];
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
     const int q = threadIdx.x + k * PIPE_THREADS;
     v[k] = ld_b128<POL>(r, 16 * (q < nq ? q : nq - 1));
   }
+  unsigned pend = 0;
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
     const int q = threadIdx.x + k * PIPE_THREADS;
-    if (q < nq) {
-      if (!Wait::ok4(v[k], tag)) v[k] = w.quad(r, 16 * q, tag);
-      put(q, v[k]);
+    if (q < nq && !Wait::ok4(v[k], tag)) pend |= 1u << k;
+  }
+  if (pend != 0u && !w.aborted) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (unsigned it = 1;; ++it) {
+      __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+      for (int k = 0; k < NQ; ++k)
+        if ((pend >> k) & 1u) v[k] = ld_b128<POL>(r, 16 * (threadIdx.x + k * PIPE_THREADS));
+#pragma unroll
+      for (int k = 0; k < NQ; ++k)
+        if (((pend >> k) & 1u) && Wait::ok4(v[k], tag)) pend &= ~(1u << k);
+      if (pend == 0u || w.give_up(it, t0)) break;
     }
+  }
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    const int q = threadIdx.x + k * PIPE_THREADS;
+    if (q < nq) put(q, v[k]);
   }
 }
 
