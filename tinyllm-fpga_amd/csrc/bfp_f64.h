@@ -324,17 +324,38 @@ __device__ __forceinline__ double dpp_f64(double x, int ctrl) {
   }
   return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
 }
+// Accumulator r_j of this lane's leaf over K = L / 8 elements known at
+// compile time: every load is issued before the first add (with L known
+// only at run time, each element was its own guarded block, one LDS round
+// trip after another).
+template <int K>
+__device__ __forceinline__ double sum_sq_acc(const int16_t *hm, const int8_t *he, int base) {
+  double x[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = base + 8 * k;
+    x[k] = bfp_val(hm[i], he[i >> 4]);
+  }
+  double r = x[0] * x[0];
+#pragma unroll
+  for (int k = 1; k < K; ++k) r = r + x[k] * x[k];
+  return r;
+}
 __device__ __forceinline__ double sum_sq_wave(const int16_t *hm, const int8_t *he, int nl, int L) {
   const int lane = threadIdx.x & 63;
   const int f = lane >> 3, j = lane & 7;
   const int base = (f < nl ? f : 0) * L + j;
   double r = 0.0;
+  if (L == 72) {   // uniform: D = 576 (8 leaves of 72)
+    r = sum_sq_acc<9>(hm, he, base);
+  } else {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if (8 * k < L) {
-      const int i = base + 8 * k;
-      const double x = bfp_val(hm[i], he[i >> 4]);
-      r = k == 0 ? x * x : r + x * x;
+    for (int k = 0; k < 16; ++k) {
+      if (8 * k < L) {
+        const int i = base + 8 * k;
+        const double x = bfp_val(hm[i], he[i >> 4]);
+        r = k == 0 ? x * x : r + x * x;
+      }
     }
   }
   r = r + dpp_f64(r, 0xB1);
