@@ -39,11 +39,11 @@ inline size_t attn_grp_lds_bytes(int max_ctx, int G) {
 // (its k_put / v_put store the cache row, out the outputs).  PPW 2: at most
 // 128 positions; 3: at most 256.  a.dump must be null.
 //
-// Every K and V row of the cache (slots 0 .. max_ctx-1, the group's 64
-// mantissas and 4 exponents) is loaded at entry, before the q|k|v input and
-// the position are known, in 16-byte parts (thread t: part t % 8 of rows
-// t / 8 + 64j), and written to LDS once the input is in; row pos is this
-// launch's k (after RoPE) and v, written by waves G and G + 1 instead.
+// The K and V rows 0 .. pos-1 of the cache (the group's 64 mantissas and 4
+// exponents a row) are loaded at entry, before the q|k|v input is in, in
+// 16-byte parts (thread t: part t % 8 of rows t / 8 + 64j), and written to
+// LDS once the input is in; row pos is this launch's k (after RoPE) and v,
+// written by waves G and G + 1 instead.
 template <int PPW, class IO, class PosF>
 __device__ __forceinline__ void attn_group_body(const LayerArgs &a, IO &io, int g, int b, PosF posf,
                                                 double *dsm) {
@@ -69,20 +69,24 @@ __device__ __forceinline__ void attn_group_body(const LayerArgs &a, IO &io, int 
   int16_t *Vm = a.v_m + (long long)b * a.max_ctx * kv_tok;
   int8_t *Ve = a.v_e + (long long)b * a.max_ctx * (kv_tok / 16);
 
-  // the staging loads (rows clamped to the cache's last slot, so no load
-  // sits in a branch; rows past the position are never read)
+  // the position first (the q|k|v input, polled below, arrives well after
+  // it), then the staging loads of rows 0 .. pos-1 only (rows from pos on
+  // read row 0, a cache hit, and are never used; no load sits in a branch)
+  const int2 pp = posf();   // (KV slot, RoPE position)
+  const int pos = pp.x, rpos = pp.y;
   uint4 kr[RT], vr[RT];
   {
     const int16_t *Kg = Km + (long long)g * HD + 8 * (tid & 7);
     const int16_t *Vg = Vm + (long long)g * HD + 8 * (tid & 7);
 #pragma unroll
     for (int j = 0; j < RT; ++j) {
-      const int t = min((tid >> 3) + 64 * j, a.max_ctx - 1);
+      int t = (tid >> 3) + 64 * j;
+      t = t < pos ? t : 0;
       kr[j] = io.k16(Kg + t * kv_tok);
       vr[j] = io.v16(Vg + t * kv_tok);
     }
   }
-  const int te = min(tid & (ER - 1), a.max_ctx - 1);
+  const int te = (tid & (ER - 1)) < pos ? (tid & (ER - 1)) : 0;
   const int ker = io.ke4(Ke + (te * kv_tok + (long long)g * HD) / 16);
   const int ver = io.ve4(Ve + (te * kv_tok + (long long)g * HD) / 16);
   // this wave's q|k|v input: q head g*G + w (waves below G), k (wave G),
@@ -90,9 +94,6 @@ __device__ __forceinline__ void attn_group_body(const LayerArgs &a, IO &io, int 
   int in_m, in_e;
   io.qkv(w < G ? (g * G + w) * HD + l : (w == G ? a.D + g * HD + l : a.D + a.KV + g * HD + l), in_m, in_e);
   io.mark(ATT_MARK_QKV);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  const int2 pp = posf();   // (KV slot, RoPE position)
-  const int pos = pp.x, rpos = pp.y;
   const int n = pos + 1;
   const double *cs = a.rope + (long long)rpos * HD;
   double rcos = 0.0, rsin = 0.0;
@@ -115,16 +116,16 @@ __device__ __forceinline__ void attn_group_body(const LayerArgs &a, IO &io, int 
     vst[pos * 64 + l] = (int16_t)in_m;
     if ((l & 15) == 0) vex[pos * 4 + (l >> 4)] = (int8_t)in_e;
   }
-  // the staged rows into LDS (all but row pos)
+  // the staged rows 0 .. pos-1 into LDS
 #pragma unroll
   for (int j = 0; j < RT; ++j) {
     const int t = (tid >> 3) + 64 * j;
-    if (t < a.max_ctx && t != pos) {
+    if (t < pos) {
       *reinterpret_cast<uint4 *>(kst + t * AG_KS + 8 * (tid & 7)) = kr[j];
       *reinterpret_cast<uint4 *>(vst + t * 64 + 8 * (tid & 7)) = vr[j];
     }
   }
-  if (tid < ER && tid < a.max_ctx && tid != pos) {
+  if (tid < ER && tid < pos) {
     *reinterpret_cast<int *>(kex + tid * 4) = ker;
     *reinterpret_cast<int *>(vex + tid * 4) = ver;
   }
