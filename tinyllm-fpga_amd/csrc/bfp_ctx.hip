@@ -193,6 +193,11 @@ LayerArgs layer_args(bfp_ctx *c, int layer, int batch) {
   }
   a.w_qkv_m = reinterpret_cast<const uint4 *>(c->qkv_m + layer * c->s_qkv_m);
   a.w_qkv_e = c->qkv_e + layer * c->s_qkv_e;
+  {
+    const int ln = layer + 1 < c->d.NL ? layer + 1 : layer;
+    a.w_qkv_next_m = reinterpret_cast<const uint4 *>(c->qkv_m + ln * c->s_qkv_m);
+    a.w_qkv_next_e = c->qkv_e + ln * c->s_qkv_e;
+  }
   a.w_o_m = reinterpret_cast<const uint4 *>(c->o_m + layer * c->s_o_m);
   a.w_o_e = c->o_e + layer * c->s_o_e;
   a.w_gu_m = reinterpret_cast<const uint4 *>(c->gu_m + layer * c->s_gu_m);

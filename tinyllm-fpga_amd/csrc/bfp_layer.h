@@ -64,6 +64,10 @@ struct LayerArgs {
   // null; t_abort is set when one of their bounded waits gives up
   unsigned *t_h1, *t_h;
   const double *g1_next;
+  // the next layer's Q|K|V weights (the D launch's RMSNorm workgroups touch
+  // them while they wait), or this layer's for the last layer
+  const uint4 *w_qkv_next_m;
+  const int8_t *w_qkv_next_e;
   // batched decode: q|k|v also as tagged words (batch x (D + 2KV)), read by
   // the attention workgroups of the Q|K|V launch (k_qkv_attn_mx), or null
   unsigned *t_qkv;

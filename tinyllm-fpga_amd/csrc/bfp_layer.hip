@@ -445,6 +445,31 @@ __global__ __launch_bounds__(64 * ATT_WAVES, (PPW == 3 ? 6 : 4)) void k_qkv_attn
   mx_mark(mx_tr<TR>(a, MX_K_QKV), 5);
 }
 
+// K 16-byte loads of thread i (of n) over the byte ranges [m, m + mb) and
+// one over [e, e + eb), offsets clamped into them (no load in a branch): a
+// later launch's weights brought into the memory-side cache, which every
+// XCD shares, by workgroups that would otherwise only wait.  Returns a value
+// the caller keeps alive to its end.  At config 5 the O, G/U and D launches
+// averaged 0.3-0.45 us less each and the decode 0.25% more tokens/s (three
+// alternated runs of each form on one box).
+template <int K>
+__device__ __forceinline__ unsigned mall_touch(const void *m, size_t mb, const void *e, size_t eb, int i, int n) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(m), (short)0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t re = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(e), (short)0, 0x7fffffff, 0x00020000);
+  unsigned acc = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {   // K x n x 16 bytes >= mb for the callers' sizes
+    size_t off = ((size_t)i + (size_t)k * n) * 16;
+    off = off < mb ? off : mb - 16;
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rm, (int)off, 0, 0);
+    acc ^= v[0];
+  }
+  const size_t oe = (size_t)i * 16 < eb ? (size_t)i * 16 : eb - 16;
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(re, (int)oe, 0, 0);
+  return acc ^ v[0];
+}
+
 // AttnTagIO whose phase stamps, in a traced launch (TR), go to the Q|K|V
 // kernel's trace rows at the workgroup's id (past the matvec blocks'):
 // 0 entry, 1 wave 0's q|k|v in, 2 RoPE and the staged rows in LDS, 3
@@ -468,10 +493,15 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 2) void k_qkv_attng_mx(LayerArgs a,
   if ((int)blockIdx.x >= nblk) {
     const int L = blockIdx.x - nblk, gk = L % a.H_KV, b = L / a.H_KV;
     mx_mark(mx_tr<TR>(a, MX_K_QKV), 0);
+    // the O launch's weights, touched while these workgroups wait for their
+    // q|k|v words, so the O blocks find them in the memory-side cache
+    const unsigned pf = mall_touch<1>(a.w_o_m, (size_t)a.D * a.D * 2, a.w_o_e, (size_t)a.D * a.D / 16,
+                                   L * blockDim.x + threadIdx.x, (gridDim.x - nblk) * blockDim.x);
     AttnTagIOT<TR> io{{{a.qkv_m + b * nq, a.qkv_e + b * (nq / 16), a.att_m + b * a.D, a.att_e + b * (a.D / 16)},
                        tw_make(a.t_qkv + (long long)b * nq, nq * 4), tw_make(a.t_abort, 4), tag},
                       mx_tr<TR>(a, MX_K_QKV)};
     attn_group_body<PPW>(a, io, gk, b, [&] { return make_int2(cur_kv_pos(a), cur_pos(a)); }, dsm);
+    asm volatile("" ::"v"(pf));
     return;
   }
   const int nT = a.D / 16, bq = nq / 16, c = blockIdx.x % bq, b0 = blockIdx.x / bq * MX_SEQ;
@@ -589,7 +619,11 @@ __global__ __launch_bounds__(64 * MX_WAVES_MAX) void k_o_res_norm_mx(LayerArgs a
   __shared__ int Mo[16 * MX_SEQ];
   extern __shared__ int8_t mx_ex[];
   if ((int)blockIdx.x >= nblk) {
+    // the G/U launch's weights, touched while these workgroups wait for h1
+    const unsigned pf = mall_touch<8>(a.w_gu_m, (size_t)a.FFN * a.D * 4, a.w_gu_e, (size_t)a.FFN * a.D / 8,
+                                      (blockIdx.x - nblk) * blockDim.x + threadIdx.x, (gridDim.x - nblk) * blockDim.x);
     norm_tagged(a, blockIdx.x - nblk, 2, a.t_h1, a.g2, reinterpret_cast<double *>(mx_ex));
+    asm volatile("" ::"v"(pf));
     return;
   }
   const int nT = a.D / 16, c = blockIdx.x % nT, b0 = blockIdx.x / nT * MX_SEQ;
@@ -655,7 +689,12 @@ __global__ __launch_bounds__(64 * MX_WAVES_D) void k_d_res_norm_mx(LayerArgs a, 
   __shared__ int Mo[16 * MX_SEQ];
   extern __shared__ int8_t mx_ex[];
   if ((int)blockIdx.x >= nblk) {
+    // the next layer's Q|K|V weights, touched while these workgroups wait for h
+    const size_t nq = (size_t)a.D + 2 * (size_t)a.KV;
+    const unsigned pf = mall_touch<4>(a.w_qkv_next_m, nq * a.D * 2, a.w_qkv_next_e, nq * a.D / 16,
+                                      (blockIdx.x - nblk) * blockDim.x + threadIdx.x, (gridDim.x - nblk) * blockDim.x);
     norm_tagged(a, blockIdx.x - nblk, 1, a.t_h, a.g1_next, reinterpret_cast<double *>(mx_ex));
+    asm volatile("" ::"v"(pf));
     return;
   }
   const int nT = a.FFN / 16, nc = a.D / 16, c = blockIdx.x % nc, b0 = blockIdx.x / nc * MX_SEQ;
