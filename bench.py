@@ -692,7 +692,47 @@ def layer_leg():
             "layer_step_us": round(us, 2), "steps_per_s": round(1e6 / us, 1),
             "roofline": hbm_roofline(nbytes, us * 1e-6,
                                      "one layer's BFP weights + KV rows 0..pos, mean over "
-                                     "positions 0-6")}
+                                     "positions 0-6"),
+            "dropin": layer_dropin_leg()}
+
+
+def layer_dropin_leg(reps=5):
+    """BASELINE config 1 as written: one layer, 8 positions decoded one at a
+    time from N(0,1) activations (synth.make_layer_inputs, the generator of
+    tests/golden/ref_layer_cfg1.npz), each position one bfp_layer_step_kv
+    call with host buffers -- the drop-in fwd_layer's cost, PCIe copies and
+    the call's synchronisation included.  Wall clock per call, the best of
+    `reps` passes per position; every pass's outputs are compared with the
+    reference's own run of the same layer (the fixture)."""
+    import numpy as np
+    import bfp.api as api
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    f = _fixture("ref_layer_cfg1.npz")
+    seed = int(f["seed"]) if f is not None else 1
+    d = Dims(NL=1, MAX_CTX=16, VOCAB=256)
+    gm = BfpModel(d)
+    gm.load_fp32(synth.make_model(d, seed=seed))
+    xs = synth.make_layer_inputs(d, 8, seed=seed)
+    qin = [tuple(a.reshape(1, -1) for a in api.tile_quantize(xs[p])) for p in range(8)]
+    best = np.full(8, np.inf)
+    exact = True if f is not None else None
+    for _ in range(reps + 1):                      # the first pass warms up
+        gm.reset_kv()
+        for p in range(8):
+            t0 = time.perf_counter()
+            om_, oe_, _ = gm.layer_step_bfp(0, p, *qin[p])
+            best[p] = min(best[p], time.perf_counter() - t0)
+            if f is not None:
+                cm, ce = api.tile_quantize(api.tile_decode(om_[0], oe_[0]))   # canonical form
+                exact = exact and bool((cm.reshape(-1) == f["hout_m"][p]).all() and
+                                       (ce == f["hout_e"][p]).all())
+    gm.close()
+    us = float(best.mean()) * 1e6
+    return {"workload": "config 1 as written: 1 layer, positions 0-7, N(0,1) activations, "
+                        "one host-buffer call per position",
+            "call_us": round(us, 2), "positions_per_s": round(1e6 / us, 1),
+            "outputs_match_reference": exact}
 
 
 # ------------------------------------------------------------ CPU baselines

@@ -31,6 +31,17 @@ __global__ void permute_embed_kernel(const float *__restrict__ v, long long n, i
   vp[q] = v[row * D + 64 * i + 4 * (h + 4 * j) + c];
 }
 
+// Two word-granular copies in one launch (n0, n1 32-bit words): the
+// single-layer boundary call's input from pinned host memory into the
+// device activations, and its output back.
+__global__ void copy_words2_kernel(const unsigned *__restrict__ s0, unsigned *__restrict__ d0, int n0,
+                                   const unsigned *__restrict__ s1, unsigned *__restrict__ d1, int n1) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n0 + n1; i += gridDim.x * blockDim.x) {
+    if (i < n0) d0[i] = s0[i];
+    else d1[i - n0] = s1[i - n0];
+  }
+}
+
 struct bfp_ctx {
   bfp_dims d{};
   int device = 0, max_batch = 1, max_ctx = 0;
@@ -94,6 +105,11 @@ struct bfp_ctx {
   };
   std::vector<PipeSched> pp_sched;   // by batch size (index batch - 1)
   std::vector<void *> allocs;
+  // pinned, mapped host memory through which the single-layer boundary call
+  // (bfp_layer_step_kv) passes its input and output, read and written by
+  // copy kernels on the stream (made on first use)
+  uint8_t *pin = nullptr, *pin_dev = nullptr;
+  size_t pin_bytes = 0;
   int last_path = -1;   // BFP_PATH_* of the last decode
   int last_form = -1;   // BFP_FORM_* of the last decode
   float last_decode_ms = 0.f, last_gen_ms = 0.f;
@@ -124,8 +140,30 @@ struct bfp_ctx {
     allocs.push_back(*p);
     return BFP_OK;
   }
+  int pinned(size_t bytes) {
+    if (bytes <= pin_bytes) return BFP_OK;
+    if (pin) {
+      HIP_TRY(hipStreamSynchronize(stream));
+      (void)hipHostFree(pin);
+      pin = pin_dev = nullptr;
+      pin_bytes = 0;
+    }
+    void *p = nullptr, *dp = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocMapped | hipHostMallocCoherent);
+    if (e != hipSuccess) return set_err(BFP_ENOMEM, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    e = hipHostGetDevicePointer(&dp, p, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(p);
+      return set_err(BFP_EIO, "hipHostGetDevicePointer: %s", hipGetErrorString(e));
+    }
+    pin = static_cast<uint8_t *>(p);
+    pin_dev = static_cast<uint8_t *>(dp);
+    pin_bytes = bytes;
+    return BFP_OK;
+  }
   ~bfp_ctx() {
     if (stream) (void)hipStreamSynchronize(stream);
+    if (pin) (void)hipHostFree(pin);
     for (void *p : allocs) (void)hipFree(p);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -771,8 +809,19 @@ int bfp_layer_step_kv(bfp_ctx *c, int layer, int pos, int kv_pos, int batch, con
   if (pos < 0) return set_err(BFP_ERANGE, "pos %d is negative", pos);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t s = c->stream;
-  HIP_TRY(hipMemcpyAsync(c->h_m, h_m, (size_t)batch * d.D * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(hipMemcpyAsync(c->h_e, h_e, (size_t)batch * d.D / 16, hipMemcpyHostToDevice, s));
+  // h in and out through pinned host memory, moved by copy kernels (four
+  // pageable hipMemcpyAsync took most of a call's time); D % 64 == 0, so
+  // both parts are whole 32-bit words
+  const size_t bm = (size_t)batch * d.D * 2, be = (size_t)batch * d.D / 16;
+  BFP_TRY(c->pinned(2 * (bm + be)));
+  memcpy(c->pin, h_m, bm);
+  memcpy(c->pin + bm, h_e, be);
+  const int nw = (int)((bm + be) / 4), cgrid = std::min((nw + 255) / 256, 64);
+  hipLaunchKernelGGL(copy_words2_kernel, dim3(cgrid), dim3(256), 0, s,
+                     reinterpret_cast<const unsigned *>(c->pin_dev), reinterpret_cast<unsigned *>(c->h_m),
+                     (int)(bm / 4), reinterpret_cast<const unsigned *>(c->pin_dev + bm),
+                     reinterpret_cast<unsigned *>(c->h_e), (int)(be / 4));
+  BFP_TRY(launch_status("layer input"));
   LayerArgs a = layer_args(c, layer, batch);
   a.pos_const = pos;
   a.kv_pos_const = kv_pos;
@@ -797,8 +846,12 @@ int bfp_layer_step_kv(bfp_ctx *c, int layer, int pos, int kv_pos, int batch, con
     a.dump = c->dump_dev;
   }
   BFP_TRY(launch_layer(a, s));
-  HIP_TRY(hipMemcpyAsync(out_m, c->h_m, (size_t)batch * d.D * 2, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipMemcpyAsync(out_e, c->h_e, (size_t)batch * d.D / 16, hipMemcpyDeviceToHost, s));
+  uint8_t *po = c->pin + bm + be, *po_dev = c->pin_dev + bm + be;
+  hipLaunchKernelGGL(copy_words2_kernel, dim3(cgrid), dim3(256), 0, s,
+                     reinterpret_cast<const unsigned *>(c->h_m), reinterpret_cast<unsigned *>(po_dev),
+                     (int)(bm / 4), reinterpret_cast<const unsigned *>(c->h_e),
+                     reinterpret_cast<unsigned *>(po_dev + bm), (int)(be / 4));
+  BFP_TRY(launch_status("layer output"));
   if (dump) {
     for (int i = 0; i < ST_COUNT; ++i) {
       if (dump->m[i])
@@ -810,6 +863,8 @@ int bfp_layer_step_kv(bfp_ctx *c, int layer, int pos, int kv_pos, int batch, con
     }
   }
   HIP_TRY(hipStreamSynchronize(s));
+  memcpy(out_m, po, bm);
+  memcpy(out_e, po + bm, be);
   return BFP_OK;
 }
 
