@@ -133,6 +133,56 @@ def test_head_sequence_lanes_equal_single(gpu, D, vocab):
     gm.close()
 
 
+@pytest.mark.parametrize("D,vocab", [(576, 4176), (128, 512), (192, 1040)],
+                         ids=["d576-ragged", "d128", "d192"])
+def test_head_bounded_equals_full(gpu, D, vocab):
+    """The bounded head (an exact int16 dot product brackets every logit;
+    only the 16-row blocks that can hold the largest one get float64
+    logits) returns the argmax of the full float64 head, first index on
+    ties, over 70 sequences (a group of 64 and a ragged one) and a
+    vocabulary whose last workgroup is short.  The embedding holds exact ties
+    within and across blocks (rows 5, 9; 3, 40 = -(5)), rows one float32 ulp
+    apart (100, 101, in two sequences' lead), zero rows (200-215, a whole
+    block, and 300) and rows of very different scales."""
+    from bfp import Dims, synth
+    from bfp.model import BfpModel
+    H = D // 64
+    cfg = dict(D=D, H_Q=H, H_KV=1, HD=64, FFN=2 * D, NL=1, MAX_CTX=8, VOCAB=vocab)
+    d = Dims(**cfg)
+    fm = synth.make_model(d, seed=37)
+    E = fm.embed
+    V = E[7].copy() * np.float32(60.0)
+    E[5] = V
+    E[9] = V
+    E[3] = -V
+    E[40] = -V
+    E[100] = E[11] * np.float32(55.0)
+    E[101] = np.nextafter(E[100], np.float32(np.inf))
+    E[200:216] = 0.0
+    E[300] = 0.0
+    E[400] *= np.float32(1e-30)
+    E[401] *= np.float32(4.0)
+    E[402] *= np.float32(1e-5)
+    gm = BfpModel(d, max_batch=70)
+    gm.load_fp32(fm)
+    rng = np.random.default_rng(37)
+    hs = [sim.fp_quantize_vec(rng.standard_normal(d.D) * (0.3 + 0.01 * b)) for b in range(70)]
+    hs[1] = sim.fp_quantize_vec(E[11].astype(np.float64) * 40.0)    # leads with rows 100/101
+    hs[2] = sim.fp_quantize_vec(-E[11].astype(np.float64) * 40.0)
+    hs[3] = np.zeros(d.D)                                            # all logits +0
+    q = [sim.tile_quantize(h) for h in hs]
+    hm = np.stack([x[0].reshape(-1) for x in q])
+    he = np.stack([x[1] for x in q])
+    am_full, lg = gm.head(hm, he, logits=True)      # logits asked for: the float64 matrix-core head
+    am_b, _ = gm.head(hm, he)                       # argmax only: the bounded head
+    for b in range(70):
+        want = int(np.argmax(lg[b]))                # first index on ties
+        assert am_full[b] == want, b
+        assert am_b[b] == want, (b, am_b[b], want)
+    assert am_b[3] == 0                             # every logit +0: the first row
+    gm.close()
+
+
 @pytest.mark.parametrize("graph", [True, False], ids=["graph", "direct"])
 def test_decode_tiny(gpu, graph):
     d, om, gm = _setup(TINY, seed=5)

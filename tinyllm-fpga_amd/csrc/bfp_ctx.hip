@@ -56,6 +56,13 @@ struct bfp_ctx {
   float *embed = nullptr;
   float *embedp = nullptr;     // the embedding permuted per row for the batched head
                                // (made when max_batch >= HEAD_SEQ_MIN)
+  // the bounded head (made with embedp): the embedding as split int16 with
+  // per-row meta, and per step the quantised hidden, its per-sequence
+  // record and the per-block bounds
+  uint4 *embq = nullptr, *hq_x = nullptr;
+  HeadQRow *embq_meta = nullptr;
+  HeadQSeq *hq_seq = nullptr;
+  double2 *hq_blk = nullptr;
   // activations (max_batch sequences)
   int16_t *h_m = nullptr, *h1_m = nullptr, *qkv_am = nullptr, *att_m = nullptr, *mlp_m = nullptr;
   int8_t *h_e = nullptr, *h1_e = nullptr, *qkv_ae = nullptr, *att_e = nullptr, *mlp_e = nullptr;
@@ -204,10 +211,26 @@ int head_part_max(const bfp_ctx *c) {
   return m;
 }
 
+// The bounded head (argmax only) where its copy exists, no logits are asked
+// for and the batch takes the float64 matrix-core form; BFP_HEAD_BOUNDED=0
+// keeps k_head_mx.
+bool head_bounded(const bfp_ctx *c, int batch, const double *logits) {
+  const char *v = getenv("BFP_HEAD_BOUNDED");
+  return c->embq && !logits && head_seq_form(c->d.D, batch, c->embedp != nullptr) && !(v && atoi(v) == 0);
+}
+
 HeadArgs head_args(bfp_ctx *c, int batch, double *logits) {
   const bfp_dims &d = c->d;
-  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, head_nwg(c, batch), c->h_m, c->h_e, c->norm_w,
+  const bool bq = head_bounded(c, batch, logits);
+  HeadArgs ha{d.D, d.VOCAB, batch, c->head_rows, bq ? 1 : head_nwg(c, batch), c->h_m, c->h_e, c->norm_w,
               c->embed, c->part_v, c->part_i, logits, c->hn, c->embedp};
+  if (bq) {
+    ha.embq = c->embq;
+    ha.embq_meta = c->embq_meta;
+    ha.hq_x = c->hq_x;
+    ha.hq_seq = c->hq_seq;
+    ha.hq_blk = c->hq_blk;
+  }
   return ha;
 }
 
@@ -544,7 +567,12 @@ bfp_ctx *bfp_create(const bfp_dims *dims, int device, int max_batch) {
       (rc = c->alloc((void **)&c->rope_row, sizeof(double) * d.HD)) ||
       (rc = c->alloc((void **)&c->embed, sizeof(float) * (size_t)d.VOCAB * d.D)) ||
       (max_batch >= HEAD_SEQ_MIN && d.D % 64 == 0 && d.D <= 576 &&
-       (rc = c->alloc((void **)&c->embedp, sizeof(float) * (size_t)d.VOCAB * d.D))) ||
+       ((rc = c->alloc((void **)&c->embedp, sizeof(float) * (size_t)d.VOCAB * d.D)) ||
+        (rc = c->alloc((void **)&c->embq, (size_t)d.VOCAB * d.D * 2)) ||
+        (rc = c->alloc((void **)&c->embq_meta, sizeof(HeadQRow) * (size_t)d.VOCAB)) ||
+        (rc = c->alloc((void **)&c->hq_x, (size_t)(B + 15) / 16 * (d.D / 64) * 64 * 32)) ||
+        (rc = c->alloc((void **)&c->hq_seq, sizeof(HeadQSeq) * B)) ||
+        (rc = c->alloc((void **)&c->hq_blk, sizeof(double2) * B * (d.VOCAB / 16))))) ||
       (rc = c->alloc((void **)&c->h_m, 2 * B * d.D)) || (rc = c->alloc((void **)&c->h_e, B * d.D / 16)) ||
       (rc = c->alloc((void **)&c->h1_m, 2 * B * d.D)) ||
       (rc = c->alloc((void **)&c->h1_e, B * d.D / 16)) ||
@@ -725,6 +753,7 @@ int bfp_load_weights(bfp_ctx *c, int which, int layer, const float *fp32, const 
         hipLaunchKernelGGL(permute_embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                            s, c->embed, n, d.D, c->embedp);
         BFP_TRY(launch_status("embed permute"));
+        BFP_TRY(launch_embq_build(c->embed, d.VOCAB, d.D, c->embq, c->embq_meta, s));
         HIP_TRY(hipStreamSynchronize(s));
       }
       return BFP_OK;

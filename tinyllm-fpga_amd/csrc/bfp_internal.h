@@ -68,6 +68,7 @@ void rope_row(double *cs, int pos, int HD, double base);
 namespace bfp {
 struct LayerArgs;
 struct HeadArgs;
+struct HeadQRow;
 struct CtlArgs;
 struct EmbedArgs;
 // mx_traced: the matrix-core matvecs stamp their phases into the buffer
@@ -84,6 +85,8 @@ int raise_lds_limit(const void *f, int bytes);
 int head_workgroups(int vocab, int D, int rows_single, int batch, bool have64);
 int launch_embed(const EmbedArgs &a, hipStream_t s);
 int launch_head(const HeadArgs &a, hipStream_t s);
+// The bounded head's copy of the embedding (k_embq_build).
+int launch_embq_build(const float *embed, int VOCAB, int D, uint4 *q, HeadQRow *meta, hipStream_t s);
 int launch_ctl(const CtlArgs &a, hipStream_t s);
 // k_ctl + step increment + the next step's k_embed in one launch; the step
 // counter's arrival count lives at state[1 + batch] and must be 0 at entry.

@@ -110,6 +110,22 @@ struct RtlHeadArgs {
   int *token;                                // argmax out (device)
 };
 
+// One sequence of the bounded head (k_head_norm's quantised hidden): the
+// scale exponent eh (hidden = 2^eh * q up to 2^eh / 2 an element), the sum
+// of q, and an upper bound of the hidden's 1-norm.
+struct HeadQSeq {
+  double h1;
+  int eh, sumx;
+};
+// One embedding row of the bounded head: its scale exponent er (row =
+// 2^er * q up to 2^er / 2 an element), sum q, and the row's parts of the
+// bound, r1 = 2^(er-1) + 2^-45 max |row| and r2 = 2^(er-1) sum |q| (both 0
+// for a zero row).
+struct HeadQRow {
+  int er, sumw;
+  double r1, r2;
+};
+
 struct HeadArgs {
   int D, VOCAB, batch, rows_per_wg, n_wg;
   const int16_t *h_m; const int8_t *h_e;   // final hidden (BFP)
@@ -120,7 +136,17 @@ struct HeadArgs {
   double *hn;                              // (batch, D) normed hidden, batch > 1 path
   const float *embedp;                     // (VOCAB, D) the embedding permuted per row, or null:
                                            // [row][(4i + c) * 16 + 4h + j] = embed[row][64i + 4(h + 4j) + c]
+  // the bounded head (k_headq_mx + k_headq_pick; all null: not used)
+  const uint4 *embq;                       // the embedding as int16, split bytes, matrix-core layout
+  const HeadQRow *embq_meta;               // (VOCAB,)
+  uint4 *hq_x;                             // the quantised hidden, split bytes, matrix-core layout
+  HeadQSeq *hq_seq;                        // (batch,)
+  double2 *hq_blk;                         // (batch, VOCAB / 16) per 16-row block: max lower, max upper bound
 };
+
+// The bounded head runs from HEAD_SEQ_MIN sequences (with the permuted
+// copy's conditions, D % 64 == 0 and D <= 576) unless logits are asked for.
+constexpr int HEADQ_SEQ = 64;   // sequences per k_headq_mx workgroup
 
 // Batches from HEAD_SEQ_MIN sequences on run the head on the float64 matrix
 // cores (k_head_mx), when the embedding's permuted copy exists and

@@ -786,11 +786,71 @@ __global__ __launch_bounds__(256) void k_head_logits(HeadArgs a) {
 // logit is summed in the same order as k_head_logits (lane l16 of a row's 16
 // lanes accumulates k = 64i + 4*l16 + c, then the same butterfly), so the
 // logits are bit-identical to the batch-1 kernel's.
+//
+// With the bounded head (a.hq_x set) the workgroup also quantises its
+// normed hidden h for k_headq_mx: q = rint(h / 2^eh) with the power of two
+// 2^eh that puts max |h| in (16383, 32767], so |h - 2^eh q| <= 2^eh / 2 and
+// |q| <= 32767; q goes out as split bytes (q = 256 qh + ql + 128) in
+// k_embq_build's layout with sequence b % 16 in place of the row (word
+// (((b / 16) * G + g) * 2 + p) * 64 + 16 kg + b % 16), with eh, sum q and
+// an upper bound of sum |h| (any summation order is within 575 rounding
+// units, so the sum times 1 + 2^-40 bounds it).
 __global__ __launch_bounds__(256) void k_head_norm(HeadArgs a) {
   extern __shared__ double dsm[];
-  const int b = blockIdx.x;
-  final_norm(a.h_m + b * a.D, a.h_e + b * (a.D / 16), a.norm_w, a.D, dsm, dsm + 3 * a.D,
-             a.hn + (long long)b * a.D);
+  const int b = blockIdx.x, D = a.D, tid = threadIdx.x;
+  if (!a.hq_x) {
+    final_norm(a.h_m + b * D, a.h_e + b * (D / 16), a.norm_w, D, dsm, dsm + 3 * D,
+               a.hn + (long long)b * D);
+    return;
+  }
+  __shared__ double rmax[4], rsum[4];
+  __shared__ int rq[4];
+  final_norm(a.h_m + b * D, a.h_e + b * (D / 16), a.norm_w, D, dsm, dsm + 3 * D, dsm);
+  lds_barrier();
+  double mx = 0.0, s1 = 0.0;
+  for (int i = tid; i < D; i += 256) {
+    const double v = dsm[i];
+    a.hn[(long long)b * D + i] = v;
+    mx = fmax(mx, fabs(v));
+    s1 += fabs(v);
+  }
+  for (int o = 32; o; o >>= 1) {
+    mx = fmax(mx, __shfl_xor(mx, o));
+    s1 += __shfl_xor(s1, o);
+  }
+  if ((tid & 63) == 0) {
+    rmax[tid >> 6] = mx;
+    rsum[tid >> 6] = s1;
+  }
+  lds_barrier();
+  mx = fmax(fmax(rmax[0], rmax[1]), fmax(rmax[2], rmax[3]));
+  int eh = 0;
+  if (mx > 0.0) {
+    eh = ilogb(mx) - 14;
+    if (ldexp(mx, -eh) > 32767.0) ++eh;
+  }
+  const int G = D / 64;
+  int sx = 0;
+  for (int sl = tid; sl < D / 16; sl += 256) {   // slot sl: elements 16sl .. +15, group sl / 4
+    unsigned hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int v = (int)rint(ldexp(dsm[16 * sl + j], -eh));
+      sx += v;
+      hw[j >> 2] |= ((unsigned)(v >> 8) & 0xffu) << (8 * (j & 3));
+      lw[j >> 2] |= ((unsigned)((v & 255) - 128) & 0xffu) << (8 * (j & 3));
+    }
+    uint4 *o = a.hq_x + ((long long)(b / 16) * G + (sl >> 2)) * 128 + 16 * (sl & 3) + (b & 15);
+    o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    o[64] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+  for (int o = 32; o; o >>= 1) sx += __shfl_xor(sx, o);
+  if ((tid & 63) == 0) rq[tid >> 6] = sx;
+  lds_barrier();
+  if (tid == 0) {
+    const double h1 = ((rsum[0] + rsum[1]) + (rsum[2] + rsum[3])) * (1.0 + 0x1p-40);
+    a.hq_seq[b] = HeadQSeq{h1, eh, (rq[0] + rq[1]) + (rq[2] + rq[3])};
+  }
 }
 
 constexpr int HEAD_SEQ_GROUP = 16;   // most sequences staged in LDS at once
@@ -1412,6 +1472,257 @@ __global__ __launch_bounds__(512) void k_head_mx(HeadArgs a, int rpw) {
   }
 }
 
+// ------------------------------------------------------------ bounded head
+// The batched head's argmax without every float64 logit.  L(s, r), the
+// logit k_head_mx forms (FMA chains and butterfly of k_head_logits), is
+// bracketed for every (sequence, row) by an exact integer dot product of
+// the two operands quantised to int16: with h = 2^eh qh + dh, |dh| <= 2^eh/2
+// (k_head_norm) and e_r = 2^er qe + de, |de| <= 2^er/2 (k_embq_build),
+//   |h.e_r - 2^(eh+er) qh.qe| <= 2^er/2 |h|_1 + 2^(eh+er)/2 |qe|_1,
+// and |L - h.e_r| <= 40 rounding units of sum |h_k e_k| <= |h|_1 max|e_r|
+// (a chain of 36 FMAs and 4 adds per term; 2^-45 is taken).  qh.qe is exact
+// (|qh.qe| < 2^40) and 2^(eh+er) qh.qe is exact in float64, so with B the
+// bound (rounded outward) every logit lies in [A - B, A + B].  B is formed
+// as |h|_1 r1 + 2^eh r2 with the row's r1 = 2^(er-1) + 2^-45 max|e_r| and
+// r2 = 2^(er-1) |qe|_1, then enlarged by 2^-20 of itself (far more than its
+// few roundings) and 2^-50 |A| (the roundings of A - B and A + B).  The row with
+// the largest L (first index on ties) has A + B >= L >= every other row's
+// A - B, so it lies in a 16-row block whose largest upper bound reaches the
+// largest lower bound T of all rows: k_headq_pick forms the exact logits of
+// those blocks only (usually one) and takes their argmax, which is the
+// argmax of all of them.
+
+// The embedding as the bounded head reads it: row r as int16 q with its own
+// scale 2^er (max |e_r| / 2^er in (16383, 32767]), split bytes (q = 256 qh +
+// ql + 128, qh = q >> 8, ql = (q & 255) - 128) in the operand layout of
+// v_mfma_i32_16x16x64_i8 (lane L: row L % 16, columns 16 (L / 16) .. +15 of
+// a 64-column group, byte j = column 16 (L / 16) + j; checked on the GPU):
+// 16-byte word ((((r / 16) * G + g) * 2 + p) * 64 + 16 kg + r % 16 holds the
+// high (p = 0) or low (p = 1) bytes of elements 64g + 16kg .. +15, so each
+// plane of a group is 1 KB read by one wave-wide load.  meta[r]: the row's
+// record (HeadQRow).  One workgroup per 16 rows.
+__global__ __launch_bounds__(256) void k_embq_build(const float *__restrict__ E, int D,
+                                                    uint4 *__restrict__ q, HeadQRow *__restrict__ meta) {
+  const int chunk = blockIdx.x, tid = threadIdx.x, i = tid >> 4, l16 = tid & 15;
+  const long long r = (long long)chunk * 16 + i;
+  const int G = D / 64;
+  const float *row = E + r * D;
+  float mx = 0.f;
+  for (int k = l16; k < D; k += 16) mx = fmaxf(mx, fabsf(row[k]));
+  for (int o = 8; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+  int er = 0;
+  if (mx > 0.f) {
+    er = ilogb((double)mx) - 14;
+    if (ldexp((double)mx, -er) > 32767.0) ++er;
+  }
+  int sw = 0, s1 = 0;
+  for (int sl = l16; sl < D / 16; sl += 16) {   // 16-element slot sl: group sl / 4, kg sl % 4
+    unsigned hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int v = (int)rint(ldexp((double)row[16 * sl + j], -er));
+      sw += v;
+      s1 += v < 0 ? -v : v;
+      hw[j >> 2] |= ((unsigned)(v >> 8) & 0xffu) << (8 * (j & 3));
+      lw[j >> 2] |= ((unsigned)((v & 255) - 128) & 0xffu) << (8 * (j & 3));
+    }
+    uint4 *o = q + ((long long)chunk * G + (sl >> 2)) * 128 + 16 * (sl & 3) + i;
+    o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    o[64] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+  for (int o = 8; o; o >>= 1) {
+    sw += __shfl_xor(sw, o, 16);
+    s1 += __shfl_xor(s1, o, 16);
+  }
+  if (l16 == 0) {
+    const bool z = mx == 0.f;
+    meta[r] = HeadQRow{er, sw, z ? 0.0 : ldexp(1.0, er - 1) + 0x1p-45 * (double)mx,
+                       z ? 0.0 : ldexp((double)s1, er - 1)};
+  }
+}
+
+// Lower and upper bounds of the logits, per (sequence, 16-row block): each
+// wave one block of rows against the workgroup's (up to) 64 sequences, in
+// groups of 16 (the matrix-core tile).  With W = 256 Wh + Wl + 128 and
+// x = 256 xh + xl + 128 over the D products,
+//   sum W x = 65536 P(Wh, xh) + 256 (P(Wh, xl) + P(Wl, xh)) + P(Wl, xl)
+//             + 128 (sum W + sum x) - 16384 D,
+// each P one v_mfma_i32_16x16x64_i8 per 64 columns (|P| < 2^24 in int32).
+// Lane L owns rows 4 (L / 16) + v of the block and sequence L % 16 of the
+// group; the block's maxima over its rows go to hq_blk[s][block].
+typedef int headq_v4 __attribute__((ext_vector_type(4)));
+template <int G>
+__global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
+  extern __shared__ uint4 xq[];   // [4 groups][G][2 planes][64 lanes]
+  __shared__ HeadQSeq sq[HEADQ_SEQ];
+  __shared__ HeadQRow rq[8 * 16];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, kg = lane >> 4, i = lane & 15;
+  const int b0 = blockIdx.y * HEADQ_SEQ;
+  const int nq = min(4, (a.batch - b0 + 15) / 16);
+  const int nch = a.VOCAB / 16;
+  const int c = min(blockIdx.x * 8 + w, nch - 1);   // past the end: block nch-1 again, not stored
+  // this wave's weights (2G 16-byte words a lane) first, then the stage
+  uint4 W[G][2];
+  const uint4 *pw = a.embq + (long long)c * G * 128 + lane;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    W[g][0] = ld_nt(pw + 128 * g);
+    W[g][1] = ld_nt(pw + 128 * g + 64);
+  }
+  for (int k = tid; k < nq * G * 128; k += 512) xq[k] = a.hq_x[(long long)(b0 / 16) * G * 128 + k];
+  if (tid < 8 * 16) {   // the workgroup's rows' records (the last block again past the end)
+    const int r = blockIdx.x * 128 + tid;
+    rq[tid] = a.embq_meta[r < a.VOCAB ? r : a.VOCAB - 16 + (r & 15)];
+  }
+  for (int k = tid; k < HEADQ_SEQ; k += 512)
+    if (b0 + k < a.batch) sq[k] = a.hq_seq[b0 + k];
+  __syncthreads();
+  const bool store = blockIdx.x * 8 + w < nch;
+  for (int q = 0; q < nq; ++q) {   // uniform
+    headq_v4 hh = {0, 0, 0, 0}, c1 = {0, 0, 0, 0}, c2 = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint4 xh4 = xq[(q * G + g) * 128 + lane], xl4 = xq[(q * G + g) * 128 + 64 + lane];
+      const headq_v4 wh = {(int)W[g][0].x, (int)W[g][0].y, (int)W[g][0].z, (int)W[g][0].w};
+      const headq_v4 wl = {(int)W[g][1].x, (int)W[g][1].y, (int)W[g][1].z, (int)W[g][1].w};
+      const headq_v4 xh = {(int)xh4.x, (int)xh4.y, (int)xh4.z, (int)xh4.w};
+      const headq_v4 xl = {(int)xl4.x, (int)xl4.y, (int)xl4.z, (int)xl4.w};
+      hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xh, hh, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xl, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xh, c2, 0, 0, 0);
+      ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xl, ll, 0, 0, 0);
+    }
+    const int s = b0 + 16 * q + i;
+    const HeadQSeq Q = sq[16 * q + i];
+    double mlo = -INFINITY, mhi = -INFINITY;
+    const long long sx = 128LL * Q.sumx - 16384LL * a.D;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const HeadQRow &Mv = rq[16 * w + 4 * kg + v];
+      // a zero row (r1 = r2 = 0): S = 0, so lo = hi = +0, its exact logit
+      const long long S = ((long long)hh[v] << 16) + ((long long)(c1[v] + c2[v]) << 8) + ll[v] +
+                          128LL * Mv.sumw + sx;
+      const double A = ldexp((double)S, Mv.er + Q.eh);
+      double B = fma(Q.h1, Mv.r1, ldexp(Mv.r2, Q.eh));
+      B = fma(B, 0x1p-20, B) + 0x1p-50 * fabs(A);
+      double lo = A - B, hi = A + B;
+      if (Mv.er + Q.eh < -1000) {   // near the underflow range: always a candidate
+        lo = -INFINITY;
+        hi = INFINITY;
+      }
+      mlo = fmax(mlo, lo);
+      mhi = fmax(mhi, hi);
+    }
+    mlo = fmax(mlo, __shfl_xor(mlo, 16));
+    mhi = fmax(mhi, __shfl_xor(mhi, 16));
+    mlo = fmax(mlo, __shfl_xor(mlo, 32));
+    mhi = fmax(mhi, __shfl_xor(mhi, 32));
+    if (store && kg == 0 && s < a.batch) a.hq_blk[(long long)s * nch + c] = make_double2(mlo, mhi);
+  }
+}
+
+// Sequence b's argmax from the bounds: T = the largest lower bound; the
+// blocks whose upper bound reaches T get their 16 exact logits
+// (k_head_logits' FMA chains and butterfly: the values k_head_mx forms) and
+// the argmax over them, first index on ties (a rule that does not depend on
+// the order the blocks are taken in), is the head's (part_v / part_i [b],
+// one entry a sequence).  All of a thread's bound loads are issued at once;
+// the candidate blocks go to an LDS list, two at a time through the
+// workgroup (16 lanes a row).
+constexpr int HEADQ_PICK_T = 512;
+constexpr int HEADQ_PICK_PER = 8;   // blocks a thread (VOCAB / 16 <= 4096 in one batch)
+template <int MAXD64, bool EXACT>
+__global__ __launch_bounds__(HEADQ_PICK_T) void k_headq_pick(HeadArgs a) {
+  extern __shared__ double hs[];   // D, then the candidate list (VOCAB / 16 ints)
+  __shared__ double rv[HEADQ_PICK_T / 64];
+  __shared__ int ri[HEADQ_PICK_T / 64];
+  __shared__ int ncand;
+  const int b = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int nch = a.VOCAB / 16, d64 = a.D / 64, l16 = tid & 15;
+  int *cand = reinterpret_cast<int *>(hs + a.D);
+  if (tid == 0) ncand = 0;
+  for (int k = tid; k < a.D; k += HEADQ_PICK_T) hs[k] = a.hn[(long long)b * a.D + k];
+  const double2 *blk = a.hq_blk + (long long)b * nch;
+  double t = -INFINITY;
+  for (int c0 = tid; c0 < nch; c0 += HEADQ_PICK_T * HEADQ_PICK_PER) {   // one pass up to 4096 blocks
+    double2 v[HEADQ_PICK_PER];
+#pragma unroll
+    for (int k = 0; k < HEADQ_PICK_PER; ++k) {
+      const int c = c0 + HEADQ_PICK_T * k;
+      v[k] = blk[c < nch ? c : nch - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < HEADQ_PICK_PER; ++k) t = fmax(t, v[k].x);   // clamped entries repeat one
+  }
+  for (int o = 32; o; o >>= 1) t = fmax(t, __shfl_xor(t, o));
+  if (l == 0) rv[w] = t;
+  __syncthreads();
+  double T = rv[0];
+#pragma unroll
+  for (int k = 1; k < HEADQ_PICK_T / 64; ++k) T = fmax(T, rv[k]);
+  for (int c = tid; c < nch; c += HEADQ_PICK_T)   // L2-resident now
+    if (blk[c].y >= T) cand[atomicAdd(&ncand, 1)] = c;
+  __syncthreads();
+  const int n = ncand;
+  double best = -INFINITY;
+  int besti = 0x7fffffff;
+  for (int k0 = 0; k0 < n; k0 += HEADQ_PICK_T / 256) {   // uniform
+    const int k = k0 + (tid >> 8);
+    const int row = cand[k < n ? k : n - 1] * 16 + ((tid >> 4) & 15);
+    const float4 *e4 = reinterpret_cast<const float4 *>(a.embed + (long long)row * a.D);
+    float4 f[MAXD64];
+#pragma unroll
+    for (int j = 0; j < MAXD64; ++j) f[j] = e4[(EXACT || j < d64 ? j : d64 - 1) * 16 + l16];
+    const double x = head_row_dot<MAXD64, EXACT>(f, hs, l16, d64);
+    if (k < n && (x > best || (x == best && row < besti))) {
+      best = x;
+      besti = row;
+    }
+  }
+  argmax_step<1>(best, besti);
+  argmax_step<2>(best, besti);
+  argmax_step<4>(best, besti);
+  argmax_step<8>(best, besti);
+  argmax_step<16>(best, besti);
+  argmax_step<32>(best, besti);
+  if (l == 0) {
+    rv[w] = best;
+    ri[w] = besti;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int k = 1; k < HEADQ_PICK_T / 64; ++k)
+      if (rv[k] > best || (rv[k] == best && ri[k] < besti)) {
+        best = rv[k];
+        besti = ri[k];
+      }
+    a.part_v[b] = best;
+    a.part_i[b] = besti;
+  }
+}
+inline size_t headq_pick_lds(int D, int VOCAB) { return (size_t)D * 8 + (size_t)(VOCAB / 16) * 4; }
+
+typedef void (*headq_mx_fn)(HeadArgs);
+static headq_mx_fn headq_mx_kernel(int G) {
+  switch (G) {
+    case 1: return k_headq_mx<1>;
+    case 2: return k_headq_mx<2>;
+    case 3: return k_headq_mx<3>;
+    case 4: return k_headq_mx<4>;
+    case 5: return k_headq_mx<5>;
+    case 6: return k_headq_mx<6>;
+    case 7: return k_headq_mx<7>;
+    case 8: return k_headq_mx<8>;
+    default: return k_headq_mx<9>;
+  }
+}
+inline int headq_mx_lds(int D) { return 4 * (D / 64) * 64 * 32; }
+
+int launch_embq_build(const float *embed, int VOCAB, int D, uint4 *q, HeadQRow *meta, hipStream_t s) {
+  hipLaunchKernelGGL(k_embq_build, dim3(VOCAB / 16), dim3(256), 0, s, embed, D, q, meta);
+  return launch_status("embedding quantisation");
+}
+
 typedef void (*head_mx_fn)(HeadArgs, int);
 static head_mx_fn head_mx_kernel(int nb) {
   switch (nb) {
@@ -1442,8 +1753,10 @@ int prepare_head_kernels(int D) {
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<9, 2, true>), sh));
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<9, 2, false>), sh));
   BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(k_head_gemv<27, 1, false>), sh));
-  if (D % 64 == 0 && D <= 576)
+  if (D % 64 == 0 && D <= 576) {
     BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(head_mx_kernel(D / 64)), head_mx_lds(D)));
+    BFP_TRY(raise_lds_limit(reinterpret_cast<const void *>(headq_mx_kernel(D / 64)), headq_mx_lds(D)));
+  }
   return BFP_OK;
 }
 
@@ -1460,6 +1773,21 @@ int launch_head(const HeadArgs &a, hipStream_t s) {
   }
   if (!a.hn) return set_err(BFP_EINVAL, "head: no normed-hidden buffer for batch %d", a.batch);
   const bool seqf = head_seq_form(a.D, a.batch, a.embedp != nullptr);
+  if (a.hq_blk) {
+    // the bounded head: one (value, index) a sequence
+    if (!seqf || a.logits || !a.embq || !a.embq_meta || !a.hq_x || !a.hq_seq || a.n_wg != 1)
+      return set_err(BFP_EINVAL, "head: bounded form without its buffers");
+    hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
+    hipLaunchKernelGGL(headq_mx_kernel(a.D / 64), dim3((a.VOCAB / 16 + 7) / 8, (a.batch + HEADQ_SEQ - 1) / HEADQ_SEQ),
+                       dim3(512), headq_mx_lds(a.D), s, a);
+    const size_t shp = headq_pick_lds(a.D, a.VOCAB);
+    if (shp > 64 * 1024) return set_err(BFP_EINVAL, "head: vocabulary %d too large for the bounded form", a.VOCAB);
+    if (a.D == 576)
+      hipLaunchKernelGGL((k_headq_pick<9, true>), dim3(a.batch), dim3(HEADQ_PICK_T), shp, s, a);
+    else
+      hipLaunchKernelGGL((k_headq_pick<9, false>), dim3(a.batch), dim3(HEADQ_PICK_T), shp, s, a);
+    return launch_status("bounded head");
+  }
   if (a.n_wg != head_workgroups(a.VOCAB, a.D, a.rows_per_wg, a.batch, a.embedp != nullptr))
     return set_err(BFP_EINVAL, "head: %d workgroups for batch %d", a.n_wg, a.batch);
   hipLaunchKernelGGL(k_head_norm, dim3(a.batch), dim3(256), sh, s, a);
