@@ -1551,6 +1551,7 @@ __global__ __launch_bounds__(256) void k_embq_build(const float *__restrict__ E,
 // Lane L owns rows 4 (L / 16) + v of the block and sequence L % 16 of the
 // group; the block's maxima over its rows go to hq_blk[s][block].
 typedef int headq_v4 __attribute__((ext_vector_type(4)));
+constexpr int HEADQ_PD = 4;   // weight groups in flight ahead of the one in use
 template <int G>
 __global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
   extern __shared__ uint4 xq[];   // [4 groups][G][2 planes][64 lanes]
@@ -1561,13 +1562,15 @@ __global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
   const int nq = min(4, (a.batch - b0 + 15) / 16);
   const int nch = a.VOCAB / 16;
   const int c = min(blockIdx.x * 8 + w, nch - 1);   // past the end: block nch-1 again, not stored
-  // this wave's weights (2G 16-byte words a lane) first, then the stage
-  uint4 W[G][2];
+  // the first weight groups of this wave's block, then the stage: the
+  // quantised hidden of the workgroup's sequences (groups past the batch are
+  // left unwritten and their products unused) and the records
   const uint4 *pw = a.embq + (long long)c * G * 128 + lane;
+  uint4 Wr[HEADQ_PD][2];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    W[g][0] = ld_nt(pw + 128 * g);
-    W[g][1] = ld_nt(pw + 128 * g + 64);
+  for (int p = 0; p < HEADQ_PD; ++p) {
+    Wr[p][0] = ld_nt(pw + 128 * (p < G ? p : G - 1));
+    Wr[p][1] = ld_nt(pw + 128 * (p < G ? p : G - 1) + 64);
   }
   for (int k = tid; k < nq * G * 128; k += 512) xq[k] = a.hq_x[(long long)(b0 / 16) * G * 128 + k];
   if (tid < 8 * 16) {   // the workgroup's rows' records (the last block again past the end)
@@ -1577,31 +1580,46 @@ __global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
   for (int k = tid; k < HEADQ_SEQ; k += 512)
     if (b0 + k < a.batch) sq[k] = a.hq_seq[b0 + k];
   __syncthreads();
-  const bool store = blockIdx.x * 8 + w < nch;
-  for (int q = 0; q < nq; ++q) {   // uniform
-    headq_v4 hh = {0, 0, 0, 0}, c1 = {0, 0, 0, 0}, c2 = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+  // the four sequence groups' products side by side: 16 independent
+  // accumulators, one group of 64 columns at a time
+  headq_v4 acc[4][4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[q][k] = headq_v4{0, 0, 0, 0};
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint4 wh4 = Wr[g % HEADQ_PD][0], wl4 = Wr[g % HEADQ_PD][1];
+    if (g + HEADQ_PD < G) {
+      Wr[g % HEADQ_PD][0] = ld_nt(pw + 128 * (g + HEADQ_PD));
+      Wr[g % HEADQ_PD][1] = ld_nt(pw + 128 * (g + HEADQ_PD) + 64);
+    }
+    const headq_v4 wh = {(int)wh4.x, (int)wh4.y, (int)wh4.z, (int)wh4.w};
+    const headq_v4 wl = {(int)wl4.x, (int)wl4.y, (int)wl4.z, (int)wl4.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
       const uint4 xh4 = xq[(q * G + g) * 128 + lane], xl4 = xq[(q * G + g) * 128 + 64 + lane];
-      const headq_v4 wh = {(int)W[g][0].x, (int)W[g][0].y, (int)W[g][0].z, (int)W[g][0].w};
-      const headq_v4 wl = {(int)W[g][1].x, (int)W[g][1].y, (int)W[g][1].z, (int)W[g][1].w};
       const headq_v4 xh = {(int)xh4.x, (int)xh4.y, (int)xh4.z, (int)xh4.w};
       const headq_v4 xl = {(int)xl4.x, (int)xl4.y, (int)xl4.z, (int)xl4.w};
-      hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xh, hh, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xl, c1, 0, 0, 0);
-      c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xh, c2, 0, 0, 0);
-      ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xl, ll, 0, 0, 0);
+      acc[q][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xh, acc[q][0], 0, 0, 0);
+      acc[q][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xl, acc[q][1], 0, 0, 0);
+      acc[q][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xh, acc[q][2], 0, 0, 0);
+      acc[q][3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xl, acc[q][3], 0, 0, 0);
     }
+  }
+  const bool store = blockIdx.x * 8 + w < nch;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
     const int s = b0 + 16 * q + i;
-    const HeadQSeq Q = sq[16 * q + i];
-    double mlo = -INFINITY, mhi = -INFINITY;
+    const HeadQSeq Q = sq[(16 * q + i) < HEADQ_SEQ ? 16 * q + i : 0];
     const long long sx = 128LL * Q.sumx - 16384LL * a.D;
+    double mlo = -INFINITY, mhi = -INFINITY;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const HeadQRow &Mv = rq[16 * w + 4 * kg + v];
       // a zero row (r1 = r2 = 0): S = 0, so lo = hi = +0, its exact logit
-      const long long S = ((long long)hh[v] << 16) + ((long long)(c1[v] + c2[v]) << 8) + ll[v] +
-                          128LL * Mv.sumw + sx;
+      const long long S = ((long long)acc[q][0][v] << 16) + ((long long)(acc[q][1][v] + acc[q][2][v]) << 8) +
+                          acc[q][3][v] + 128LL * Mv.sumw + sx;
       const double A = ldexp((double)S, Mv.er + Q.eh);
       double B = fma(Q.h1, Mv.r1, ldexp(Mv.r2, Q.eh));
       B = fma(B, 0x1p-20, B) + 0x1p-50 * fabs(A);
@@ -1617,7 +1635,7 @@ __global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
     mhi = fmax(mhi, __shfl_xor(mhi, 16));
     mlo = fmax(mlo, __shfl_xor(mlo, 32));
     mhi = fmax(mhi, __shfl_xor(mhi, 32));
-    if (store && kg == 0 && s < a.batch) a.hq_blk[(long long)s * nch + c] = make_double2(mlo, mhi);
+    if (q < nq && store && kg == 0 && s < a.batch) a.hq_blk[(long long)s * nch + c] = make_double2(mlo, mhi);
   }
 }
 
@@ -1630,7 +1648,7 @@ __global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
 // the candidate blocks go to an LDS list, two at a time through the
 // workgroup (16 lanes a row).
 constexpr int HEADQ_PICK_T = 512;
-constexpr int HEADQ_PICK_PER = 8;   // blocks a thread (VOCAB / 16 <= 4096 in one batch)
+constexpr int HEADQ_PICK_PER = 8;   // blocks a thread kept in registers (VOCAB / 16 <= 4096)
 template <int MAXD64, bool EXACT>
 __global__ __launch_bounds__(HEADQ_PICK_T) void k_headq_pick(HeadArgs a) {
   extern __shared__ double hs[];   // D, then the candidate list (VOCAB / 16 ints)
@@ -1643,24 +1661,35 @@ __global__ __launch_bounds__(HEADQ_PICK_T) void k_headq_pick(HeadArgs a) {
   if (tid == 0) ncand = 0;
   for (int k = tid; k < a.D; k += HEADQ_PICK_T) hs[k] = a.hn[(long long)b * a.D + k];
   const double2 *blk = a.hq_blk + (long long)b * nch;
-  double t = -INFINITY;
-  for (int c0 = tid; c0 < nch; c0 += HEADQ_PICK_T * HEADQ_PICK_PER) {   // one pass up to 4096 blocks
+  // the first HEADQ_PICK_PER blocks of the thread stay in registers (all of
+  // them up to 4096 blocks); any further ones are read again below
+  double t = -INFINITY, hv[HEADQ_PICK_PER];
+  {
     double2 v[HEADQ_PICK_PER];
 #pragma unroll
     for (int k = 0; k < HEADQ_PICK_PER; ++k) {
-      const int c = c0 + HEADQ_PICK_T * k;
+      const int c = tid + HEADQ_PICK_T * k;
       v[k] = blk[c < nch ? c : nch - 1];
     }
 #pragma unroll
-    for (int k = 0; k < HEADQ_PICK_PER; ++k) t = fmax(t, v[k].x);   // clamped entries repeat one
+    for (int k = 0; k < HEADQ_PICK_PER; ++k) {
+      t = fmax(t, v[k].x);   // clamped entries repeat one
+      hv[k] = v[k].y;
+    }
   }
+  for (int c = tid + HEADQ_PICK_T * HEADQ_PICK_PER; c < nch; c += HEADQ_PICK_T) t = fmax(t, blk[c].x);
   for (int o = 32; o; o >>= 1) t = fmax(t, __shfl_xor(t, o));
   if (l == 0) rv[w] = t;
   __syncthreads();
   double T = rv[0];
 #pragma unroll
   for (int k = 1; k < HEADQ_PICK_T / 64; ++k) T = fmax(T, rv[k]);
-  for (int c = tid; c < nch; c += HEADQ_PICK_T)   // L2-resident now
+#pragma unroll
+  for (int k = 0; k < HEADQ_PICK_PER; ++k) {
+    const int c = tid + HEADQ_PICK_T * k;
+    if (c < nch && hv[k] >= T) cand[atomicAdd(&ncand, 1)] = c;
+  }
+  for (int c = tid + HEADQ_PICK_T * HEADQ_PICK_PER; c < nch; c += HEADQ_PICK_T)
     if (blk[c].y >= T) cand[atomicAdd(&ncand, 1)] = c;
   __syncthreads();
   const int n = ncand;
