@@ -333,7 +333,12 @@ int bfp_rtl_decode(bfp_ctx *ctx, const int32_t *prompt, int n_prompt, int n_gen,
                    int16_t *hist_m, int8_t *hist_e);
 
 /* Decode head (full.py:438-440): final norm, float64 logits over the raw
- * embedding, first-index argmax.  logits may be NULL. */
+ * embedding, first-index argmax.  logits may be NULL: then, from 32
+ * sequences on (contexts made with max_batch >= 32), the argmax comes from
+ * the bounded head, which forms float64 logits only for the rows that can
+ * hold the largest (an exact int16 dot product brackets every logit) and
+ * returns the same index; the environment variable BFP_HEAD_BOUNDED=0
+ * keeps the full head. */
 int bfp_head(bfp_ctx *ctx, int batch, const int16_t *h_m, const int8_t *h_e, double *logits,
              int32_t *argmax);
 
