@@ -1572,13 +1572,30 @@ __global__ __launch_bounds__(512, 4) void k_headq_mx(HeadArgs a) {
     Wr[p][0] = ld_nt(pw + 128 * (p < G ? p : G - 1));
     Wr[p][1] = ld_nt(pw + 128 * (p < G ? p : G - 1) + 64);
   }
-  for (int k = tid; k < nq * G * 128; k += 512) xq[k] = a.hq_x[(long long)(b0 / 16) * G * 128 + k];
-  if (tid < 8 * 16) {   // the workgroup's rows' records (the last block again past the end)
-    const int r = blockIdx.x * 128 + tid;
-    rq[tid] = a.embq_meta[r < a.VOCAB ? r : a.VOCAB - 16 + (r & 15)];
+  {
+    // every staging load of a thread before its stores (one after another,
+    // load then store, the stage took 6 us)
+    constexpr int SPT = (4 * G * 128 + 511) / 512;
+    const int lim = nq * G * 128;
+    const uint4 *src = a.hq_x + (long long)(b0 / 16) * G * 128;
+    uint4 st[SPT];
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const int k = tid + 512 * j;
+      st[j] = src[k < lim ? k : lim - 1];
+    }
+    const int r = blockIdx.x * 128 + (tid & 127);   // the rows' records (the last block again past the end)
+    const HeadQRow rr = a.embq_meta[r < a.VOCAB ? r : a.VOCAB - 16 + (r & 15)];
+    const int bs = b0 + (tid & (HEADQ_SEQ - 1));
+    const HeadQSeq ss = a.hq_seq[bs < a.batch ? bs : a.batch - 1];
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const int k = tid + 512 * j;
+      if (k < lim) xq[k] = st[j];
+    }
+    if (tid < 8 * 16) rq[tid] = rr;
+    if (tid < HEADQ_SEQ) sq[tid] = ss;
   }
-  for (int k = tid; k < HEADQ_SEQ; k += 512)
-    if (b0 + k < a.batch) sq[k] = a.hq_seq[b0 + k];
   __syncthreads();
   // the four sequence groups' products side by side: 16 independent
   // accumulators, one group of 64 columns at a time
@@ -1659,7 +1676,10 @@ __global__ __launch_bounds__(HEADQ_PICK_T) void k_headq_pick(HeadArgs a) {
   const int nch = a.VOCAB / 16, d64 = a.D / 64, l16 = tid & 15;
   int *cand = reinterpret_cast<int *>(hs + a.D);
   if (tid == 0) ncand = 0;
-  for (int k = tid; k < a.D; k += HEADQ_PICK_T) hs[k] = a.hn[(long long)b * a.D + k];
+  // the normed hidden (D <= 2 * HEADQ_PICK_T) with the bounds' loads below,
+  // stored once they are all issued
+  const double *hb = a.hn + (long long)b * a.D;
+  const double h0 = hb[tid < a.D ? tid : 0], h1v = hb[tid + HEADQ_PICK_T < a.D ? tid + HEADQ_PICK_T : 0];
   const double2 *blk = a.hq_blk + (long long)b * nch;
   // the first HEADQ_PICK_PER blocks of the thread stay in registers (all of
   // them up to 4096 blocks); any further ones are read again below
@@ -1677,6 +1697,8 @@ __global__ __launch_bounds__(HEADQ_PICK_T) void k_headq_pick(HeadArgs a) {
       hv[k] = v[k].y;
     }
   }
+  if (tid < a.D) hs[tid] = h0;
+  if (tid + HEADQ_PICK_T < a.D) hs[tid + HEADQ_PICK_T] = h1v;
   for (int c = tid + HEADQ_PICK_T * HEADQ_PICK_PER; c < nch; c += HEADQ_PICK_T) t = fmax(t, blk[c].x);
   for (int o = 32; o; o >>= 1) t = fmax(t, __shfl_xor(t, o));
   if (l == 0) rv[w] = t;
