@@ -243,6 +243,34 @@ def test_decode_errors(gpu):
     gm.close()
 
 
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_non_finite_embedding_refused(gpu, bad):
+    """The bounded head's logit bounds hold for finite embeddings only, so
+    bfp_load_weights(BFP_EMBED) refuses a NaN or an infinity (naming its
+    row and column); a finite embedding loaded afterwards decodes as the
+    oracle does, on the batch-1 and the batched (bounded head) paths."""
+    from bfp import Dims, synth
+    from bfp._lib import BfpError
+    from bfp.model import BfpModel
+    d = Dims(**TINY)
+    fm = synth.make_model(d, seed=21)
+    om = sim.build_model(fm)
+    gm = BfpModel(d, max_batch=32)
+    gm.load_fp32(fm)
+    e = fm.embed.copy()
+    e[300, 77] = bad
+    with pytest.raises(BfpError, match=r"\(300, 77\) is not finite"):
+        gm.load_tensor("embed", fp32=e)
+    gm.load_tensor("embed", fp32=fm.embed)
+    prompts = np.stack([synth.make_prompt(d, 4, seed=60 + b) for b in range(32)])
+    toks, _ = gm.decode(prompts, 5)
+    for b in (0, 17, 31):
+        assert list(toks[b]) == sim.decode(om, prompts[b], 5)[4:], f"sequence {b}"
+    toks1, _ = gm.decode(prompts[:1], 5)
+    assert list(toks1[0]) == list(toks[0])
+    gm.close()
+
+
 def test_decode_long_context(gpu):
     """BASELINE config 4's positions on a 2-layer model: a 48-token prompt,
     then greedy decode through position 2047 (KV cache of 2048 positions,

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 #include "bfp.h"
@@ -746,6 +747,12 @@ int bfp_load_weights(bfp_ctx *c, int which, int layer, const float *fp32, const 
     }
     case BFP_EMBED: {
       if (!fp32) return set_err(BFP_EINVAL, "the embedding must be given as float32");
+      // The head's bounds hold for finite values only: with a NaN or an
+      // infinity no block's bounds would bracket the largest logit, so such
+      // an embedding is refused here.
+      for (size_t i = 0, n = (size_t)d.VOCAB * d.D; i < n; ++i)
+        if (!std::isfinite(fp32[i]))
+          return set_err(BFP_EINVAL, "embedding value (%zu, %zu) is not finite", i / d.D, i % d.D);
       HIP_TRY(hipMemcpy(c->embed, fp32, sizeof(float) * (size_t)d.VOCAB * d.D,
                         hipMemcpyHostToDevice));
       if (c->embedp) {
