@@ -232,7 +232,9 @@ int bfp_get_dims(const bfp_ctx *ctx, bfp_dims *out);
  * full.py:312-318) from float32 -- quantize_W on the device (full.py:110-119)
  * -- or from the reference layout (m, e).  BFP_G1/G2/NORM_W: float32
  * (quantised as fp_quantize_vec, full.py:322-323,413) or (m, e).
- * BFP_EMBED: float32 only (the head uses the raw table, full.py:439).
+ * BFP_EMBED: float32 only (the head uses the raw table, full.py:439); a
+ * NaN or infinity in it is refused with BFP_EINVAL (the batched head's
+ * logit bounds hold for finite values only).
  * layer is ignored for EMBED and NORM_W.  Host buffers are copied. */
 int bfp_load_weights(bfp_ctx *ctx, int which, int layer, const float *fp32, const int16_t *m,
                      const int8_t *e);
