@@ -845,20 +845,29 @@ int bfp_layer_step_kv(bfp_ctx *c, int layer, int pos, int kv_pos, int batch, con
   if (pos < 0) return set_err(BFP_ERANGE, "pos %d is negative", pos);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t s = c->stream;
-  // h in and out through pinned host memory, moved by copy kernels (four
-  // pageable hipMemcpyAsync took most of a call's time); D % 64 == 0, so
-  // both parts are whole 32-bit words
+  // h in and out through pinned host memory (four pageable hipMemcpyAsync
+  // took most of a call's time); D % 64 == 0, so both parts are whole
+  // 32-bit words.  At batch 1 the layer's kernels read h from the mapped
+  // buffer and write the output back into it; larger batches move it to
+  // and from the device activations with copy kernels.
   const size_t bm = (size_t)batch * d.D * 2, be = (size_t)batch * d.D / 16;
   BFP_TRY(c->pinned(2 * (bm + be)));
   memcpy(c->pin, h_m, bm);
   memcpy(c->pin + bm, h_e, be);
+  const bool direct = batch == 1;
   const int nw = (int)((bm + be) / 4), cgrid = std::min((nw + 255) / 256, 64);
-  hipLaunchKernelGGL(copy_words2_kernel, dim3(cgrid), dim3(256), 0, s,
-                     reinterpret_cast<const unsigned *>(c->pin_dev), reinterpret_cast<unsigned *>(c->h_m),
-                     (int)(bm / 4), reinterpret_cast<const unsigned *>(c->pin_dev + bm),
-                     reinterpret_cast<unsigned *>(c->h_e), (int)(be / 4));
-  BFP_TRY(launch_status("layer input"));
+  if (!direct) {
+    hipLaunchKernelGGL(copy_words2_kernel, dim3(cgrid), dim3(256), 0, s,
+                       reinterpret_cast<const unsigned *>(c->pin_dev), reinterpret_cast<unsigned *>(c->h_m),
+                       (int)(bm / 4), reinterpret_cast<const unsigned *>(c->pin_dev + bm),
+                       reinterpret_cast<unsigned *>(c->h_e), (int)(be / 4));
+    BFP_TRY(launch_status("layer input"));
+  }
   LayerArgs a = layer_args(c, layer, batch);
+  if (direct) {
+    a.h_m = reinterpret_cast<int16_t *>(c->pin_dev);
+    a.h_e = reinterpret_cast<int8_t *>(c->pin_dev + bm);
+  }
   a.pos_const = pos;
   a.kv_pos_const = kv_pos;
   std::vector<double> row;
@@ -882,12 +891,14 @@ int bfp_layer_step_kv(bfp_ctx *c, int layer, int pos, int kv_pos, int batch, con
     a.dump = c->dump_dev;
   }
   BFP_TRY(launch_layer(a, s));
-  uint8_t *po = c->pin + bm + be, *po_dev = c->pin_dev + bm + be;
-  hipLaunchKernelGGL(copy_words2_kernel, dim3(cgrid), dim3(256), 0, s,
-                     reinterpret_cast<const unsigned *>(c->h_m), reinterpret_cast<unsigned *>(po_dev),
-                     (int)(bm / 4), reinterpret_cast<const unsigned *>(c->h_e),
-                     reinterpret_cast<unsigned *>(po_dev + bm), (int)(be / 4));
-  BFP_TRY(launch_status("layer output"));
+  uint8_t *po = direct ? c->pin : c->pin + bm + be, *po_dev = c->pin_dev + bm + be;
+  if (!direct) {
+    hipLaunchKernelGGL(copy_words2_kernel, dim3(cgrid), dim3(256), 0, s,
+                       reinterpret_cast<const unsigned *>(c->h_m), reinterpret_cast<unsigned *>(po_dev),
+                       (int)(bm / 4), reinterpret_cast<const unsigned *>(c->h_e),
+                       reinterpret_cast<unsigned *>(po_dev + bm), (int)(be / 4));
+    BFP_TRY(launch_status("layer output"));
+  }
   if (dump) {
     for (int i = 0; i < ST_COUNT; ++i) {
       if (dump->m[i])
