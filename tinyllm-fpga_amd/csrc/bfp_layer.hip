@@ -106,8 +106,8 @@ __global__ __launch_bounds__(64 * NW) void k_gu(LayerArgs a) {
   double *leaf = dsm + 3 * a.D;
   int *xs = reinterpret_cast<int *>(leaf + PW_MAX_LEAVES);
   int *xes = xs + nT * 16;
-  __shared__ int redM[NW * 16];
-  __shared__ long long redA[NW * 16];
+  __shared__ int redM[2 * NW * 16];
+  __shared__ long long redA[2 * NW * 16];
   const int c = blockIdx.x, b = blockIdx.y;
   ChunkRegs<TPT> RG, RU;
   load_chunk<NW, TPT>(RG, a.w_gu_m + (long long)(2 * c) * nT * 32,
@@ -124,8 +124,7 @@ __global__ __launch_bounds__(64 * NW) void k_gu(LayerArgs a) {
   __syncthreads();
   long long Ag, Au;
   int Mg, Mu;
-  chunk_AM<NW, TPT>(RG, xs, xes, nT, redM, redA, Ag, Mg);
-  chunk_AM<NW, TPT>(RU, xs, xes, nT, redM, redA, Au, Mu);
+  chunk_AM2<NW, TPT>(RG, RU, xs, xes, nT, redM, redA, Ag, Mg, Au, Mu);   // G and U in one pass
   if (threadIdx.x < 64) epi_gu(a, b, c, Ag, Mg, Au, Mu, threadIdx.x < 16);
 }
 
