@@ -23,7 +23,14 @@ WHICH = {"Wq": 0, "Wk": 1, "Wv": 2, "Wo": 3, "Wg": 4, "Wu": 5, "Wd": 6, "g1": 7,
 
 
 def _p(a: np.ndarray) -> int:
-    return a.ctypes.data
+    """The address of a's data.  A writable, C-contiguous, non-empty array's
+    buffer is taken through ctypes (about 0.9 us a call, against 2 us for
+    a.ctypes.data, four of which a single-layer call makes); any other
+    array goes through a.ctypes.data."""
+    try:
+        return C.addressof(C.c_char.from_buffer(a))
+    except (TypeError, ValueError, BufferError):
+        return a.ctypes.data
 
 
 def _c16(a):
